@@ -1,0 +1,130 @@
+"""ctypes binding of the C ABI in include/mi355_gemm.h (libmi355gemm.so).
+
+This is the binding a Python host would write against the library; the GPU
+parity tests call the kernels through it, so what they check is the C
+boundary itself.  torch must be imported before the library is loaded so that
+the library binds to the HIP runtime torch already loaded (both carry the
+soname libamdhip64.so.7).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libmi355gemm.so")
+
+MI_OK = 0
+MI_ERR_NULL_POINTER = -1
+MI_ERR_BAD_SIZE = -2
+MI_ERR_BAD_LAYOUT = -3
+MI_ERR_BAD_LD = -4
+MI_ERR_NOT_SQUARE = -5
+MI_ERR_WORKSPACE = -6
+MI_ERR_NO_DEVICE = -7
+
+MI_OP_N, MI_OP_T = 0, 1
+MI_DENSE, MI_LOWER, MI_UPPER = 0, 1, 2
+CFG64, CFG128, CFG256 = 1, 2, 3
+
+_i64 = ctypes.c_int64
+_vp = ctypes.c_void_p
+_sz = ctypes.c_size_t
+
+
+class GemmArgs(ctypes.Structure):
+    """mirror of mi_gemm_args"""
+    _fields_ = [
+        ("A", _vp), ("B", _vp), ("C", _vp),
+        ("M", _i64), ("N", _i64), ("K", _i64), ("batch", _i64),
+        ("lda", _i64), ("ldb", _i64), ("ldc", _i64),
+        ("stride_a", _i64), ("stride_b", _i64), ("stride_c", _i64),
+        ("op_a", ctypes.c_int32), ("op_b", ctypes.c_int32),
+        ("structure", ctypes.c_int32), ("plan_override", ctypes.c_int32),
+        ("workspace", _vp), ("workspace_bytes", _sz),
+    ]
+
+
+class Plan(ctypes.Structure):
+    """mirror of mi_plan"""
+    _fields_ = [
+        ("plan_id", ctypes.c_int32), ("block_m", ctypes.c_int32), ("block_n", ctypes.c_int32),
+        ("block_k", ctypes.c_int32), ("tiles_m", ctypes.c_int32), ("tiles_n", ctypes.c_int32),
+        ("split_k", ctypes.c_int32), ("k_chunk", _i64), ("group_m", ctypes.c_int32),
+        ("grid", _i64), ("workspace_bytes", _sz),
+    ]
+
+
+# name -> (restype, argtypes); every symbol include/mi355_gemm.h declares
+SIGNATURES = {
+    "mi_gemm_f32": (ctypes.c_int, [ctypes.POINTER(GemmArgs), _vp]),
+    "mi_gemm_workspace_bytes": (_sz, [ctypes.POINTER(GemmArgs)]),
+    "mi_gemm_plan": (ctypes.c_int, [ctypes.POINTER(GemmArgs), ctypes.c_int32, ctypes.POINTER(Plan)]),
+    "mi_square_matmul_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _vp]),
+    "mi_matmul_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
+    "mi_batched_matmul_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
+    "mi_gemv_workspace_bytes": (_sz, [_i64, _i64]),
+    "mi_gemv_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _vp, _sz, _vp]),
+    "mi_matmul_large_k_workspace_bytes": (_sz, [_i64, _i64, _i64]),
+    "mi_matmul_large_k_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp, _sz, _vp]),
+    "mi_gemm_small_k_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
+    "mi_tall_skinny_matmul_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _vp]),
+    "mi_tensor3d_matmul_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
+    "mi_tensor4d_matmul_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp]),
+    "mi_diag_mult_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _vp]),
+    "mi_symmetric_matmul_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _vp]),
+    "mi_upper_tri_matmul_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _vp]),
+    "mi_lower_tri_mul_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _vp]),
+    "mi_matmul_transposed_a_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
+    "mi_matmul_transposed_b_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
+    "mi_matmul_transposed_both_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
+    "mi_fill_uniform_f32": (ctypes.c_int, [_vp, _i64, ctypes.c_uint64, _i64, _vp]),
+    "mi_status_string": (ctypes.c_char_p, [ctypes.c_int]),
+    "mi_version": (ctypes.c_char_p, []),
+}
+
+_lib = None
+
+
+def lib():
+    """Load libmi355gemm.so (after torch) and attach the C signatures."""
+    global _lib
+    if _lib is None:
+        import torch  # noqa: F401  -- bind to torch's HIP runtime
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is not built; run cupilot-kernels_amd/build.py")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+class MiError(RuntimeError):
+    def __init__(self, status: int, where: str = ""):
+        self.status = status
+        msg = lib().mi_status_string(status).decode()
+        super().__init__(f"{where}: {msg} (status {status})" if where else msg)
+
+
+def check(status: int, where: str = "") -> None:
+    if status != MI_OK:
+        raise MiError(status, where)
+
+
+def plan(M, N, K, batch=1, op_a=MI_OP_N, op_b=MI_OP_N, structure=MI_DENSE, num_cus=256,
+         workspace_bytes=0, plan_override=0, lda=None, ldb=None, ldc=None):
+    """Host-only scheduler query (mi_gemm_plan); no device needed."""
+    a = GemmArgs()
+    a.M, a.N, a.K, a.batch = M, N, K, batch
+    a.op_a, a.op_b, a.structure = op_a, op_b, structure
+    a.lda = lda if lda is not None else (K if op_a == MI_OP_N else M)
+    a.ldb = ldb if ldb is not None else (N if op_b == MI_OP_N else K)
+    a.ldc = ldc if ldc is not None else N
+    a.workspace_bytes = workspace_bytes
+    a.plan_override = plan_override
+    p = Plan()
+    rc = lib().mi_gemm_plan(ctypes.byref(a), num_cus, ctypes.byref(p))
+    return rc, p

@@ -1,0 +1,278 @@
+// abi.cpp -- extern "C" entry points of libmi355gemm.so (declared in
+// include/mi355_gemm.h).  Validation happens here, before any launch; the
+// scheduler resolves the kernel; launches are asynchronous on the caller's
+// stream.  Nothing here allocates device memory or keeps state between calls
+// other than an immutable per-device CU count.
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstdint>
+
+#include "../../include/mi355_gemm.h"
+#include "mi_internal.hpp"
+
+namespace mi {
+int validate_shape(const mi_gemm_args& a);
+int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* launch);
+}  // namespace mi
+
+using namespace mi;
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_cu_count[kMaxDevices];  // 0 = not queried yet
+
+int device_cus(int* status) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) {
+        *status = MI_ERR_NO_DEVICE;
+        return 0;
+    }
+    if (dev < kMaxDevices) {
+        const int cached = g_cu_count[dev].load(std::memory_order_relaxed);
+        if (cached > 0) return cached;
+    }
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+        *status = MI_ERR_NO_DEVICE;
+        return 0;
+    }
+    if (dev < kMaxDevices) g_cu_count[dev].store(n, std::memory_order_relaxed);
+    return n;
+}
+
+int hip_rc(hipError_t e) { return e == hipSuccess ? MI_OK : (int)e; }
+
+hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+mi_gemm_args dense_args(const float* A, const float* B, float* C, int64_t M, int64_t K, int64_t N,
+                        int op_a, int op_b) {
+    mi_gemm_args a{};
+    a.A = A;
+    a.B = B;
+    a.C = C;
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.batch = 1;
+    a.op_a = op_a;
+    a.op_b = op_b;
+    a.lda = op_a == MI_OP_N ? K : M;
+    a.ldb = op_b == MI_OP_N ? N : K;
+    a.ldc = N;
+    a.structure = MI_DENSE;
+    return a;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* mi_status_string(int status) {
+    switch (status) {
+        case MI_OK: return "ok";
+        case MI_ERR_NULL_POINTER: return "null pointer argument";
+        case MI_ERR_BAD_SIZE: return "invalid size (negative, or beyond the supported range)";
+        case MI_ERR_BAD_LAYOUT: return "invalid op / structure combination";
+        case MI_ERR_BAD_LD: return "leading dimension or batch stride too small";
+        case MI_ERR_NOT_SQUARE: return "structured (triangular) product needs square operands";
+        case MI_ERR_WORKSPACE: return "workspace missing or too small";
+        case MI_ERR_NO_DEVICE: return "no HIP device available";
+        default: break;
+    }
+    if (status > 0) return hipGetErrorString(static_cast<hipError_t>(status));
+    return "unknown status";
+}
+
+const char* mi_version(void) { return "mi355_gemm 0.1.0 gfx950"; }
+
+int mi_gemm_plan(const mi_gemm_args* args, int32_t num_cus, mi_plan* out) {
+    if (!args || !out) return MI_ERR_NULL_POINTER;
+    return plan_gemm(*args, num_cus, *out, nullptr);
+}
+
+size_t mi_gemm_workspace_bytes(const mi_gemm_args* args) {
+    if (!args) return 0;
+    mi_gemm_args a = *args;
+    a.workspace_bytes = SIZE_MAX;  // ask what the preferred plan wants
+    int st = MI_OK;
+    const int cus = device_cus(&st);
+    mi_plan p{};
+    if (plan_gemm(a, st == MI_OK ? cus : 256, p, nullptr) != MI_OK) return 0;
+    return p.workspace_bytes;
+}
+
+int mi_gemm_f32(const mi_gemm_args* args, void* stream) {
+    if (!args) return MI_ERR_NULL_POINTER;
+    const mi_gemm_args& a = *args;
+    int rc = validate_shape(a);
+    if (rc != MI_OK) return rc;
+    const bool empty_out = a.M == 0 || a.N == 0 || a.batch == 0;
+    if (empty_out) return MI_OK;
+    if (!a.C) return MI_ERR_NULL_POINTER;
+    hipStream_t s = as_stream(stream);
+    if (a.K == 0) return hip_rc(launch_fill_zero_2d(a.C, a.M, a.N, a.ldc, a.batch, a.stride_c, s));
+    if (!a.A || !a.B) return MI_ERR_NULL_POINTER;
+
+    int st = MI_OK;
+    const int cus = device_cus(&st);
+    if (st != MI_OK) return st;
+    mi_plan p{};
+    GemmLaunch g{};
+    rc = plan_gemm(a, cus, p, &g);
+    if (rc != MI_OK) return rc;
+    if (g.split_k > 1 && (!a.workspace || a.workspace_bytes < p.workspace_bytes))
+        return MI_ERR_WORKSPACE;
+
+    hipError_t e;
+    if (a.op_a == MI_OP_N && a.op_b == MI_OP_N) e = launch_gemm_nn(g, s);
+    else if (a.op_a == MI_OP_T && a.op_b == MI_OP_N) e = launch_gemm_tn(g, s);
+    else if (a.op_a == MI_OP_N && a.op_b == MI_OP_T) e = launch_gemm_nt(g, s);
+    else e = launch_gemm_tt(g, s);
+    if (e != hipSuccess) return hip_rc(e);
+    if (g.split_k > 1)
+        e = launch_splitk_reduce(g.ws, a.C, g.M, g.N, g.batch, g.split_k, a.ldc, a.stride_c, s);
+    return hip_rc(e);
+}
+
+// ---- named operators ---------------------------------------------------------
+
+int mi_square_matmul_f32(const float* A, const float* B, float* C, int64_t N, void* stream) {
+    mi_gemm_args a = dense_args(A, B, C, N, N, N, MI_OP_N, MI_OP_N);
+    return mi_gemm_f32(&a, stream);
+}
+
+int mi_matmul_f32(const float* A, const float* B, float* C, int64_t M, int64_t K, int64_t N,
+                  void* stream) {
+    mi_gemm_args a = dense_args(A, B, C, M, K, N, MI_OP_N, MI_OP_N);
+    return mi_gemm_f32(&a, stream);
+}
+
+int mi_batched_matmul_f32(const float* A, const float* B, float* C, int64_t batch, int64_t M,
+                          int64_t K, int64_t N, void* stream) {
+    mi_gemm_args a = dense_args(A, B, C, M, K, N, MI_OP_N, MI_OP_N);
+    a.batch = batch;
+    a.stride_a = M * K;
+    a.stride_b = K * N;
+    a.stride_c = M * N;
+    return mi_gemm_f32(&a, stream);
+}
+
+size_t mi_gemv_workspace_bytes(int64_t M, int64_t K) {
+    if (M <= 0 || K <= 0) return 0;
+    return gemv_plan(M, K, true).ws_bytes;
+}
+
+int mi_gemv_f32(const float* A, const float* x, float* y, int64_t M, int64_t K, void* workspace,
+                size_t workspace_bytes, void* stream) {
+    if (M < 0 || K < 0 || M > INT32_MAX || K > INT32_MAX - 1024) return MI_ERR_BAD_SIZE;
+    if (M == 0) return MI_OK;
+    if (!y) return MI_ERR_NULL_POINTER;
+    hipStream_t s = as_stream(stream);
+    if (K == 0) return hip_rc(launch_fill_zero_2d(y, 1, M, M, 1, 0, s));
+    if (!A || !x) return MI_ERR_NULL_POINTER;
+    const bool aligned = K % 4 == 0 && ((uintptr_t)A & 15u) == 0 && ((uintptr_t)x & 15u) == 0;
+    GemvPlan p = gemv_plan(M, K, aligned);
+    if (p.split_k > 1 && (!workspace || workspace_bytes < p.ws_bytes)) {
+        // Not enough scratch for the split: run unsplit (same result order
+        // per row is not required -- each split sum is deterministic either way).
+        p.split_k = 1;
+        p.k_chunk = (int)K;
+        p.ws_bytes = 0;
+    }
+    return hip_rc(launch_gemv(p, A, x, y, static_cast<float*>(workspace), (int)M, (int)K, K, s));
+}
+
+size_t mi_matmul_large_k_workspace_bytes(int64_t M, int64_t K, int64_t N) {
+    mi_gemm_args a = dense_args(nullptr, nullptr, nullptr, M, K, N, MI_OP_N, MI_OP_N);
+    return mi_gemm_workspace_bytes(&a);
+}
+
+int mi_matmul_large_k_f32(const float* A, const float* B, float* C, int64_t M, int64_t K,
+                          int64_t N, void* workspace, size_t workspace_bytes, void* stream) {
+    mi_gemm_args a = dense_args(A, B, C, M, K, N, MI_OP_N, MI_OP_N);
+    a.workspace = workspace;
+    a.workspace_bytes = workspace ? workspace_bytes : 0;
+    return mi_gemm_f32(&a, stream);
+}
+
+int mi_gemm_small_k_f32(const float* A, const float* B, float* C, int64_t M, int64_t K, int64_t N,
+                        void* stream) {
+    mi_gemm_args a = dense_args(A, B, C, M, K, N, MI_OP_N, MI_OP_N);
+    return mi_gemm_f32(&a, stream);
+}
+
+int mi_tall_skinny_matmul_f32(const float* A, const float* B, float* C, int64_t M, int64_t N,
+                              void* stream) {
+    mi_gemm_args a = dense_args(A, B, C, M, N, M, MI_OP_N, MI_OP_N);
+    return mi_gemm_f32(&a, stream);
+}
+
+int mi_tensor3d_matmul_f32(const float* A, const float* B, float* out, int64_t N, int64_t M,
+                           int64_t K, int64_t L, void* stream) {
+    if (N < 0 || M < 0) return MI_ERR_BAD_SIZE;
+    mi_gemm_args a = dense_args(A, B, out, N * M, K, L, MI_OP_N, MI_OP_N);
+    return mi_gemm_f32(&a, stream);
+}
+
+int mi_tensor4d_matmul_f32(const float* A, const float* B, float* out, int64_t b, int64_t i,
+                           int64_t j, int64_t l, int64_t k, void* stream) {
+    if (b < 0 || i < 0 || j < 0) return MI_ERR_BAD_SIZE;
+    mi_gemm_args a = dense_args(A, B, out, b * i * j, l, k, MI_OP_N, MI_OP_N);
+    return mi_gemm_f32(&a, stream);
+}
+
+int mi_diag_mult_f32(const float* a, const float* B, float* out, int64_t N, int64_t M,
+                     void* stream) {
+    if (N < 0 || M < 0) return MI_ERR_BAD_SIZE;
+    if (N == 0 || M == 0) return MI_OK;
+    if (!a || !B || !out) return MI_ERR_NULL_POINTER;
+    return hip_rc(launch_diag(a, B, out, N, M, as_stream(stream)));
+}
+
+int mi_symmetric_matmul_f32(const float* A, const float* B, float* C, int64_t N, void* stream) {
+    // A = A^T and B = B^T, so A . B = A . (B^T) with B read as stored N x K:
+    // both operands are then K-contiguous.
+    mi_gemm_args a = dense_args(A, B, C, N, N, N, MI_OP_N, MI_OP_T);
+    return mi_gemm_f32(&a, stream);
+}
+
+int mi_upper_tri_matmul_f32(const float* A, const float* B, float* C, int64_t N, void* stream) {
+    mi_gemm_args a = dense_args(A, B, C, N, N, N, MI_OP_N, MI_OP_N);
+    a.structure = MI_UPPER;
+    return mi_gemm_f32(&a, stream);
+}
+
+int mi_lower_tri_mul_f32(const float* A, const float* B, float* C, int64_t N, void* stream) {
+    mi_gemm_args a = dense_args(A, B, C, N, N, N, MI_OP_N, MI_OP_N);
+    a.structure = MI_LOWER;
+    return mi_gemm_f32(&a, stream);
+}
+
+int mi_matmul_transposed_a_f32(const float* A, const float* B, float* C, int64_t M, int64_t K,
+                               int64_t N, void* stream) {
+    mi_gemm_args a = dense_args(A, B, C, M, K, N, MI_OP_T, MI_OP_N);
+    return mi_gemm_f32(&a, stream);
+}
+
+int mi_matmul_transposed_b_f32(const float* A, const float* B, float* C, int64_t M, int64_t K,
+                               int64_t N, void* stream) {
+    mi_gemm_args a = dense_args(A, B, C, M, K, N, MI_OP_N, MI_OP_T);
+    return mi_gemm_f32(&a, stream);
+}
+
+int mi_matmul_transposed_both_f32(const float* A, const float* B, float* C, int64_t M, int64_t K,
+                                  int64_t N, void* stream) {
+    mi_gemm_args a = dense_args(A, B, C, M, K, N, MI_OP_T, MI_OP_T);
+    return mi_gemm_f32(&a, stream);
+}
+
+int mi_fill_uniform_f32(float* out, int64_t n, uint64_t seed, int64_t offset, void* stream) {
+    if (n < 0 || offset < 0) return MI_ERR_BAD_SIZE;
+    if (n == 0) return MI_OK;
+    if (!out) return MI_ERR_NULL_POINTER;
+    return hip_rc(launch_fill_uniform(out, n, seed, offset, as_stream(stream)));
+}
+
+}  // extern "C"

@@ -1,0 +1,381 @@
+// gemm_kernel.hpp -- fp32 MFMA contraction engine for gfx950 (CDNA4).
+//
+// One kernel template covers the whole dense family of the reference
+// (kernels/1,2,3,6,7,8,9,10,11,13,16,17,18) and the triangular pair
+// (kernels/14,15): C[b] = op_a(A[b]) . op_b(B[b]) in true fp32 on
+// v_mfma_f32_32x32x2_f32 (the reference quantises to fp16/bf16/tf32 first).
+//
+// Structure of one workgroup:
+//   * a BM x BN output tile; waves arranged WAVES_M x WAVES_N, each owning a
+//     WM x WN sub-tile held as (WM/32) x (WN/32) MFMA accumulators (16 VGPR each);
+//   * K is walked in BK = 16 slices through two LDS buffers (one barrier per
+//     slice: the next slice's global loads are issued before the MFMAs of the
+//     current one and written to the other buffer after them);
+//   * each operand is kept in LDS in the orientation it has in HBM, so every
+//     global load is a coalesced 16-byte load and every LDS store a
+//     ds_write_b128 with no transpose:
+//       K-contiguous operand (A row-major, B stored N x K): [mn][BK + 4],
+//         fragments read with one ds_read_b128 per 4 MFMA steps;
+//       MN-contiguous operand (A stored K x M, B row-major): [BK][MN + 4],
+//         fragments read with ds_read_b32 (32 consecutive floats per half wave).
+//     Within a k-block of 8, lane half h = lane / 32 and MFMA step s use
+//     k = 8*kb + 4*h + s for both operands, which is what lets the
+//     K-contiguous side use 16-byte reads.
+//   * epilogue writes straight from the accumulators (row = 8*(r/4) + 4*h +
+//     r%4, col = lane % 32 for accumulator register r), masked at the matrix
+//     edge and, for the triangular modes, on the diagonal.
+// Split-K (used for K >> M, N) writes fp32 partial tiles to a workspace that
+// a second kernel sums in fixed split order, so results are deterministic.
+#pragma once
+
+#include "mi_device.hpp"
+#include "mi_internal.hpp"
+
+namespace mi {
+
+template <int BM_, int BN_, int WM_, int WN_>
+struct Tile {
+    static constexpr int BM = BM_, BN = BN_, BK = 16, WM = WM_, WN = WN_;
+    static constexpr int WAVES_M = BM / WM, WAVES_N = BN / WN;
+    static constexpr int NW = WAVES_M * WAVES_N, NT = NW * 64;
+    static constexpr int TM = WM / 32, TN = WN / 32;
+};
+
+using Tile64 = Tile<64, 64, 32, 32>;
+using Tile128 = Tile<128, 128, 64, 64>;
+using Tile256 = Tile<256, 256, 128, 64>;
+
+enum { kDense = 0, kLower = 1, kUpper = 2 };
+
+// One operand tile of ROWS (m or n) x BK (k) floats, staged through registers.
+template <int ROWS, int BK, int NT, bool KCONTIG, int VEC>
+struct TileLoader {
+    static constexpr int PAD = 4;
+    static constexpr int LD = KCONTIG ? (BK + PAD) : (ROWS + PAD);
+    static constexpr int ELEMS = KCONTIG ? ROWS * LD : BK * LD;
+    static constexpr int SLOTS = ROWS * BK / 4;  // 16-byte slots per tile
+    static_assert(SLOTS % NT == 0, "tile must split evenly over the workgroup");
+    static constexpr int NS = SLOTS / NT;
+
+    f4 v[NS];
+
+    // First element (mn, k) of slot idx; its 4 elements run along k when the
+    // operand is K-contiguous, along mn otherwise.
+    __device__ __forceinline__ static void slot_pos(int idx, int& mn, int& k) {
+        if (KCONTIG) {
+            mn = idx / (BK / 4);
+            k = (idx % (BK / 4)) * 4;
+        } else {
+            k = idx / (ROWS / 4);
+            mn = (idx % (ROWS / 4)) * 4;
+        }
+    }
+
+    // Load the tile at (mn0, k0).  Elements with mn >= mn_ext or k >= k_end
+    // read as zero.  VEC == 4 requires the contiguous extent and ld to be
+    // multiples of 4 and a 16-byte aligned base (checked by the host).
+    __device__ __forceinline__ void load(const float* __restrict__ base, int64_t ld, int mn0,
+                                         int mn_ext, int k0, int k_end, int tid) {
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            int mn, k;
+            slot_pos(tid + s * NT, mn, k);
+            const int gmn = mn0 + mn, gk = k0 + k;
+            if (VEC == 4) {
+                const bool ok = gmn < mn_ext && gk < k_end;
+                const int64_t off = KCONTIG ? (int64_t)gmn * ld + gk : (int64_t)gk * ld + gmn;
+                if (ok) {
+                    v[s] = *reinterpret_cast<const f4*>(base + off);
+                } else {
+                    v[s] = f4{0.f, 0.f, 0.f, 0.f};
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int emn = KCONTIG ? gmn : gmn + e;
+                    const int ek = KCONTIG ? gk + e : gk;
+                    const bool ok = emn < mn_ext && ek < k_end;
+                    const int64_t off = KCONTIG ? (int64_t)emn * ld + ek : (int64_t)ek * ld + emn;
+                    v[s][e] = ok ? base[off] : 0.f;
+                }
+            }
+        }
+    }
+
+    // Triangular input masks: IS_A selects the row operand (mn = i) else the
+    // column operand (mn = j).  LOWER keeps A[i][k] for k <= i and B[k][j] for
+    // k >= j; UPPER the mirror image.
+    template <int MODE, bool IS_A>
+    __device__ __forceinline__ void mask(int mn0, int k0, int tid) {
+        if (MODE == kDense) return;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            int mn, k;
+            slot_pos(tid + s * NT, mn, k);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int emn = mn0 + (KCONTIG ? mn : mn + e);
+                const int ek = k0 + (KCONTIG ? k + e : k);
+                bool keep;
+                if (MODE == kLower) keep = IS_A ? (ek <= emn) : (ek >= emn);
+                else keep = IS_A ? (ek >= emn) : (ek <= emn);
+                if (!keep) v[s][e] = 0.f;
+            }
+        }
+    }
+
+    __device__ __forceinline__ void store(float* lds, int tid) const {
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            int mn, k;
+            slot_pos(tid + s * NT, mn, k);
+            float* dst = KCONTIG ? lds + mn * LD + k : lds + k * LD + mn;
+            *reinterpret_cast<f4*>(dst) = v[s];
+        }
+    }
+
+    // Operand values for the 4 MFMA steps of k-block kb, 32-row group at r0.
+    __device__ __forceinline__ static void frag(const float* lds, int r0, int kb, int lane,
+                                                float out[4]) {
+        const int half = lane >> 5;
+        if (KCONTIG) {
+            const f4 t = *reinterpret_cast<const f4*>(lds + (r0 + (lane & 31)) * LD + kb * 8 + half * 4);
+            out[0] = t[0];
+            out[1] = t[1];
+            out[2] = t[2];
+            out[3] = t[3];
+        } else {
+            const float* p = lds + (kb * 8 + half * 4) * LD + r0 + (lane & 31);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) out[s] = p[s * LD];
+        }
+    }
+};
+
+// Which output tile this workgroup owns and which K range it reduces.
+// Returns false for a triangular off-structure tile (written with zeros).
+template <class T, int MODE>
+__device__ __forceinline__ bool tile_of(const GemmParams& p, int& tm, int& tn, int& k_begin,
+                                        int& k_end) {
+    const int pid = xcd_remap(blockIdx.x, gridDim.x);
+    if (MODE == kDense) {
+        raster(pid, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
+        k_begin = blockIdx.y * p.k_chunk;
+        k_end = min(p.K, k_begin + p.k_chunk);
+        return true;
+    }
+    const int nt = p.tiles_m;  // square tiling
+    const int ncomp = nt * (nt + 1) / 2;
+    if (pid < ncomp) {
+        // Longest K ranges first: diagonal distance d = nt-1 down to 0; the
+        // distance-d band holds nt-d tiles, each reducing (d+1) tiles of K.
+        int rem = pid, d = nt - 1;
+        while (rem >= nt - d) {
+            rem -= nt - d;
+            --d;
+        }
+        if (MODE == kLower) {
+            tm = rem + d;
+            tn = rem;
+            k_begin = tn * T::BN;
+            k_end = min(p.K, (tm + 1) * T::BM);
+        } else {
+            tm = rem;
+            tn = rem + d;
+            k_begin = tm * T::BM;
+            k_end = min(p.K, (tn + 1) * T::BN);
+        }
+        return true;
+    }
+    // Off-structure tiles, row by row: for LOWER the strictly upper tiles.
+    int z = pid - ncomp, r = 0;
+    while (z >= nt - 1 - r) {
+        z -= nt - 1 - r;
+        ++r;
+    }
+    if (MODE == kLower) {
+        tm = r;
+        tn = r + 1 + z;
+    } else {
+        tm = r + 1 + z;
+        tn = r;
+    }
+    k_begin = k_end = 0;
+    return false;
+}
+
+template <class T, bool AT, bool BT, int VEC, int MODE>
+__global__ void __launch_bounds__(T::NT) gemm_f32_kernel(const GemmParams p) {
+    constexpr bool A_KC = !AT;  // A row-major (M x K) is contiguous along K
+    constexpr bool B_KC = BT;   // B stored N x K is contiguous along K
+    using LA = TileLoader<T::BM, T::BK, T::NT, A_KC, VEC>;
+    using LB = TileLoader<T::BN, T::BK, T::NT, B_KC, VEC>;
+    __shared__ __attribute__((aligned(16))) float sA[2][LA::ELEMS];
+    __shared__ __attribute__((aligned(16))) float sB[2][LB::ELEMS];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave / T::WAVES_N;
+    const int wn = wave % T::WAVES_N;
+
+    int tm, tn, k_begin, k_end;
+    const bool compute = tile_of<T, MODE>(p, tm, tn, k_begin, k_end);
+    const int m0 = tm * T::BM, n0 = tn * T::BN;
+    const int batch = blockIdx.z;
+
+    if (!compute) {
+        float* C = p.C + (int64_t)batch * p.sc;
+        for (int e = tid; e < T::BM * T::BN; e += T::NT) {
+            const int row = m0 + e / T::BN, col = n0 + e % T::BN;
+            if (row < p.M && col < p.N) C[(int64_t)row * p.ldc + col] = 0.f;
+        }
+        return;
+    }
+
+    const float* __restrict__ A = p.A + (int64_t)batch * p.sa;
+    const float* __restrict__ B = p.B + (int64_t)batch * p.sb;
+
+    f16v acc[T::TM][T::TN];
+#pragma unroll
+    for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < T::TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    const int nk = k_end > k_begin ? (k_end - k_begin + T::BK - 1) / T::BK : 0;
+    if (nk > 0) {
+        LA la;
+        LB lb;
+        la.load(A, p.lda, m0, p.M, k_begin, k_end, tid);
+        lb.load(B, p.ldb, n0, p.N, k_begin, k_end, tid);
+        la.template mask<MODE, true>(m0, k_begin, tid);
+        lb.template mask<MODE, false>(n0, k_begin, tid);
+        la.store(sA[0], tid);
+        lb.store(sB[0], tid);
+        __syncthreads();
+
+        for (int it = 0; it < nk; ++it) {
+            const int cur = it & 1;
+            const bool more = it + 1 < nk;
+            if (more) {
+                const int k0 = k_begin + (it + 1) * T::BK;
+                la.load(A, p.lda, m0, p.M, k0, k_end, tid);
+                lb.load(B, p.ldb, n0, p.N, k0, k_end, tid);
+                la.template mask<MODE, true>(m0, k0, tid);
+                lb.template mask<MODE, false>(n0, k0, tid);
+            }
+            const float* As = sA[cur];
+            const float* Bs = sB[cur];
+#pragma unroll
+            for (int kb = 0; kb < T::BK / 8; ++kb) {
+                float a[T::TM][4], b[T::TN][4];
+#pragma unroll
+                for (int i = 0; i < T::TM; ++i) LA::frag(As, wm * T::WM + i * 32, kb, lane, a[i]);
+#pragma unroll
+                for (int j = 0; j < T::TN; ++j) LB::frag(Bs, wn * T::WN + j * 32, kb, lane, b[j]);
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+#pragma unroll
+                    for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+                        for (int j = 0; j < T::TN; ++j)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s], b[j][s],
+                                                                             acc[i][j], 0, 0, 0);
+            }
+            if (more) {
+                la.store(sA[cur ^ 1], tid);
+                lb.store(sB[cur ^ 1], tid);
+            }
+            __syncthreads();
+        }
+    }
+
+    float* C;
+    int64_t ldc;
+    if (p.split_k > 1) {
+        C = p.ws + (int64_t)blockIdx.y * p.ws_split_stride + (int64_t)batch * p.ws_batch_stride;
+        ldc = p.N;
+    } else {
+        C = p.C + (int64_t)batch * p.sc;
+        ldc = p.ldc;
+    }
+    const int half = lane >> 5;
+#pragma unroll
+    for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < T::TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = m0 + wm * T::WM + i * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
+                const int col = n0 + wn * T::WN + j * 32 + (lane & 31);
+                if (row < p.M && col < p.N) {
+                    float v = acc[i][j][r];
+                    if (MODE == kLower && col > row) v = 0.f;
+                    if (MODE == kUpper && col < row) v = 0.f;
+                    C[(int64_t)row * ldc + col] = v;
+                }
+            }
+}
+
+inline GemmParams make_params(const GemmLaunch& g) {
+    GemmParams p;
+    p.A = g.A;
+    p.B = g.B;
+    p.C = g.C;
+    p.ws = g.ws;
+    p.M = g.M;
+    p.N = g.N;
+    p.K = g.K;
+    p.tiles_m = g.tiles_m;
+    p.tiles_n = g.tiles_n;
+    p.group_m = g.group_m;
+    p.k_chunk = g.k_chunk;
+    p.split_k = g.split_k;
+    p.lda = g.lda;
+    p.ldb = g.ldb;
+    p.ldc = g.ldc;
+    p.sa = g.sa;
+    p.sb = g.sb;
+    p.sc = g.sc;
+    p.ws_batch_stride = (int64_t)g.M * g.N;
+    p.ws_split_stride = p.ws_batch_stride * g.batch;
+    return p;
+}
+
+template <class T, bool AT, bool BT, int VEC, int MODE>
+hipError_t launch_one(const GemmLaunch& g, hipStream_t s) {
+    const GemmParams p = make_params(g);
+    dim3 grid((unsigned)g.grid_x, (unsigned)g.split_k, (unsigned)g.batch);
+    hipLaunchKernelGGL((gemm_f32_kernel<T, AT, BT, VEC, MODE>), grid, dim3(T::NT), 0, s, p);
+    return hipGetLastError();
+}
+
+template <class T, bool AT, bool BT>
+hipError_t launch_cfg(const GemmLaunch& g, hipStream_t s) {
+    if (g.structure == kDense) {
+        return g.vec == 4 ? launch_one<T, AT, BT, 4, kDense>(g, s)
+                          : launch_one<T, AT, BT, 1, kDense>(g, s);
+    }
+    if constexpr (!AT && !BT) {
+        if (g.structure == kLower)
+            return g.vec == 4 ? launch_one<T, AT, BT, 4, kLower>(g, s)
+                              : launch_one<T, AT, BT, 1, kLower>(g, s);
+        return g.vec == 4 ? launch_one<T, AT, BT, 4, kUpper>(g, s)
+                          : launch_one<T, AT, BT, 1, kUpper>(g, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+template <bool AT, bool BT>
+hipError_t launch_layout(const GemmLaunch& g, hipStream_t s) {
+    switch (g.cfg) {
+        case kCfg64: return launch_cfg<Tile64, AT, BT>(g, s);
+        case kCfg128: return launch_cfg<Tile128, AT, BT>(g, s);
+        case kCfg256: return launch_cfg<Tile256, AT, BT>(g, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace mi

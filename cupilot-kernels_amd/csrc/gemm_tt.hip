@@ -1,0 +1,7 @@
+// gemm_tt.hip -- instantiations of the fp32 MFMA engine for op_a = t, op_b = t
+// (one translation unit per operand layout so they compile in parallel).
+#include "gemm_kernel.hpp"
+
+namespace mi {
+hipError_t launch_gemm_tt(const GemmLaunch& g, hipStream_t s) { return launch_layout<true, true>(g, s); }
+}  // namespace mi

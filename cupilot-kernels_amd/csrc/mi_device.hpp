@@ -1,0 +1,50 @@
+// mi_device.hpp -- device-side helpers shared by the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mi {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+
+// MI355X dispatches consecutive workgroups round-robin over its 8 XCDs, each
+// with a private L2.  xcd_remap() turns the hardware order into an order in
+// which every XCD receives one contiguous range of logical tile ids, so tiles
+// that share A rows / B columns run on the same L2.  A bijection on [0, n).
+constexpr int kNumXcd = 8;
+
+__device__ __forceinline__ int xcd_remap(int bid, int n) {
+    const int xcd = bid % kNumXcd;
+    const int local = bid / kNumXcd;
+    const int q = n / kNumXcd;
+    const int r = n % kNumXcd;
+    return xcd < r ? xcd * (q + 1) + local : r * (q + 1) + (xcd - r) * q + local;
+}
+
+// Grouped raster: walk group_m tile-rows column by column so a wave of
+// concurrently running tiles covers a compact block of C.
+__device__ __forceinline__ void raster(int pid, int tiles_m, int tiles_n, int group_m,
+                                       int& tm, int& tn) {
+    const int in_group = group_m * tiles_n;
+    const int g = pid / in_group;
+    const int first_m = g * group_m;
+    const int rows = min(tiles_m - first_m, group_m);
+    const int r = pid - g * in_group;
+    tm = first_m + r % rows;
+    tn = r / rows;
+}
+
+__device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
+    uint64_t z = x + 0x9E3779B97F4A7C15ULL;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+    return z ^ (z >> 31);
+}
+
+__device__ __forceinline__ float uniform_from_bits(uint64_t z) {
+    return (float)(uint32_t)(z >> 40) * 0x1p-23f - 1.0f;
+}
+
+}  // namespace mi

@@ -1,0 +1,90 @@
+// mi_internal.hpp -- interface between the ABI/scheduler (host C++) and the
+// kernel translation units.  Not installed; the public boundary is
+// include/mi355_gemm.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace mi {
+
+// Tile configurations of the fp32 MFMA contraction engine (v_mfma_f32_32x32x2_f32).
+//   id  block (BM x BN)  waves  wave tile   LDS (double-buffered)
+//   1   64 x 64          4      32 x 32     ~20 KiB
+//   2   128 x 128        4      64 x 64     ~40 KiB
+//   3   256 x 256        8      128 x 64    ~80 KiB
+enum TileCfgId { kCfg64 = 1, kCfg128 = 2, kCfg256 = 3, kNumCfg = 4 };
+
+struct CfgInfo {
+    int bm, bn, bk, threads;
+};
+inline CfgInfo cfg_info(int id) {
+    switch (id) {
+        case kCfg64: return {64, 64, 16, 256};
+        case kCfg128: return {128, 128, 16, 256};
+        case kCfg256: return {256, 256, 16, 512};
+        default: return {0, 0, 0, 0};
+    }
+}
+
+// Fully resolved contraction launch (all validation done by the caller).
+struct GemmLaunch {
+    const float* A;
+    const float* B;
+    float* C;
+    float* ws;            // split-K partials: split_k x batch x M x N (ld = N)
+    int M, N, K, batch;
+    int64_t lda, ldb, ldc;
+    int64_t sa, sb, sc;
+    int op_a, op_b;       // 0 = N, 1 = T
+    int structure;        // 0 dense, 1 lower, 2 upper
+    int cfg;              // TileCfgId
+    int vec;              // 4: 16-byte operand loads; 1: element loads
+    int split_k;
+    int k_chunk;
+    int tiles_m, tiles_n;
+    int group_m;
+    int grid_x;           // workgroups per (split, batch)
+};
+
+// Kernel-side parameter block (passed by value).
+struct GemmParams {
+    const float* A;
+    const float* B;
+    float* C;
+    float* ws;
+    int M, N, K;
+    int tiles_m, tiles_n, group_m;
+    int k_chunk, split_k;
+    int64_t lda, ldb, ldc;
+    int64_t sa, sb, sc;
+    int64_t ws_split_stride;  // elements between consecutive split slices
+    int64_t ws_batch_stride;
+};
+
+hipError_t launch_gemm_nn(const GemmLaunch& g, hipStream_t s);
+hipError_t launch_gemm_tn(const GemmLaunch& g, hipStream_t s);
+hipError_t launch_gemm_nt(const GemmLaunch& g, hipStream_t s);
+hipError_t launch_gemm_tt(const GemmLaunch& g, hipStream_t s);
+
+hipError_t launch_splitk_reduce(const float* ws, float* C, int M, int N, int batch, int split_k,
+                                int64_t ldc, int64_t sc, hipStream_t s);
+hipError_t launch_fill_zero_2d(float* C, int64_t rows, int64_t cols, int64_t ld, int64_t batch,
+                               int64_t batch_stride, hipStream_t s);
+hipError_t launch_fill_uniform(float* out, int64_t n, uint64_t seed, int64_t offset, hipStream_t s);
+hipError_t launch_diag(const float* a, const float* B, float* out, int64_t N, int64_t M,
+                       hipStream_t s);
+
+struct GemvPlan {
+    int split_k;
+    int k_chunk;
+    int rows_per_wg;
+    int vec;
+    size_t ws_bytes;
+};
+GemvPlan gemv_plan(int64_t M, int64_t K, bool aligned);
+hipError_t launch_gemv(const GemvPlan& p, const float* A, const float* x, float* y, float* ws,
+                       int M, int K, int64_t lda, hipStream_t s);
+
+}  // namespace mi

@@ -1,0 +1,257 @@
+// stream_kernels.hip -- HBM-bound kernels of the GEMM family on gfx950, plus
+// the split-K reduction and the fills.
+//
+//   gemv_kernel    y = A.x (kernels/4_Matrix_vector_multiplication_best_kernel.cu:6-80
+//                  is the reference's version).  Every wave owns ROWS rows and
+//                  walks K with 16-byte non-temporal loads of A (A is read
+//                  exactly once, so it should not evict x from L2); each x
+//                  float4 it loads is used for all ROWS rows, cutting the x
+//                  traffic to 1/ROWS of A's.  The per-lane partial sums are
+//                  reduced across the wave with xor shuffles at the end.
+//                  Optional split over K writes per-split partial sums that a
+//                  second pass adds in fixed order.
+//   diag_kernel    out[i,j] = a[i] * B[i,j]
+//                  (kernels/12_Matmul_with_diagonal_matrices_best_kernel.cu:9-38):
+//                  a pure 16-byte streaming copy-scale, one row per iteration.
+//   splitk_reduce  C = sum over splits of the partial tiles, in split order.
+//   fill kernels   zero fill and the counter-based uniform generator.
+#include "mi_device.hpp"
+#include "mi_internal.hpp"
+
+namespace mi {
+
+// ---------------------------------------------------------------------------
+// GEMV
+// ---------------------------------------------------------------------------
+constexpr int kGemvThreads = 256;
+constexpr int kGemvWaves = kGemvThreads / 64;
+
+template <int ROWS, int UNROLL, bool VEC>
+__global__ void __launch_bounds__(kGemvThreads)
+    gemv_kernel(const float* __restrict__ A, const float* __restrict__ x, float* __restrict__ y,
+                float* __restrict__ ws, int M, int K, int64_t lda, int k_chunk, int split_k) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int row0 = (blockIdx.x * kGemvWaves + wave) * ROWS;
+    if (row0 >= M) return;
+    const int split = blockIdx.y;
+    const int kb = split * k_chunk;
+    const int ke = min(K, kb + k_chunk);
+    const int nrows = min(ROWS, M - row0);
+
+    const float* arow[ROWS];
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) arow[r] = A + (int64_t)(row0 + min(r, nrows - 1)) * lda;
+
+    float acc[ROWS];
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) acc[r] = 0.f;
+
+    if (VEC) {
+        constexpr int STEP = 64 * 4 * UNROLL;  // floats per wave iteration
+        // Full iterations cover [kb, full_end): every load is in range, so all
+        // UNROLL*ROWS loads of an iteration can be in flight together.
+        const int full_end = ke > kb ? kb + ((ke - kb) / STEP) * STEP : kb;
+        int k = kb + lane * 4;
+        for (; k < full_end; k += STEP) {
+            f4 xv[UNROLL];
+            f4 av[UNROLL][ROWS];
+#pragma unroll
+            for (int u = 0; u < UNROLL; ++u) {
+                xv[u] = *reinterpret_cast<const f4*>(x + k + u * 256);
+#pragma unroll
+                for (int r = 0; r < ROWS; ++r)
+                    av[u][r] = __builtin_nontemporal_load(reinterpret_cast<const f4*>(arow[r] + k + u * 256));
+            }
+#pragma unroll
+            for (int u = 0; u < UNROLL; ++u)
+#pragma unroll
+                for (int r = 0; r < ROWS; ++r) {
+                    acc[r] = fmaf(av[u][r][0], xv[u][0], acc[r]);
+                    acc[r] = fmaf(av[u][r][1], xv[u][1], acc[r]);
+                    acc[r] = fmaf(av[u][r][2], xv[u][2], acc[r]);
+                    acc[r] = fmaf(av[u][r][3], xv[u][3], acc[r]);
+                }
+        }
+        // Remainder, 256 floats per step (K is a multiple of 4 here).
+        for (; k < ke; k += 256) {
+            const f4 xv = *reinterpret_cast<const f4*>(x + k);
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) {
+                const f4 av = __builtin_nontemporal_load(reinterpret_cast<const f4*>(arow[r] + k));
+                acc[r] = fmaf(av[0], xv[0], acc[r]);
+                acc[r] = fmaf(av[1], xv[1], acc[r]);
+                acc[r] = fmaf(av[2], xv[2], acc[r]);
+                acc[r] = fmaf(av[3], xv[3], acc[r]);
+            }
+        }
+    } else {
+        for (int k = kb + lane; k < ke; k += 64) {
+            const float xv = x[k];
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) acc[r] = fmaf(arow[r][k], xv, acc[r]);
+        }
+    }
+
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+        float v = acc[r];
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+        acc[r] = v;
+    }
+    if (lane == 0) {
+        float* out = split_k > 1 ? ws + (int64_t)split * M : y;
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r)
+            if (r < nrows) out[row0 + r] = acc[r];
+    }
+}
+
+__global__ void gemv_reduce_kernel(const float* __restrict__ ws, float* __restrict__ y, int M,
+                                   int split_k) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= M) return;
+    float s = 0.f;
+    for (int t = 0; t < split_k; ++t) s += ws[(int64_t)t * M + i];
+    y[i] = s;
+}
+
+constexpr int kGemvRows = 8;
+constexpr int kGemvUnroll = 2;
+
+GemvPlan gemv_plan(int64_t M, int64_t K, bool aligned) {
+    GemvPlan p;
+    p.rows_per_wg = kGemvWaves * kGemvRows;
+    p.vec = aligned ? 4 : 1;
+    const int64_t wgs = (M + p.rows_per_wg - 1) / p.rows_per_wg;
+    // Aim for >= 2048 workgroups (8 per CU on 256 CUs) so every CU keeps many
+    // loads in flight; split K only when the rows alone do not get there and
+    // each split still streams >= 16 KiB per row.
+    int split = 1;
+    while (wgs * split < 2048 && K / (split * 2) >= 4096) split *= 2;
+    p.split_k = split;
+    int64_t chunk = (K + split - 1) / split;
+    chunk = (chunk + 255) / 256 * 256;
+    p.k_chunk = (int)chunk;
+    p.ws_bytes = split > 1 ? (size_t)split * (size_t)M * sizeof(float) : 0;
+    return p;
+}
+
+hipError_t launch_gemv(const GemvPlan& p, const float* A, const float* x, float* y, float* ws,
+                       int M, int K, int64_t lda, hipStream_t s) {
+    const int wgs = (M + p.rows_per_wg - 1) / p.rows_per_wg;
+    dim3 grid(wgs, p.split_k);
+    if (p.vec == 4)
+        hipLaunchKernelGGL((gemv_kernel<kGemvRows, kGemvUnroll, true>), grid, dim3(kGemvThreads), 0, s,
+                           A, x, y, ws, M, K, lda, p.k_chunk, p.split_k);
+    else
+        hipLaunchKernelGGL((gemv_kernel<kGemvRows, kGemvUnroll, false>), grid, dim3(kGemvThreads), 0,
+                           s, A, x, y, ws, M, K, lda, p.k_chunk, p.split_k);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || p.split_k == 1) return e;
+    hipLaunchKernelGGL(gemv_reduce_kernel, dim3((M + 255) / 256), dim3(256), 0, s, ws, y, M, p.split_k);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// diag(a) . B
+// ---------------------------------------------------------------------------
+constexpr int kDiagThreads = 256;
+
+template <bool VEC>
+__global__ void __launch_bounds__(kDiagThreads)
+    diag_kernel(const float* __restrict__ a, const float* __restrict__ B, float* __restrict__ out,
+                int64_t N, int64_t M) {
+    for (int64_t i = blockIdx.x; i < N; i += gridDim.x) {
+        const float s = a[i];
+        const float* src = B + i * M;
+        float* dst = out + i * M;
+        if (VEC) {
+            const int64_t m4 = M / 4;
+            for (int64_t c = threadIdx.x; c < m4; c += kDiagThreads) {
+                const f4 v = __builtin_nontemporal_load(reinterpret_cast<const f4*>(src) + c);
+                __builtin_nontemporal_store(v * s, reinterpret_cast<f4*>(dst) + c);
+            }
+        } else {
+            for (int64_t c = threadIdx.x; c < M; c += kDiagThreads)
+                __builtin_nontemporal_store(__builtin_nontemporal_load(src + c) * s, dst + c);
+        }
+    }
+}
+
+hipError_t launch_diag(const float* a, const float* B, float* out, int64_t N, int64_t M,
+                       hipStream_t s) {
+    const bool vec = (M % 4 == 0) && ((uintptr_t)B % 16 == 0) && ((uintptr_t)out % 16 == 0);
+    const int64_t grid = N < 65536 ? N : 65536;
+    if (vec)
+        hipLaunchKernelGGL((diag_kernel<true>), dim3((unsigned)grid), dim3(kDiagThreads), 0, s, a, B, out, N, M);
+    else
+        hipLaunchKernelGGL((diag_kernel<false>), dim3((unsigned)grid), dim3(kDiagThreads), 0, s, a, B, out, N, M);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// split-K reduction and fills
+// ---------------------------------------------------------------------------
+__global__ void splitk_reduce_kernel(const float* __restrict__ ws, float* __restrict__ C, int M,
+                                     int N, int split_k, int64_t ldc, int64_t sc,
+                                     int64_t split_stride) {
+    const int64_t per_batch = (int64_t)M * N;
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int b = blockIdx.y;
+    if (e >= per_batch) return;
+    const float* src = ws + (int64_t)b * per_batch + e;
+    float s = 0.f;
+    for (int t = 0; t < split_k; ++t) s += src[(int64_t)t * split_stride];
+    const int64_t row = e / N, col = e % N;
+    C[(int64_t)b * sc + row * ldc + col] = s;
+}
+
+hipError_t launch_splitk_reduce(const float* ws, float* C, int M, int N, int batch, int split_k,
+                                int64_t ldc, int64_t sc, hipStream_t s) {
+    const int64_t per_batch = (int64_t)M * N;
+    dim3 grid((unsigned)((per_batch + 255) / 256), (unsigned)batch);
+    hipLaunchKernelGGL(splitk_reduce_kernel, grid, dim3(256), 0, s, ws, C, M, N, split_k, ldc, sc,
+                       per_batch * batch);
+    return hipGetLastError();
+}
+
+__global__ void fill_zero_kernel(float* __restrict__ C, int64_t rows, int64_t cols, int64_t ld,
+                                 int64_t batch_stride) {
+    const int64_t per = rows * cols;
+    const int64_t b = blockIdx.y;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < per;
+         e += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = e / cols, c = e % cols;
+        C[b * batch_stride + r * ld + c] = 0.f;
+    }
+}
+
+hipError_t launch_fill_zero_2d(float* C, int64_t rows, int64_t cols, int64_t ld, int64_t batch,
+                               int64_t batch_stride, hipStream_t s) {
+    const int64_t per = rows * cols;
+    if (per == 0 || batch == 0) return hipSuccess;
+    int64_t blocks = (per + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)blocks, (unsigned)batch), dim3(256), 0, s, C,
+                       rows, cols, ld, batch_stride);
+    return hipGetLastError();
+}
+
+__global__ void fill_uniform_kernel(float* __restrict__ out, int64_t n, uint64_t base) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        out[i] = uniform_from_bits(splitmix64(base + (uint64_t)i));
+}
+
+hipError_t launch_fill_uniform(float* out, int64_t n, uint64_t seed, int64_t offset, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    int64_t blocks = (n + 255) / 256;
+    if (blocks > 262144) blocks = 262144;
+    hipLaunchKernelGGL(fill_uniform_kernel, dim3((unsigned)blocks), dim3(256), 0, s, out, n,
+                       (seed << 40) + (uint64_t)offset);
+    return hipGetLastError();
+}
+
+}  // namespace mi

@@ -1,0 +1,206 @@
+/*
+ * mi355_gemm.h -- C ABI of the MI355X (gfx950) GEMM-family library
+ * (libmi355gemm.so).
+ *
+ * Drop-in boundary for the GEMM-family operators of champloo2878/cuPilot-Kernels
+ * (kernels/1..4, 6..18).  Each reference operator is a libtorch host function
+ * `torch::Tensor <name>(torch::Tensor A, torch::Tensor B)`; the entry points
+ * below are what a C FFI for those operators binds: device pointers, sizes and
+ * a stream, no torch types.  Each one cites the reference function it replaces.
+ *
+ * Conventions (all entry points):
+ *   - Pointers are device pointers to fp32 data; matrices are row-major with
+ *     the stated leading dimension (elements).
+ *   - `stream` is a hipStream_t passed as void*; NULL is the null stream.
+ *     Work is enqueued asynchronously; nothing synchronises the host.
+ *   - The library never allocates or frees device memory and keeps no pointer
+ *     after returning.  Entry points that need scratch take a workspace; its
+ *     size comes from the matching *_workspace_bytes query.
+ *   - Return value: MI_OK (0); a negative mi_status for an invalid argument
+ *     (checked before any launch); a positive hipError_t for a launch failure.
+ *     mi_status_string() turns either into text.
+ *   - A zero-size dimension is valid: the output is written with zeros where it
+ *     has elements (or left untouched if it has none) and no MFMA kernel runs.
+ *   - Reentrant: no global mutable state; concurrent calls on different
+ *     streams are independent.
+ */
+#ifndef MI355_GEMM_H
+#define MI355_GEMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#ifndef MI_API
+#define MI_API __attribute__((visibility("default")))
+#endif
+
+typedef enum {
+    MI_OK = 0,
+    MI_ERR_NULL_POINTER = -1,
+    MI_ERR_BAD_SIZE = -2,       /* negative size, or size beyond int32 tiles */
+    MI_ERR_BAD_LAYOUT = -3,     /* op / structure enum out of range */
+    MI_ERR_BAD_LD = -4,         /* leading dimension smaller than the row */
+    MI_ERR_NOT_SQUARE = -5,     /* structured op on a non-square problem */
+    MI_ERR_WORKSPACE = -6,      /* workspace missing or too small */
+    MI_ERR_NO_DEVICE = -7       /* no HIP device / device query failed */
+} mi_status;
+
+typedef enum { MI_OP_N = 0, MI_OP_T = 1 } mi_op;
+
+typedef enum {
+    MI_DENSE = 0,
+    MI_LOWER = 1,   /* C = tril(tril(A) . tril(B)), exact zeros above the diagonal */
+    MI_UPPER = 2    /* C = triu(triu(A) . triu(B)), exact zeros below the diagonal */
+} mi_structure;
+
+/*
+ * Generic strided-batched contraction C[b] = op_a(A[b]) . op_b(B[b]).
+ *   op_a = N: A[b] is M x K with row stride lda;  T: A[b] is stored K x M (lda).
+ *   op_b = N: B[b] is K x N with row stride ldb;  T: B[b] is stored N x K (ldb).
+ *   C[b] is M x N with row stride ldc.  stride_* are batch strides in elements
+ *   (stride_b = 0 broadcasts one B to every batch).
+ * Every named entry point below is a thin front of this one.
+ */
+typedef struct {
+    const float* A;
+    const float* B;
+    float* C;
+    int64_t M, N, K, batch;
+    int64_t lda, ldb, ldc;
+    int64_t stride_a, stride_b, stride_c;
+    int32_t op_a, op_b;       /* mi_op */
+    int32_t structure;        /* mi_structure; square, batch 1, N/N layouts */
+    int32_t plan_override;    /* 0 = scheduler's choice; else an mi_plan_id (tests, tuning) */
+    void* workspace;
+    size_t workspace_bytes;
+} mi_gemm_args;
+
+/* Scheduler decision for one contraction (host-only, no device access). */
+typedef struct {
+    int32_t plan_id;        /* kernel instantiation */
+    int32_t block_m, block_n, block_k;
+    int32_t tiles_m, tiles_n;
+    int32_t split_k;        /* 1 = no split; else K is cut into split_k chunks */
+    int64_t k_chunk;        /* elements of K per split (multiple of block_k) */
+    int32_t group_m;        /* tile rows per raster group */
+    int64_t grid;           /* workgroups launched by the contraction kernel */
+    size_t workspace_bytes; /* split-K partial tiles */
+} mi_plan;
+
+MI_API int mi_gemm_f32(const mi_gemm_args* args, void* stream);
+MI_API size_t mi_gemm_workspace_bytes(const mi_gemm_args* args);
+/* Pure host function: what mi_gemm_f32 would launch on a device with num_cus
+ * compute units.  Exposed for tests and tuning. */
+MI_API int mi_gemm_plan(const mi_gemm_args* args, int32_t num_cus, mi_plan* out);
+
+/* ---- one entry point per reference operator ------------------------------ */
+
+/* kernels/1_Square_matrix_multiplication_best_kernel.cu:189 matmul_cuda(A, B):
+ * C = A . B, all N x N. */
+MI_API int mi_square_matmul_f32(const float* A, const float* B, float* C, int64_t N, void* stream);
+
+/* kernels/2_Standard_matrix_multiplication_best_kernel.cu:117 matmul_cuda and
+ * kernels/8_Matmul_with_irregular_shapes_best_kernel.cu:155 matmul_cuda:
+ * C (M x N) = A (M x K) . B (K x N), any sizes. */
+MI_API int mi_matmul_f32(const float* A, const float* B, float* C,
+                  int64_t M, int64_t K, int64_t N, void* stream);
+
+/* kernels/3_Batched_matrix_multiplication_best_kernel.cu:113 batched_matmul_cuda:
+ * C[b] (M x N) = A[b] (M x K) . B[b] (K x N). */
+MI_API int mi_batched_matmul_f32(const float* A, const float* B, float* C,
+                          int64_t batch, int64_t M, int64_t K, int64_t N, void* stream);
+
+/* kernels/4_Matrix_vector_multiplication_best_kernel.cu:84 gemv_cuda:
+ * y (M) = A (M x K) . x (K).  Uses a workspace of mi_gemv_workspace_bytes(M, K)
+ * bytes for its deterministic split-K partial sums (may be 0 bytes). */
+MI_API size_t mi_gemv_workspace_bytes(int64_t M, int64_t K);
+MI_API int mi_gemv_f32(const float* A, const float* x, float* y, int64_t M, int64_t K,
+                void* workspace, size_t workspace_bytes, void* stream);
+
+/* kernels/6_Matmul_with_large_K_dimension_best_kernel.cu:128 matmul_cuda:
+ * C (M x N) = A (M x K) . B (K x N) for K >> M, N; single-launch split-K with a
+ * fixed-order reduction (bitwise deterministic).  Workspace from
+ * mi_matmul_large_k_workspace_bytes. */
+MI_API size_t mi_matmul_large_k_workspace_bytes(int64_t M, int64_t K, int64_t N);
+MI_API int mi_matmul_large_k_f32(const float* A, const float* B, float* C,
+                          int64_t M, int64_t K, int64_t N,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/* kernels/7_Matmul_with_small_K_dimension_best_kernel.cu:80 gemm_cuda:
+ * C (M x N) = A (M x K) . B (K x N) for small K (store-bound). */
+MI_API int mi_gemm_small_k_f32(const float* A, const float* B, float* C,
+                        int64_t M, int64_t K, int64_t N, void* stream);
+
+/* kernels/9_Tall_skinny_matrix_multiplication_best_kernel.cu:145
+ * tall_skinny_matmul_cuda: A is M x N, B is N x M, C (M x M) = A . B. */
+MI_API int mi_tall_skinny_matmul_f32(const float* A, const float* B, float* C,
+                              int64_t M, int64_t N, void* stream);
+
+/* kernels/10_3D_tensor_matrix_multiplication_best_kernel.cu:180 batched_matmul_cuda:
+ * out[n] (M x L) = A[n] (M x K) . B (K x L), A is N x M x K. */
+MI_API int mi_tensor3d_matmul_f32(const float* A, const float* B, float* out,
+                           int64_t N, int64_t M, int64_t K, int64_t L, void* stream);
+
+/* kernels/11_4D_tensor_matrix_multiplication_best_kernel.cu:132 tensor_matmul_cuda:
+ * out[b,i,j,:] = A[b,i,j,:] . B, A is b x i x j x l, B is l x k. */
+MI_API int mi_tensor4d_matmul_f32(const float* A, const float* B, float* out,
+                           int64_t b, int64_t i, int64_t j, int64_t l, int64_t k,
+                           void* stream);
+
+/* kernels/12_Matmul_with_diagonal_matrices_best_kernel.cu:43 diag_mult_cuda:
+ * out (N x M) = diag(a) . B, a has length N; one fp32 multiply per element. */
+MI_API int mi_diag_mult_f32(const float* a, const float* B, float* out,
+                     int64_t N, int64_t M, void* stream);
+
+/* kernels/13_Matmul_for_symmetric_matrices_best_kernel.cu:134
+ * symmetric_matmul_cuda: C = A . B for symmetric N x N A and B.  The kernel
+ * reads both operands K-contiguous (valid because A = A^T and B = B^T). */
+MI_API int mi_symmetric_matmul_f32(const float* A, const float* B, float* C, int64_t N,
+                            void* stream);
+
+/* kernels/14_Matmul_for_upper_triangular_matrices_best_kernel.cu:135
+ * upper_tri_matmul_cuda: C = triu(triu(A) . triu(B)), N x N; zero tiles are
+ * skipped and the lower triangle is written with exact zeros. */
+MI_API int mi_upper_tri_matmul_f32(const float* A, const float* B, float* C, int64_t N,
+                            void* stream);
+
+/* kernels/15_Matmul_for_lower_triangular_matrices_best_kernel.cu:155
+ * lower_tri_mul_cuda: C = tril(tril(A) . tril(B)), N x N. */
+MI_API int mi_lower_tri_mul_f32(const float* A, const float* B, float* C, int64_t N,
+                         void* stream);
+
+/* kernels/16_Matmul_with_transposed_A_best_kernel.cu:124 matmul_transposed_cuda:
+ * C (M x N) = A^T . B with A stored K x M and B K x N. */
+MI_API int mi_matmul_transposed_a_f32(const float* A, const float* B, float* C,
+                               int64_t M, int64_t K, int64_t N, void* stream);
+
+/* kernels/17_Matmul_with_transposed_B_best_kernel.cu:267 matmul_cuda:
+ * C (M x N) = A . B^T with A M x K and B stored N x K. */
+MI_API int mi_matmul_transposed_b_f32(const float* A, const float* B, float* C,
+                               int64_t M, int64_t K, int64_t N, void* stream);
+
+/* kernels/18_Matmul_with_transposed_both_best_kernel.cu:152 matmul_transposed_cuda:
+ * C (M x N) = A^T . B^T with A stored K x M and B stored N x K. */
+MI_API int mi_matmul_transposed_both_f32(const float* A, const float* B, float* C,
+                                  int64_t M, int64_t K, int64_t N, void* stream);
+
+/* ---- utilities ------------------------------------------------------------ */
+
+/* Counter-based input generator (no reference counterpart; test and benchmark
+ * inputs): out[i] = float(splitmix64((seed << 40) + offset + i) >> 40) * 2^-23 - 1,
+ * uniform on [-1, 1), bit-identical to the host generator. */
+MI_API int mi_fill_uniform_f32(float* out, int64_t n, uint64_t seed, int64_t offset, void* stream);
+
+MI_API const char* mi_status_string(int status);
+/* Library version, e.g. "mi355_gemm 0.1.0 gfx950". */
+MI_API const char* mi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MI355_GEMM_H */

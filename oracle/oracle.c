@@ -1,0 +1,225 @@
+/*
+ * oracle.c -- TEST INFRASTRUCTURE ONLY.
+ *
+ * CPU restatement of the mathematics of the reference's GEMM-family operators
+ * (champloo2878/cuPilot-Kernels, kernels/1..18 except 5), accumulated in fp64.
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load
+ * this library, and only as the checker.  The product path never calls it.
+ *
+ * The reference computes in fp16/bf16/tf32 on tensor cores; the operators it
+ * stands for are exact real-number contractions, so the oracle restates the
+ * operator, not the reference's rounding.  Each function cites the reference
+ * wrapper whose shape logic it follows:
+ *
+ *   orc_gemm_f64      C[b] = op(A[b]) . op(B[b])  (dense / batched / transposed)
+ *                     kernels/1_...:190, 2_...:122-124, 3_...:126-131,
+ *                     6_...:131-134, 7_...:81-85, 8_...:156-160, 9_...:146-148,
+ *                     10_...:181-186, 11_...:136-146, 13_...:135-136,
+ *                     16_...:127-132 (A stored KxM), 17_...:268-272 (B stored NxK),
+ *                     18_...:156-160 (both)
+ *   orc_gemm_f64 with structure LOWER / UPPER
+ *                     tril(tril(A).tril(B)) -- kernels/15_...:155-206 (k-range
+ *                     [bx,by], zero store above the diagonal);
+ *                     triu(triu(A).triu(B)) -- kernels/14_...:57,74-75,84-85 (input
+ *                     masks), 123-128 (masked store)
+ *   orc_gemv_f64      y = A.x -- kernels/4_...:84-92 (B is Kx1, output Mx1)
+ *   orc_diag_f32      out[i,j] = a[i]*B[i,j] -- kernels/12_...:43-62 (one fp32
+ *                     multiply per element, so bitwise-exact)
+ *   orc_fill_uniform_f32 / orc_fill_int_f32
+ *                     counter-based splitmix64 input generator shared with the
+ *                     device fill kernel, so any element can be regenerated on
+ *                     the host without copying a multi-GiB operand back.
+ *
+ * Pins (tests/test_oracle.py): published splitmix64 vectors, committed integer
+ * fixtures (exact), numpy float64 matmul (independent implementation),
+ * identity/permutation/all-ones/rank-1 closed forms, brute force on tiny shapes,
+ * planted-mistake checks (transposed operand, dropped term, wrong triangle).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define ORC_EXPORT __attribute__((visibility("default")))
+
+/* ---- generator -------------------------------------------------------- */
+
+/* splitmix64 output function (S. Vigna, public domain algorithm): the value
+ * the sequential generator returns for state x. */
+ORC_EXPORT uint64_t orc_splitmix64(uint64_t x) {
+    uint64_t z = x + 0x9E3779B97F4A7C15ULL;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+    return z ^ (z >> 31);
+}
+
+/* Element i of stream `seed`: x = splitmix64((seed << 40) + i);
+ * v = float(x >> 40) * 2^-23 - 1, exact in fp32, uniform on [-1, 1 - 2^-23]. */
+ORC_EXPORT void orc_fill_uniform_f32(float* out, int64_t n, uint64_t seed, int64_t offset) {
+    const uint64_t base = (seed << 40) + (uint64_t)offset;
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) {
+        uint64_t z = orc_splitmix64(base + (uint64_t)i);
+        out[i] = (float)(z >> 40) * 0x1p-23f - 1.0f;
+    }
+}
+
+/* Integer-valued variant: v = lo + (x >> 32) % (hi - lo + 1). */
+ORC_EXPORT void orc_fill_int_f32(float* out, int64_t n, uint64_t seed, int64_t offset,
+                                 int32_t lo, int32_t hi) {
+    const uint64_t base = (seed << 40) + (uint64_t)offset;
+    const uint64_t span = (uint64_t)(hi - lo + 1);
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) {
+        uint64_t z = orc_splitmix64(base + (uint64_t)i);
+        out[i] = (float)(lo + (int64_t)((z >> 32) % span));
+    }
+}
+
+/* ---- dense / structured contraction ------------------------------------ */
+
+enum { ORC_DENSE = 0, ORC_LOWER = 1, ORC_UPPER = 2 };
+
+/* Element (r, c) of a logical matrix held with row stride rs and column
+ * stride cs (the transposed layouts are just swapped strides). */
+static inline double at2(const float* p, int64_t r, int64_t c, int64_t rs, int64_t cs) {
+    return (double)p[r * rs + c * cs];
+}
+
+/*
+ * C[b][i][j] = sum_k opA[b][i][k] * opB[b][k][j], fp64 accumulation, written
+ * as double.  Logical opA is MxK with element (i,k) at A[b*sa + i*a_rs + k*a_cs];
+ * logical opB is KxN with (k,j) at B[b*sb + k*b_rs + j*b_cs]; C is dense
+ * batch x M x N (row-major).
+ * structure LOWER: inputs masked to their lower triangles, output to its
+ *   lower triangle (exact zeros above); UPPER symmetric.  Square only.
+ * rows: if non-NULL, only rows rows[0..nrows) of every batch are produced and
+ *   C is batch x nrows x N.
+ */
+ORC_EXPORT void orc_gemm_f64(const float* A, const float* B, double* C,
+                             int64_t batch, int64_t M, int64_t N, int64_t K,
+                             int64_t sa, int64_t a_rs, int64_t a_cs,
+                             int64_t sb, int64_t b_rs, int64_t b_cs,
+                             int32_t structure, const int64_t* rows, int64_t nrows) {
+    const int64_t R = rows ? nrows : M;
+    for (int64_t b = 0; b < batch; ++b) {
+        const float* Ab = A + b * sa;
+        const float* Bb = B + b * sb;
+        /* opB materialised as a dense KxN double panel so the inner loop is unit stride */
+        double* Bd = (double*)malloc((size_t)(K * N > 0 ? K * N : 1) * sizeof(double));
+#pragma omp parallel for schedule(static)
+        for (int64_t k = 0; k < K; ++k) {
+            for (int64_t j = 0; j < N; ++j) {
+                double v = at2(Bb, k, j, b_rs, b_cs);
+                if (structure == ORC_LOWER && k < j) v = 0.0;
+                if (structure == ORC_UPPER && k > j) v = 0.0;
+                Bd[k * N + j] = v;
+            }
+        }
+        double* Cb = C + b * R * N;
+#pragma omp parallel for schedule(dynamic, 4)
+        for (int64_t r = 0; r < R; ++r) {
+            const int64_t i = rows ? rows[r] : r;
+            double* crow = Cb + r * N;
+            for (int64_t j = 0; j < N; ++j) crow[j] = 0.0;
+            for (int64_t k = 0; k < K; ++k) {
+                double a = at2(Ab, i, k, a_rs, a_cs);
+                if (structure == ORC_LOWER && k > i) a = 0.0;
+                if (structure == ORC_UPPER && k < i) a = 0.0;
+                if (a == 0.0) continue;
+                const double* brow = Bd + k * N;
+                for (int64_t j = 0; j < N; ++j) crow[j] += a * brow[j];
+            }
+            if (structure == ORC_LOWER)
+                for (int64_t j = i + 1; j < N; ++j) crow[j] = 0.0;
+            if (structure == ORC_UPPER)
+                for (int64_t j = 0; j < i && j < N; ++j) crow[j] = 0.0;
+        }
+        free(Bd);
+    }
+}
+
+/* Sparse sampling: out[t] = sum_k opA[b_t][i_t][k] * opB[b_t][k][j_t] for the
+ * listed (b, i, j) triples; used at full BASELINE sizes where a dense fp64
+ * reference would not fit the test budget. Dense structure only. */
+ORC_EXPORT void orc_gemm_entries_f64(const float* A, const float* B, double* out,
+                                     const int64_t* bij, int64_t count, int64_t K,
+                                     int64_t sa, int64_t a_rs, int64_t a_cs,
+                                     int64_t sb, int64_t b_rs, int64_t b_cs) {
+#pragma omp parallel for schedule(static)
+    for (int64_t t = 0; t < count; ++t) {
+        const int64_t b = bij[3 * t], i = bij[3 * t + 1], j = bij[3 * t + 2];
+        const float* Ab = A + b * sa;
+        const float* Bb = B + b * sb;
+        double s = 0.0;
+        for (int64_t k = 0; k < K; ++k) s += at2(Ab, i, k, a_rs, a_cs) * at2(Bb, k, j, b_rs, b_cs);
+        out[t] = s;
+    }
+}
+
+/* y[i] = sum_k A[i*lda + k] * x[k] for the listed rows (all rows if rows == NULL). */
+ORC_EXPORT void orc_gemv_f64(const float* A, const float* x, double* y, int64_t M, int64_t K,
+                             int64_t lda, const int64_t* rows, int64_t nrows) {
+    const int64_t R = rows ? nrows : M;
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < R; ++r) {
+        const int64_t i = rows ? rows[r] : r;
+        const float* a = A + i * lda;
+        double s = 0.0;
+        for (int64_t k = 0; k < K; ++k) s += (double)a[k] * (double)x[k];
+        y[r] = s;
+    }
+}
+
+/* GEMV over a generated A: row i of A is stream seed_a at offset i*K, so an
+ * 8 GiB operand can be checked row by row without holding it. */
+ORC_EXPORT void orc_gemv_generated_f64(uint64_t seed_a, const float* x, double* y, int64_t K,
+                                       const int64_t* rows, int64_t nrows) {
+#pragma omp parallel
+    {
+        float* buf = (float*)malloc((size_t)K * sizeof(float));
+#pragma omp for schedule(dynamic, 1)
+        for (int64_t r = 0; r < nrows; ++r) {
+            const uint64_t base = (seed_a << 40) + (uint64_t)(rows[r] * K);
+            for (int64_t k = 0; k < K; ++k) {
+                uint64_t z = orc_splitmix64(base + (uint64_t)k);
+                buf[k] = (float)(z >> 40) * 0x1p-23f - 1.0f;
+            }
+            double s = 0.0;
+            for (int64_t k = 0; k < K; ++k) s += (double)buf[k] * (double)x[k];
+            y[r] = s;
+        }
+        free(buf);
+    }
+}
+
+/* out[i*M + j] = a[i] * B[i*M + j] in fp32: a single rounding, so the device
+ * result must match bitwise. */
+ORC_EXPORT void orc_diag_f32(const float* a, const float* B, float* out, int64_t N, int64_t M) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < N; ++i)
+        for (int64_t j = 0; j < M; ++j) out[i * M + j] = a[i] * B[i * M + j];
+}
+
+/* max_t |got[t] - ref[t]| over n elements (fp32 result vs fp64 reference). */
+ORC_EXPORT double orc_max_abs_diff(const float* got, const double* ref, int64_t n) {
+    double m = 0.0;
+#pragma omp parallel for reduction(max : m)
+    for (int64_t t = 0; t < n; ++t) {
+        double d = fabs((double)got[t] - ref[t]);
+        if (d != d) d = INFINITY; /* NaN counts as failure */
+        if (d > m) m = d;
+    }
+    return m;
+}
+
+ORC_EXPORT int orc_num_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}

@@ -1,0 +1,115 @@
+"""GPU tests of the drop-in operator layer: each reference function name
+(``ck.pNN.<name>(A, B)``, kernels/N_...) on torch tensors, against the fp64
+oracle, including transposed-view inputs and the reference's zero-size paths."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import assert_close, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+
+def _u(orc, shape, seed):
+    return orc.uniform(shape, seed)
+
+
+def test_every_pid_module(ck, orc, dev):
+    M, K, N = 130, 96, 70
+    a, b = _u(orc, (M, K), 1), _u(orc, (K, N), 2)
+    A, B = to_dev(a), to_dev(b)
+    ref = orc.gemm(a, b)
+    for fn in (ck.p02.matmul_cuda, ck.p06.matmul_cuda, ck.p07.gemm_cuda, ck.p08.matmul_cuda):
+        assert_close(orc, to_host(fn(A, B)), ref, K, what=str(fn))
+
+    s = _u(orc, (N, N), 3)
+    S = to_dev(s)
+    assert_close(orc, to_host(ck.p01.matmul_cuda(S, S)), orc.gemm(s, s), N, what="p01")
+
+    a3, b3 = _u(orc, (3, 20, 30), 4), _u(orc, (3, 30, 40), 5)
+    assert_close(orc, to_host(ck.p03.batched_matmul_cuda(to_dev(a3), to_dev(b3))),
+                 orc.gemm(a3, b3), 30, what="p03")
+
+    x = _u(orc, (K, 1), 6)
+    y = ck.p04.gemv_cuda(A, to_dev(x))
+    assert tuple(y.shape) == (M, 1)
+    assert_close(orc, to_host(y)[:, 0], orc.gemv(a, x[:, 0]), K, what="p04")
+
+    ts_a, ts_b = _u(orc, (200, 16), 7), _u(orc, (16, 200), 8)
+    assert_close(orc, to_host(ck.p09.tall_skinny_matmul_cuda(to_dev(ts_a), to_dev(ts_b))),
+                 orc.gemm(ts_a, ts_b), 16, what="p09")
+
+    t3, w = _u(orc, (4, 25, K), 9), _u(orc, (K, N), 10)
+    out = ck.p10.batched_matmul_cuda(to_dev(t3), to_dev(w))
+    assert tuple(out.shape) == (4, 25, N)
+    assert_close(orc, to_host(out).reshape(-1, N), orc.gemm(t3.reshape(-1, K), w), K, what="p10")
+
+    t4 = _u(orc, (2, 3, 5, K), 11)
+    out = ck.p11.tensor_matmul_cuda(to_dev(t4), to_dev(w))
+    assert tuple(out.shape) == (2, 3, 5, N)
+    assert_close(orc, to_host(out).reshape(-1, N), orc.gemm(t4.reshape(-1, K), w), K, what="p11")
+
+    d = _u(orc, (M,), 12)
+    np.testing.assert_array_equal(to_host(ck.p12.diag_mult_cuda(to_dev(d), A)), orc.diag_mult(d, a))
+
+    r1, r2 = _u(orc, (N, N), 13), _u(orc, (N, N), 14)
+    sa, sb = (r1 + r1.T) / 2, (r2 + r2.T) / 2
+    assert_close(orc, to_host(ck.p13.symmetric_matmul_cuda(to_dev(sa), to_dev(sb))),
+                 orc.gemm(sa, sb), N, what="p13")
+    up = to_host(ck.p14.upper_tri_matmul_cuda(to_dev(np.triu(r1)), to_dev(np.triu(r2))))
+    assert_close(orc, up, orc.gemm(np.triu(r1), np.triu(r2), orc.UPPER), N, what="p14")
+    lo = to_host(ck.p15.lower_tri_mul_cuda(to_dev(np.tril(r1)), to_dev(np.tril(r2))))
+    assert_close(orc, lo, orc.gemm(np.tril(r1), np.tril(r2), orc.LOWER), N, what="p15")
+
+    at, bt = _u(orc, (K, M), 15), _u(orc, (N, K), 16)
+    assert_close(orc, to_host(ck.p16.matmul_transposed_cuda(to_dev(at), B)),
+                 orc.gemm(at.T, b), K, what="p16")
+    assert_close(orc, to_host(ck.p17.matmul_cuda(A, to_dev(bt))), orc.gemm(a, bt.T), K,
+                 what="p17")
+    assert_close(orc, to_host(ck.p18.matmul_transposed_cuda(to_dev(at), to_dev(bt))),
+                 orc.gemm(at.T, bt.T), K, what="p18")
+
+
+def test_transposed_views_are_consumed_in_place(ck, orc, dev):
+    M, K, N = 100, 80, 60
+    a, b = _u(orc, (K, M), 21), _u(orc, (N, K), 22)  # stored transposed
+    A_view, B_view = to_dev(a).t(), to_dev(b).t()     # logical M x K and K x N views
+    assert not A_view.is_contiguous() and not B_view.is_contiguous()
+    got = to_host(ck.p02.matmul_cuda(A_view, B_view))
+    assert_close(orc, got, orc.gemm(a.T, b.T), K, what="views")
+    # a sliced (non-unit, non-transposed) view goes through a copy
+    big = to_dev(_u(orc, (M, 2 * K), 23))
+    sl = big[:, ::2]
+    got = to_host(ck.p02.matmul_cuda(sl, to_dev(b.T.copy())))
+    assert_close(orc, got, orc.gemm(np.ascontiguousarray(to_host(sl)), b.T.copy()), K, what="slice")
+
+
+def test_model_new_wrappers(ck, orc, dev):
+    a, b = _u(orc, (64, 48), 31), _u(orc, (48, 32), 32)
+    out = ck.ModelNew(2)(to_dev(a), to_dev(b))
+    assert_close(orc, to_host(out), orc.gemm(a, b), 48, what="ModelNew(2)")
+    with pytest.raises(ValueError):
+        ck.ModelNew(5)
+
+
+def test_zero_size_inputs(ck, dev):
+    e = torch.empty((0, 5), device="cuda")
+    f = torch.empty((5, 3), device="cuda")
+    assert tuple(ck.p02.matmul_cuda(e, f).shape) == (0, 3)
+    z = ck.p02.matmul_cuda(torch.empty((4, 0), device="cuda"), torch.empty((0, 3), device="cuda"))
+    assert tuple(z.shape) == (4, 3) and torch.all(z == 0)
+    assert tuple(ck.p01.matmul_cuda(torch.empty((0, 0), device="cuda"),
+                                    torch.empty((0, 0), device="cuda")).shape) == (0, 0)
+    y = ck.p04.gemv_cuda(torch.empty((3, 0), device="cuda"), torch.empty((0, 1), device="cuda"))
+    assert torch.all(y == 0)
+
+
+def test_runs_on_current_stream(ck, orc, dev):
+    a, b = _u(orc, (256, 256), 41), _u(orc, (256, 256), 42)
+    A, B = to_dev(a), to_dev(b)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        C = ck.p02.matmul_cuda(A, B)
+    s.synchronize()
+    assert_close(orc, C.cpu().numpy(), orc.gemm(a, b), 256, what="side stream")

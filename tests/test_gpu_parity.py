@@ -1,0 +1,345 @@
+"""GPU parity of the HIP kernels, called through the C ABI (libmi355gemm.so),
+against the fp64 CPU oracle on the same seeded inputs.
+
+Bar: normalised max error <= 1e-4 (max|C - C64| / (sqrt(K) max|A| max|B|))
+for real-valued inputs; bitwise equality for integer-valued inputs (every
+partial sum is an integer below 2^24, so any summation order is exact), for
+diag(a).B (one fp32 multiply) and for the structural zeros of the triangular
+products; bitwise equality across repeated runs (determinism).
+"""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import (assert_close, cur_stream, dev_uniform, gemm_args, run_gemm, to_dev, to_host,
+                      vp, workspace)
+
+pytestmark = pytest.mark.gpu
+
+LAYOUTS = [(0, 0), (1, 0), (0, 1), (1, 1)]  # (op_a, op_b): NN, TN, NT, TT
+SHAPES = [  # (M, N, K) -- tile multiples, ragged edges, degenerate extents
+    (1024, 1024, 1024), (256, 256, 16), (128, 64, 48), (1023, 517, 2049), (1, 1, 1),
+    (65, 129, 31), (7, 63, 65), (300, 4, 257), (4, 300, 8), (333, 333, 1),
+]
+
+
+def _host_operands(orc, M, N, K, op_a, op_b, seed):
+    """Stored (not logical) operands, as the kernels see them."""
+    a_st = orc.uniform((K, M) if op_a else (M, K), seed)
+    b_st = orc.uniform((N, K) if op_b else (K, N), seed + 1)
+    return a_st, b_st
+
+
+def _logical(x_st, op):
+    return x_st.T if op else x_st
+
+
+@pytest.mark.parametrize("n", [1, 3, 1000, 65537])
+@pytest.mark.parametrize("seed", [0, 17, 2 ** 20 + 5])
+def test_device_generator_matches_host(ck, orc, dev, n, seed):
+    got = to_host(dev_uniform(ck, (n,), seed))
+    np.testing.assert_array_equal(got, orc.uniform((n,), seed))
+    off = to_host(dev_uniform(ck, (n,), seed, offset=12345))
+    np.testing.assert_array_equal(off, orc.uniform((n,), seed, offset=12345))
+
+
+@pytest.mark.parametrize("op_a,op_b", LAYOUTS)
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_gemm_layouts_auto_plan(ck, orc, dev, op_a, op_b, M, N, K):
+    a_st, b_st = _host_operands(orc, M, N, K, op_a, op_b, seed=7)
+    A, B = to_dev(a_st), to_dev(b_st)
+    C = torch.full((M, N), float("nan"), device="cuda")
+    args = gemm_args(ck, A, B, C, M, N, K, op_a, op_b)
+    ws = workspace(ck, args)
+    args = gemm_args(ck, A, B, C, M, N, K, op_a, op_b, ws=ws)
+    ck.abi.check(run_gemm(ck, args), "mi_gemm_f32")
+    ref = orc.gemm(_logical(a_st, op_a), _logical(b_st, op_b))
+    assert_close(orc, to_host(C), ref, K, np.abs(a_st).max(), np.abs(b_st).max(),
+                 f"layout {op_a}{op_b} {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("op_a,op_b", LAYOUTS)
+@pytest.mark.parametrize("cfg", [1, 2, 3])
+@pytest.mark.parametrize("M,N,K", [(512, 512, 512), (300, 200, 100), (64, 640, 37)])
+def test_gemm_every_tile_config(ck, orc, dev, op_a, op_b, cfg, M, N, K):
+    a_st, b_st = _host_operands(orc, M, N, K, op_a, op_b, seed=11)
+    A, B = to_dev(a_st), to_dev(b_st)
+    C = torch.full((M, N), float("nan"), device="cuda")
+    ck.abi.check(run_gemm(ck, gemm_args(ck, A, B, C, M, N, K, op_a, op_b, override=cfg)))
+    ref = orc.gemm(_logical(a_st, op_a), _logical(b_st, op_b))
+    assert_close(orc, to_host(C), ref, K, np.abs(a_st).max(), np.abs(b_st).max(),
+                 f"cfg {cfg} layout {op_a}{op_b} {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("op_a,op_b", LAYOUTS)
+@pytest.mark.parametrize("cfg", [1, 2, 3])
+def test_integer_inputs_bitwise(ck, orc, dev, op_a, op_b, cfg):
+    M, N, K = 200, 136, 1000
+    a_st = orc.integers((K, M) if op_a else (M, K), seed=21)
+    b_st = orc.integers((N, K) if op_b else (K, N), seed=22)
+    A, B = to_dev(a_st), to_dev(b_st)
+    C = torch.empty((M, N), device="cuda")
+    ck.abi.check(run_gemm(ck, gemm_args(ck, A, B, C, M, N, K, op_a, op_b, override=cfg)))
+    ref = orc.gemm(_logical(a_st, op_a), _logical(b_st, op_b))
+    assert np.all(ref == np.round(ref))
+    np.testing.assert_array_equal(to_host(C), ref.astype(np.float32))
+
+
+def test_closed_forms_identity_ones_rank1(ck, orc, dev):
+    n = 384
+    I = np.eye(n, dtype=np.float32)
+    X = orc.uniform((n, n), seed=31)
+    for a, b, want in [(I, X, X), (X, I, X),
+                       (np.ones((n, 700), np.float32), np.ones((700, n), np.float32),
+                        np.full((n, n), 700, np.float32))]:
+        C = torch.empty((a.shape[0], b.shape[1]), device="cuda")
+        ck.abi.check(run_gemm(ck, gemm_args(ck, to_dev(a), to_dev(b), C, a.shape[0], b.shape[1],
+                                            a.shape[1])))
+        np.testing.assert_array_equal(to_host(C), want)
+    u = orc.integers((n, 1), seed=32, lo=-3, hi=3)
+    v = orc.integers((1, n), seed=33, lo=-3, hi=3)
+    C = torch.empty((n, n), device="cuda")
+    ck.abi.check(run_gemm(ck, gemm_args(ck, to_dev(u), to_dev(v), C, n, n, 1)))
+    np.testing.assert_array_equal(to_host(C), u * v)
+
+
+@pytest.mark.parametrize("split", [2, 3, 8, 64])
+@pytest.mark.parametrize("cfg", [1, 2, 3])
+def test_split_k_partition_and_determinism(ck, orc, dev, split, cfg):
+    M, N, K = 160, 96, 20000
+    a_st, b_st = orc.uniform((M, K), 41), orc.uniform((K, N), 42)
+    A, B = to_dev(a_st), to_dev(b_st)
+    ov = cfg | (split << 8)
+    C = torch.empty((M, N), device="cuda")
+    probe = gemm_args(ck, A, B, C, M, N, K, override=ov)
+    ws = workspace(ck, probe)
+    outs = []
+    for _ in range(3):
+        C = torch.full((M, N), float("nan"), device="cuda")
+        ck.abi.check(run_gemm(ck, gemm_args(ck, A, B, C, M, N, K, override=ov, ws=ws)))
+        outs.append(to_host(C))
+    assert_close(orc, outs[0], orc.gemm(a_st, b_st), K, what=f"split {split} cfg {cfg}")
+    for o in outs[1:]:
+        np.testing.assert_array_equal(o, outs[0])
+
+
+def test_split_k_without_workspace_is_rejected(ck, dev):
+    M, N, K = 64, 64, 8192
+    A = torch.zeros((M, K), device="cuda")
+    B = torch.zeros((K, N), device="cuda")
+    C = torch.zeros((M, N), device="cuda")
+    rc = run_gemm(ck, gemm_args(ck, A, B, C, M, N, K, override=2 | (4 << 8)))
+    assert rc == ck.abi.MI_ERR_WORKSPACE
+
+
+@pytest.mark.parametrize("op_a,op_b", LAYOUTS)
+def test_strided_batched_and_broadcast(ck, orc, dev, op_a, op_b):
+    batch, M, N, K = 5, 96, 80, 72
+    a_st = orc.uniform((batch,) + ((K, M) if op_a else (M, K)), 51)
+    b_st = orc.uniform((batch,) + ((N, K) if op_b else (K, N)), 52)
+    A, B = to_dev(a_st), to_dev(b_st)
+    C = torch.empty((batch, M, N), device="cuda")
+    sa, sb = a_st[0].size, b_st[0].size
+    ck.abi.check(run_gemm(ck, gemm_args(ck, A, B, C, M, N, K, op_a, op_b, batch=batch, sa=sa,
+                                        sb=sb, sc=M * N)))
+    la = np.swapaxes(a_st, 1, 2) if op_a else a_st
+    lb = np.swapaxes(b_st, 1, 2) if op_b else b_st
+    assert_close(orc, to_host(C), orc.gemm(la, lb), K, what="batched")
+    # stride_b = 0 broadcasts B[0] to every batch
+    C2 = torch.empty((batch, M, N), device="cuda")
+    ck.abi.check(run_gemm(ck, gemm_args(ck, A, B, C2, M, N, K, op_a, op_b, batch=batch, sa=sa,
+                                        sb=0, sc=M * N)))
+    assert_close(orc, to_host(C2), orc.gemm(la, np.ascontiguousarray(lb[:1])), K,
+                 what="broadcast")
+
+
+def test_leading_dimensions_larger_than_rows(ck, orc, dev):
+    M, N, K = 100, 60, 50
+    big_a = orc.uniform((M, K + 13), 61)
+    big_b = orc.uniform((K, N + 7), 62)
+    C_big = torch.full((M, N + 5), -7.0, device="cuda")
+    ck.abi.check(run_gemm(ck, gemm_args(ck, to_dev(big_a), to_dev(big_b), C_big, M, N, K,
+                                        lda=K + 13, ldb=N + 7, ldc=N + 5)))
+    got = to_host(C_big)
+    assert_close(orc, got[:, :N], orc.gemm(big_a[:, :K], big_b[:, :N]), K, what="ld")
+    assert np.all(got[:, N:] == -7.0), "wrote outside the ldc window"
+
+
+@pytest.mark.parametrize("structure", [1, 2])
+@pytest.mark.parametrize("n", [1, 5, 64, 100, 257, 640])
+@pytest.mark.parametrize("cfg", [0, 1, 2, 3])
+def test_triangular_products(ck, orc, dev, structure, n, cfg):
+    tri = np.tril if structure == 1 else np.triu
+    a = tri(orc.uniform((n, n), 71))
+    b = tri(orc.uniform((n, n), 72))
+    C = torch.full((n, n), float("nan"), device="cuda")
+    ck.abi.check(run_gemm(ck, gemm_args(ck, to_dev(a), to_dev(b), C, n, n, n,
+                                        structure=structure, override=cfg)))
+    got = to_host(C)
+    ref = orc.gemm(a, b, structure)
+    assert_close(orc, got, ref, n, what=f"tri {structure} n={n} cfg={cfg}")
+    zero = np.triu(np.ones((n, n), bool), 1) if structure == 1 else np.tril(np.ones((n, n), bool), -1)
+    z = got[zero]
+    assert np.all(z == 0.0) and not np.any(np.signbit(z)), "structural zeros must be +0.0"
+
+
+@pytest.mark.parametrize("structure", [1, 2])
+def test_triangular_masks_non_triangular_input(ck, orc, dev, structure):
+    # The operator is tril(tril(A) tril(B)) / triu(triu(A) triu(B)): entries of
+    # the inputs outside the triangle must not leak into the result.
+    n = 300
+    a, b = orc.uniform((n, n), 73), orc.uniform((n, n), 74)
+    C = torch.empty((n, n), device="cuda")
+    ck.abi.check(run_gemm(ck, gemm_args(ck, to_dev(a), to_dev(b), C, n, n, n, structure=structure)))
+    assert_close(orc, to_host(C), orc.gemm(a, b, structure), n, what="masked inputs")
+
+
+@pytest.mark.parametrize("M,K", [(1, 1), (7, 5), (1000, 4096), (4097, 8192), (33, 65536),
+                                 (300, 1023), (64, 1 << 18), (5000, 4)])
+@pytest.mark.parametrize("with_ws", [True, False])
+def test_gemv(ck, orc, dev, M, K, with_ws):
+    a = orc.uniform((M, K), 81)
+    x = orc.uniform((K,), 82)
+    A, X = to_dev(a), to_dev(x)
+    y = torch.full((M,), float("nan"), device="cuda")
+    L = ck.abi.lib()
+    nws = L.mi_gemv_workspace_bytes(M, K)
+    ws = torch.empty(max(nws, 1), dtype=torch.uint8, device="cuda") if (with_ws and nws) else None
+    ck.abi.check(L.mi_gemv_f32(vp(A), vp(X), vp(y), M, K, vp(ws) if ws is not None else None,
+                               nws if ws is not None else 0, cur_stream()), "gemv")
+    assert_close(orc, to_host(y), orc.gemv(a, x), K, np.abs(a).max(), np.abs(x).max(), "gemv")
+
+
+def test_gemv_unaligned_pointer(ck, orc, dev):
+    M, K = 129, 2048
+    a = orc.uniform((M * K + 1,), 83)
+    x = orc.uniform((K + 1,), 84)
+    A, X = to_dev(a), to_dev(x)
+    y = torch.empty((M,), device="cuda")
+    L = ck.abi.lib()
+    ck.abi.check(L.mi_gemv_f32(ctypes.c_void_p(A.data_ptr() + 4), ctypes.c_void_p(X.data_ptr() + 4),
+                               vp(y), M, K, None, 0, cur_stream()))
+    assert_close(orc, to_host(y), orc.gemv(a[1:].reshape(M, K), x[1:]), K, what="gemv unaligned")
+
+
+@pytest.mark.parametrize("N,M", [(1, 1), (3, 5), (8192, 8), (100, 1027), (513, 4096)])
+def test_diag_mult_bitwise(ck, orc, dev, N, M):
+    a = orc.uniform((N,), 91)
+    b = orc.uniform((N, M), 92)
+    out = torch.empty((N, M), device="cuda")
+    da, db = to_dev(a), to_dev(b)  # keep the device buffers alive across the launch
+    ck.abi.check(ck.abi.lib().mi_diag_mult_f32(vp(da), vp(db), vp(out), N, M, cur_stream()))
+    np.testing.assert_array_equal(to_host(out), orc.diag_mult(a, b))
+
+
+def test_named_entry_points(ck, orc, dev):
+    """Every per-operator C entry point against the oracle on a moderate shape."""
+    L = ck.abi.lib()
+    s = cur_stream()
+    M, K, N = 192, 160, 224
+    a, b = orc.uniform((M, K), 101), orc.uniform((K, N), 102)
+    A, B = to_dev(a), to_dev(b)
+
+    keep = []
+
+    def d(x):  # device copy that stays alive until the test ends
+        t = to_dev(x)
+        keep.append(t)
+        return vp(t)
+
+    def run(fn, *args):
+        ck.abi.check(fn(*args, s), fn.__name__)
+
+    C = torch.empty((M, N), device="cuda")
+    run(L.mi_matmul_f32, vp(A), vp(B), vp(C), M, K, N)
+    assert_close(orc, to_host(C), orc.gemm(a, b), K, what="mi_matmul_f32")
+    run(L.mi_gemm_small_k_f32, vp(A), vp(B), vp(C), M, K, N)
+    assert_close(orc, to_host(C), orc.gemm(a, b), K, what="mi_gemm_small_k_f32")
+
+    sq = orc.uniform((N, N), 103)
+    S = to_dev(sq)
+    C2 = torch.empty((N, N), device="cuda")
+    run(L.mi_square_matmul_f32, vp(S), vp(S), vp(C2), N)
+    assert_close(orc, to_host(C2), orc.gemm(sq, sq), N, what="square")
+
+    at = orc.uniform((K, M), 104)  # A stored K x M
+    bt = orc.uniform((N, K), 105)  # B stored N x K
+    At, Bt = to_dev(at), to_dev(bt)
+    run(L.mi_matmul_transposed_a_f32, vp(At), vp(B), vp(C), M, K, N)
+    assert_close(orc, to_host(C), orc.gemm(at.T, b), K, what="transposed_a")
+    run(L.mi_matmul_transposed_b_f32, vp(A), vp(Bt), vp(C), M, K, N)
+    assert_close(orc, to_host(C), orc.gemm(a, bt.T), K, what="transposed_b")
+    run(L.mi_matmul_transposed_both_f32, vp(At), vp(Bt), vp(C), M, K, N)
+    assert_close(orc, to_host(C), orc.gemm(at.T, bt.T), K, what="transposed_both")
+
+    bb, m3, k3, n3 = 3, 40, 56, 72
+    a3, b3 = orc.uniform((bb, m3, k3), 106), orc.uniform((bb, k3, n3), 107)
+    C3 = torch.empty((bb, m3, n3), device="cuda")
+    run(L.mi_batched_matmul_f32, d((a3)), d((b3)), vp(C3), bb, m3, k3, n3)
+    assert_close(orc, to_host(C3), orc.gemm(a3, b3), k3, what="batched")
+
+    t3 = orc.uniform((4, 33, k3), 108)
+    w = orc.uniform((k3, n3), 109)
+    O3 = torch.empty((4, 33, n3), device="cuda")
+    run(L.mi_tensor3d_matmul_f32, d((t3)), d((w)), vp(O3), 4, 33, k3, n3)
+    assert_close(orc, to_host(O3).reshape(-1, n3), orc.gemm(t3.reshape(-1, k3), w), k3, what="3d")
+
+    t4 = orc.uniform((2, 3, 5, k3), 110)
+    O4 = torch.empty((2, 3, 5, n3), device="cuda")
+    run(L.mi_tensor4d_matmul_f32, d((t4)), d((w)), vp(O4), 2, 3, 5, k3, n3)
+    assert_close(orc, to_host(O4).reshape(-1, n3), orc.gemm(t4.reshape(-1, k3), w), k3, what="4d")
+
+    ta = orc.uniform((300, 24), 111)
+    tb = orc.uniform((24, 300), 112)
+    O = torch.empty((300, 300), device="cuda")
+    run(L.mi_tall_skinny_matmul_f32, d((ta)), d((tb)), vp(O), 300, 24)
+    assert_close(orc, to_host(O), orc.gemm(ta, tb), 24, what="tall_skinny")
+
+    r1, r2 = orc.uniform((N, N), 113), orc.uniform((N, N), 114)
+    sa, sb = (r1 + r1.T) / 2, (r2 + r2.T) / 2
+    run(L.mi_symmetric_matmul_f32, d((sa)), d((sb)), vp(C2), N)
+    assert_close(orc, to_host(C2), orc.gemm(sa, sb), N, what="symmetric")
+
+    lo_a, lo_b = np.tril(r1), np.tril(r2)
+    run(L.mi_lower_tri_mul_f32, d((lo_a)), d((lo_b)), vp(C2), N)
+    assert_close(orc, to_host(C2), orc.gemm(lo_a, lo_b, orc.LOWER), N, what="lower")
+    up_a, up_b = np.triu(r1), np.triu(r2)
+    run(L.mi_upper_tri_matmul_f32, d((up_a)), d((up_b)), vp(C2), N)
+    assert_close(orc, to_host(C2), orc.gemm(up_a, up_b, orc.UPPER), N, what="upper")
+
+    Ml, Kl, Nl = 64, 100000, 48
+    al, bl = orc.uniform((Ml, Kl), 115), orc.uniform((Kl, Nl), 116)
+    nws = L.mi_matmul_large_k_workspace_bytes(Ml, Kl, Nl)
+    ws = torch.empty(max(nws, 1), dtype=torch.uint8, device="cuda")
+    Cl = torch.empty((Ml, Nl), device="cuda")
+    run(L.mi_matmul_large_k_f32, d((al)), d((bl)), vp(Cl), Ml, Kl, Nl, vp(ws), nws)
+    assert_close(orc, to_host(Cl), orc.gemm(al, bl), Kl, what="large_k")
+
+
+def test_zero_sizes(ck, dev):
+    L = ck.abi.lib()
+    s = cur_stream()
+    C = torch.full((4, 5), 3.0, device="cuda")
+    A = torch.ones((4, 0), device="cuda")
+    B = torch.ones((0, 5), device="cuda")
+    ck.abi.check(L.mi_matmul_f32(vp(A), vp(B), vp(C), 4, 0, 5, s))
+    assert torch.all(C == 0)
+    for M, N in [(0, 5), (4, 0)]:
+        assert L.mi_matmul_f32(None, None, None, M, 3, N, s) == 0
+
+
+@pytest.mark.parametrize("cfg", [1, 2, 3])
+def test_repeatability_bitwise(ck, orc, dev, cfg):
+    M, N, K = 512, 384, 1536
+    A, B = dev_uniform(ck, (M, K), 121), dev_uniform(ck, (K, N), 122)
+    first = None
+    for _ in range(20):
+        C = torch.empty((M, N), device="cuda")
+        ck.abi.check(run_gemm(ck, gemm_args(ck, A, B, C, M, N, K, override=cfg)))
+        h = to_host(C)
+        if first is None:
+            first = h
+        else:
+            np.testing.assert_array_equal(h, first)
