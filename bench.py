@@ -1,0 +1,228 @@
+"""Benchmark of the GEMM-family hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--mode full|gemm|gemv|copy]
+
+One step = the BASELINE configs[1] workload: an fp32 8192^3 GEMM in each of the
+four operand layouts (A.B, A^T.B, A.B^T, A^T.B^T), run through the drop-in
+operators of reference PIDs 1, 16, 17 and 18 on synthetic uniform[-1, 1)
+inputs already resident in HBM.  ``value`` is the step's aggregate fp32
+TFLOP/s.  The line also carries:
+  * ``roofline``: the NN contraction kernel's algorithmic flops per launch
+    over its average duration, measured with HIP events on the launch stream
+    inside the timed region, against the 157.3 TFLOP/s fp32 MFMA peak;
+    ``traffic`` is read from the rocprofv3 PMC summary in profiles/ when present;
+  * ``gemv``: the BASELINE GEMV (A 32768 x 65536) in GB/s against 8 TB/s HBM;
+  * ``cpu_baseline``: host fp32 torch.matmul (the CPU operator the reference's
+    kernels replace) on the same 8192^3 problem, timed on this host's cores.
+Only one GPU is supported: --gpus N with N > 1 exits with a message.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+METRIC = "fp32 TFLOP/s (% MFMA peak) @8192³ GEMM; GB/s (% HBM peak) on GEMV"
+PEAK_TFLOPS = 157.3   # MI355X dense fp32 MFMA
+PEAK_HBM_GBS = 8000.0  # MI355X HBM3E
+N = 8192
+GEMV_M, GEMV_K = 32768, 65536
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "gemm_f32_nn_8192_traffic.txt")
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=10)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--mode", choices=["full", "gemm", "gemv", "copy"], default="full",
+                   help="profiling variants: only the GEMM, only the GEMV, or a plain "
+                        "1 GiB device copy (PMC calibration)")
+    return p.parse_args()
+
+
+def read_traffic():
+    """HBM bytes per NN 8192^3 launch from the committed PMC summary, or None."""
+    try:
+        txt = open(TRAFFIC_FILE).read()
+    except OSError:
+        return None
+    m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", txt, re.M)
+    return float(m.group(1)) if m else None
+
+
+def main() -> int:
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
+              "the GEMM-family path has no multi-GPU leg here.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    sys.path.insert(0, REPO)
+    import __graft_entry__
+
+    ck = __graft_entry__.load_package()
+    L = ck.abi.lib()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream()
+
+    def fill(t, seed):
+        import ctypes
+        ck.abi.check(L.mi_fill_uniform_f32(ctypes.c_void_p(t.data_ptr()), t.numel(), seed, 0,
+                                           ctypes.c_void_p(stream.cuda_stream)), "fill")
+        return t
+
+    if args.mode == "copy":
+        src = torch.empty(1 << 28, device=dev)
+        dst = torch.empty_like(src)
+        fill(src, 5)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("copy: 1 GiB read + 1 GiB write x3")
+        return 0
+
+    out = {}
+    if args.mode in ("full", "gemm"):
+        # BASELINE seeds: 16 * cfg_index + tensor_index, configs[1] -> 16 (A), 17 (B)
+        A = fill(torch.empty((N, N), device=dev), 16)
+        B = fill(torch.empty((N, N), device=dev), 17)
+        layouts = [("NN", ck.p01.matmul_cuda), ("TN", ck.p16.matmul_transposed_cuda),
+                   ("NT", ck.p17.matmul_cuda), ("TT", ck.p18.matmul_transposed_cuda)]
+        for _ in range(args.warmup):
+            for _, fn in layouts:
+                fn(A, B)
+        torch.cuda.synchronize()
+        n_ev = args.steps * len(layouts) + 1
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(n_ev)]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        evs[0].record(stream)
+        i = 1
+        for _ in range(args.steps):
+            for _, fn in layouts:
+                fn(A, B)
+                evs[i].record(stream)
+                i += 1
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        per = [[] for _ in layouts]
+        for s in range(args.steps):
+            for j in range(len(layouts)):
+                k = 1 + s * len(layouts) + j
+                per[j].append(evs[k - 1].elapsed_time(evs[k]))
+        step_ms = evs[0].elapsed_time(evs[-1]) / args.steps
+        flops = 2.0 * N ** 3
+        out["gemm"] = {
+            "step_ms": step_ms,
+            "wall_ms_per_step": wall * 1e3 / args.steps,
+            "tflops": len(layouts) * flops / (step_ms * 1e-3) / 1e12,
+            "per_layout_ms": {name: sum(v) / len(v) for (name, _), v in zip(layouts, per)},
+        }
+        out["gemm"]["per_layout_tflops"] = {
+            k: flops / (v * 1e-3) / 1e12 for k, v in out["gemm"]["per_layout_ms"].items()}
+        nn_ms = out["gemm"]["per_layout_ms"]["NN"]
+        out["roofline"] = {
+            "bound": "mfma",
+            "kernel": "mi::gemm_f32_kernel<Tile<256,256,128,64>, NN, vec4, dense>",
+            "achieved": flops / (nn_ms * 1e-3) / 1e12,
+            "peak": PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": flops / (nn_ms * 1e-3) / 1e12 / PEAK_TFLOPS,
+            "traffic": read_traffic(),
+            "algorithmic_flops_per_launch": flops,
+            "avg_launch_ms": nn_ms,
+        }
+        log(f"gemm 8192^3: step {step_ms:.3f} ms, {out['gemm']['tflops']:.1f} TFLOP/s "
+            f"{out['gemm']['per_layout_tflops']}")
+        del A, B
+        torch.cuda.empty_cache()
+
+    if args.mode in ("full", "gemv"):
+        import ctypes
+        A = fill(torch.empty((GEMV_M, GEMV_K), device=dev), 48)   # configs[3] -> 48 (A)
+        x = fill(torch.empty((GEMV_K, 1), device=dev), 50)        # x -> 50
+        for _ in range(max(args.warmup, 1)):
+            ck.p04.gemv_cuda(A, x)
+        torch.cuda.synchronize()
+        reps = max(args.steps, 5)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            ck.p04.gemv_cuda(A, x)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        nbytes = (GEMV_M * GEMV_K + GEMV_K + GEMV_M) * 4
+        out["gemv"] = {"shape": [GEMV_M, GEMV_K], "ms": ms, "gbps": nbytes / (ms * 1e-3) / 1e9,
+                       "frac": nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+                       "algorithmic_bytes": nbytes}
+        log(f"gemv {GEMV_M}x{GEMV_K}: {ms:.3f} ms, {out['gemv']['gbps']:.0f} GB/s")
+        del A, x
+        torch.cuda.empty_cache()
+
+    if args.mode != "full":
+        return 0
+
+    cpu = None
+    if not args.no_cpu:
+        threads = os.cpu_count() or 1
+        torch.set_num_threads(threads)
+        a = torch.rand((N, N)) * 2 - 1
+        b = torch.rand((N, N)) * 2 - 1
+        torch.matmul(a[:512], b)  # warm the BLAS thread pool
+        best = float("inf")
+        for _ in range(2):
+            t = time.perf_counter()
+            torch.matmul(a, b)
+            best = min(best, time.perf_counter() - t)
+        cpu = {"value": 2.0 * N ** 3 / best / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+               "kind": "reference",
+               "sample": f"host fp32 torch.matmul 8192^3 NN (the CPU operator the reference's "
+                         f"kernels replace), best of 2 after a warm-up, {best * 1e3:.0f} ms; "
+                         f"torch {torch.__version__}"}
+        log(f"cpu baseline: {cpu['value']:.3f} TFLOP/s on {cpu['cores']} threads")
+
+    g = out["gemm"]
+    line = {
+        "metric": METRIC,
+        "value": round(g["tflops"], 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(g["step_ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "fp32 GEMM M=N=K=8192 in layouts NN, TN, NT, TT "
+                               "(BASELINE configs[1]); one step = one GEMM per layout",
+                   "M": N, "N": N, "K": N, "layouts": ["NN", "TN", "NT", "TT"],
+                   "inputs": "uniform[-1,1) splitmix64 seeds 16/17, resident in HBM"},
+        "frac_of_peak": round(g["tflops"] / PEAK_TFLOPS, 4),
+        "per_layout_tflops": {k: round(v, 2) for k, v in g["per_layout_tflops"].items()},
+        "roofline": out["roofline"],
+        "gemv": out.get("gemv"),
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -60,6 +60,9 @@ SIGNATURES = {
     "mi_gemm_f32": (ctypes.c_int, [ctypes.POINTER(GemmArgs), _vp]),
     "mi_gemm_workspace_bytes": (_sz, [ctypes.POINTER(GemmArgs)]),
     "mi_gemm_plan": (ctypes.c_int, [ctypes.POINTER(GemmArgs), ctypes.c_int32, ctypes.POINTER(Plan)]),
+    "mi_gemm_tile_of": (ctypes.c_int, [ctypes.POINTER(GemmArgs), ctypes.c_int32, _i64, ctypes.c_int32,
+                                       ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32),
+                                       ctypes.POINTER(_i64), ctypes.POINTER(_i64)]),
     "mi_square_matmul_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _vp]),
     "mi_matmul_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "mi_batched_matmul_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
@@ -114,9 +117,9 @@ def check(status: int, where: str = "") -> None:
         raise MiError(status, where)
 
 
-def plan(M, N, K, batch=1, op_a=MI_OP_N, op_b=MI_OP_N, structure=MI_DENSE, num_cus=256,
-         workspace_bytes=0, plan_override=0, lda=None, ldb=None, ldc=None):
-    """Host-only scheduler query (mi_gemm_plan); no device needed."""
+def make_args(M, N, K, batch=1, op_a=MI_OP_N, op_b=MI_OP_N, structure=MI_DENSE,
+              workspace_bytes=0, plan_override=0, lda=None, ldb=None, ldc=None):
+    """An mi_gemm_args with no pointers (for the host-only queries)."""
     a = GemmArgs()
     a.M, a.N, a.K, a.batch = M, N, K, batch
     a.op_a, a.op_b, a.structure = op_a, op_b, structure
@@ -125,6 +128,21 @@ def plan(M, N, K, batch=1, op_a=MI_OP_N, op_b=MI_OP_N, structure=MI_DENSE, num_c
     a.ldc = ldc if ldc is not None else N
     a.workspace_bytes = workspace_bytes
     a.plan_override = plan_override
+    return a
+
+
+def plan(M, N, K, num_cus=256, **kw):
+    """Host-only scheduler query (mi_gemm_plan); no device needed."""
+    a = make_args(M, N, K, **kw)
     p = Plan()
     rc = lib().mi_gemm_plan(ctypes.byref(a), num_cus, ctypes.byref(p))
     return rc, p
+
+
+def tile_of(args, wg, split=0, num_cus=256):
+    """(status, tile_m, tile_n, k_begin, k_end) for workgroup wg (mi_gemm_tile_of)."""
+    tm, tn = ctypes.c_int32(), ctypes.c_int32()
+    kb, ke = _i64(), _i64()
+    rc = lib().mi_gemm_tile_of(ctypes.byref(args), num_cus, wg, split, ctypes.byref(tm),
+                               ctypes.byref(tn), ctypes.byref(kb), ctypes.byref(ke))
+    return rc, tm.value, tn.value, kb.value, ke.value

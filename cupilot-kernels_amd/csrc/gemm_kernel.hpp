@@ -152,56 +152,32 @@ struct TileLoader {
     }
 };
 
-// Which output tile this workgroup owns and which K range it reduces.
-// Returns false for a triangular off-structure tile (written with zeros).
-template <class T, int MODE>
-__device__ __forceinline__ bool tile_of(const GemmParams& p, int& tm, int& tn, int& k_begin,
-                                        int& k_end) {
-    const int pid = xcd_remap(blockIdx.x, gridDim.x);
+// Which output tile workgroup `bid` (of `nblocks`) owns and which K range
+// [k_begin, k_end) it reduces for split `split`.  Returns false for a
+// triangular off-structure tile (written with zeros).  Shared by the kernel
+// and the host introspection entry point mi_gemm_tile_of.
+template <int BM, int BN, int MODE>
+__host__ __device__ __forceinline__ bool tile_of(const GemmParams& p, int bid, int nblocks, int split,
+                                                 int& tm, int& tn, int& k_begin, int& k_end) {
     if (MODE == kDense) {
+        const int pid = xcd_remap(bid, nblocks);
         raster(pid, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
-        k_begin = blockIdx.y * p.k_chunk;
-        k_end = min(p.K, k_begin + p.k_chunk);
+        k_begin = split * p.k_chunk;
+        k_end = p.K < k_begin + p.k_chunk ? p.K : k_begin + p.k_chunk;
         return true;
     }
-    const int nt = p.tiles_m;  // square tiling
-    const int ncomp = nt * (nt + 1) / 2;
-    if (pid < ncomp) {
-        // Longest K ranges first: diagonal distance d = nt-1 down to 0; the
-        // distance-d band holds nt-d tiles, each reducing (d+1) tiles of K.
-        int rem = pid, d = nt - 1;
-        while (rem >= nt - d) {
-            rem -= nt - d;
-            --d;
-        }
-        if (MODE == kLower) {
-            tm = rem + d;
-            tn = rem;
-            k_begin = tn * T::BN;
-            k_end = min(p.K, (tm + 1) * T::BM);
-        } else {
-            tm = rem;
-            tn = rem + d;
-            k_begin = tm * T::BM;
-            k_end = min(p.K, (tn + 1) * T::BN);
-        }
-        return true;
+    // Triangular tiles differ in length, so they keep the hardware's
+    // round-robin XCD order: every XCD then draws from the whole longest-first
+    // list instead of one XCD receiving all the longest tiles.
+    const bool lower = MODE == kLower;
+    if (!tri_tile(bid, p.tiles_m, lower, tm, tn)) {
+        k_begin = k_end = 0;
+        return false;
     }
-    // Off-structure tiles, row by row: for LOWER the strictly upper tiles.
-    int z = pid - ncomp, r = 0;
-    while (z >= nt - 1 - r) {
-        z -= nt - 1 - r;
-        ++r;
-    }
-    if (MODE == kLower) {
-        tm = r;
-        tn = r + 1 + z;
-    } else {
-        tm = r + 1 + z;
-        tn = r;
-    }
-    k_begin = k_end = 0;
-    return false;
+    const int hi = lower ? (tm + 1) * BM : (tn + 1) * BN;
+    k_begin = lower ? tn * BN : tm * BM;
+    k_end = p.K < hi ? p.K : hi;
+    return true;
 }
 
 template <class T, bool AT, bool BT, int VEC, int MODE>
@@ -220,7 +196,8 @@ __global__ void __launch_bounds__(T::NT) gemm_f32_kernel(const GemmParams p) {
     const int wn = wave % T::WAVES_N;
 
     int tm, tn, k_begin, k_end;
-    const bool compute = tile_of<T, MODE>(p, tm, tn, k_begin, k_end);
+    const bool compute =
+        tile_of<T::BM, T::BN, MODE>(p, blockIdx.x, gridDim.x, blockIdx.y, tm, tn, k_begin, k_end);
     const int m0 = tm * T::BM, n0 = tn * T::BN;
     const int batch = blockIdx.z;
 

