@@ -44,9 +44,10 @@ def parse_args():
     p.add_argument("--steps", type=int, default=10)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    p.add_argument("--mode", choices=["full", "gemm", "gemv", "copy"], default="full",
-                   help="profiling variants: only the GEMM, only the GEMV, or a plain "
-                        "1 GiB device copy (PMC calibration)")
+    p.add_argument("--mode", choices=["full", "gemm", "gemv", "configs", "copy"], default="full",
+                   help="profiling variants: only the GEMM, only the GEMV, only the per-config "
+                        "table, or a plain 1 GiB device copy (PMC calibration)")
+    p.add_argument("--no-configs", action="store_true", help="skip the per-config table")
     return p.parse_args()
 
 
@@ -58,6 +59,84 @@ def read_traffic():
         return None
     m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", txt, re.M)
     return float(m.group(1)) if m else None
+
+
+def _time(fn, stream, reps, warm):
+    import torch
+    for _ in range(warm):
+        fn(0)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(reps):
+        fn(i + 1)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def run_configs(ck, fill, dev, stream):
+    """Every other BASELINE config at full size, through its operator: ms per
+    call and throughput in the config's unit (algorithmic flops or bytes)."""
+    import torch
+    res = {}
+
+    def rec(name, ms, flops=None, nbytes=None):
+        r = {"ms": round(ms, 4)}
+        if flops is not None:
+            r["tflops"] = round(flops / (ms * 1e-3) / 1e12, 2)
+            r["frac_mfma"] = round(r["tflops"] / PEAK_TFLOPS, 4)
+        if nbytes is not None:
+            r["gbps"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+            r["frac_hbm"] = round(r["gbps"] / PEAK_HBM_GBS, 4)
+        res[name] = r
+        log(f"config {name}: {r}")
+
+    def u(shape, seed):
+        return fill(torch.empty(shape, device=dev), seed)
+
+    A, B = u((1024, 1024), 0), u((1024, 1024), 1)
+    rec("cfg0_nn_1024", _time(lambda i: ck.p01.matmul_cuda(A, B), stream, 20, 3), 2 * 1024 ** 3)
+    A, B = u((128, 512, 1024), 32), u((128, 1024, 768), 33)
+    rec("batched_128x512x1024x768", _time(lambda i: ck.p03.batched_matmul_cuda(A, B), stream, 10, 2),
+        2 * 128 * 512 * 1024 * 768)
+    A, B = u((16, 1024, 2048), 34), u((2048, 768), 35)
+    rec("tensor3d_16x1024x2048x768", _time(lambda i: ck.p10.batched_matmul_cuda(A, B), stream, 10, 2),
+        2 * 16 * 1024 * 2048 * 768)
+    A, B = u((8, 64, 128, 256), 36), u((256, 512), 37)
+    rec("tensor4d_8x64x128x256x512", _time(lambda i: ck.p11.tensor_matmul_cuda(A, B), stream, 10, 2),
+        2 * 65536 * 256 * 512)
+    A, B = u((16384, 32), 51), u((32, 16384), 52)
+    rec("small_k_16384x16384x32", _time(lambda i: ck.p07.gemm_cuda(A, B), stream, 10, 2),
+        2 * 16384 * 16384 * 32, 4 * (2 * 16384 * 32 + 16384 * 16384))
+    # diag: two input/output sets (1 GiB in all) alternate so the 256 MB MALL
+    # cannot serve a repeat from cache
+    a2 = [u((8192,), 53), u((8192,), 55)]
+    B2 = [u((8192, 8192), 54), u((8192, 8192), 56)]
+    rec("diag_8192", _time(lambda i: ck.p12.diag_mult_cuda(a2[i % 2], B2[i % 2]), stream, 20, 4),
+        None, 4 * (8192 + 2 * 8192 * 8192))
+    del a2, B2
+    A, B = u((256, 1 << 20), 64), u((1 << 20, 256), 65)
+    rec("large_k_256x256x1048576", _time(lambda i: ck.p06.matmul_cuda(A, B), stream, 10, 2),
+        2 * 256 * 256 * (1 << 20))
+    del A, B
+    A, B = u((65536, 64), 66), u((64, 65536), 67)
+    rec("tall_skinny_65536x64", _time(lambda i: ck.p09.tall_skinny_matmul_cuda(A, B), stream, 5, 1),
+        2 * 65536 * 65536 * 64, 4 * (2 * 65536 * 64 + 65536 * 65536))
+    torch.cuda.empty_cache()
+    n = 8192
+    tri_flops = n * (n + 1) * (n + 2) / 3
+    A, B = torch.tril(u((n, n), 68)), torch.tril(u((n, n), 69))
+    rec("lower_tri_8192", _time(lambda i: ck.p15.lower_tri_mul_cuda(A, B), stream, 10, 2), tri_flops)
+    A, B = torch.triu(u((n, n), 68)), torch.triu(u((n, n), 69))
+    rec("upper_tri_8192", _time(lambda i: ck.p14.upper_tri_matmul_cuda(A, B), stream, 10, 2), tri_flops)
+    R1, R2 = u((n, n), 70), u((n, n), 71)
+    A, B = (R1 + R1.t()) / 2, (R2 + R2.t()) / 2
+    del R1, R2
+    rec("symmetric_8192", _time(lambda i: ck.p13.symmetric_matmul_cuda(A, B), stream, 10, 2), 2 * n ** 3)
+    del A, B
+    torch.cuda.empty_cache()
+    return res
 
 
 def main() -> int:
@@ -155,10 +234,11 @@ def main() -> int:
         import ctypes
         A = fill(torch.empty((GEMV_M, GEMV_K), device=dev), 48)   # configs[3] -> 48 (A)
         x = fill(torch.empty((GEMV_K, 1), device=dev), 50)        # x -> 50
-        for _ in range(max(args.warmup, 1)):
+        # the first passes over a fresh 8 GiB operand run slower (page warm-up)
+        for _ in range(max(args.warmup, 10)):
             ck.p04.gemv_cuda(A, x)
         torch.cuda.synchronize()
-        reps = max(args.steps, 5)
+        reps = max(args.steps, 20)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
         for _ in range(reps):
@@ -173,6 +253,9 @@ def main() -> int:
         log(f"gemv {GEMV_M}x{GEMV_K}: {ms:.3f} ms, {out['gemv']['gbps']:.0f} GB/s")
         del A, x
         torch.cuda.empty_cache()
+
+    if args.mode in ("full", "configs") and not args.no_configs:
+        out["configs"] = run_configs(ck, fill, dev, stream)
 
     if args.mode != "full":
         return 0
@@ -218,6 +301,7 @@ def main() -> int:
         "per_layout_tflops": {k: round(v, 2) for k, v in g["per_layout_tflops"].items()},
         "roofline": out["roofline"],
         "gemv": out.get("gemv"),
+        "configs": out.get("configs"),
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
