@@ -25,7 +25,7 @@ MI_ERR_NO_DEVICE = -7
 
 MI_OP_N, MI_OP_T = 0, 1
 MI_DENSE, MI_LOWER, MI_UPPER = 0, 1, 2
-CFG64, CFG128, CFG256 = 1, 2, 3
+CFG64, CFG128, CFG256, CFG128K32, CFG128K64, CFG_PANEL32, CFG_PANEL64 = 1, 2, 3, 4, 5, 6, 7
 
 _i64 = ctypes.c_int64
 _vp = ctypes.c_void_p
@@ -51,7 +51,7 @@ class Plan(ctypes.Structure):
         ("plan_id", ctypes.c_int32), ("block_m", ctypes.c_int32), ("block_n", ctypes.c_int32),
         ("block_k", ctypes.c_int32), ("tiles_m", ctypes.c_int32), ("tiles_n", ctypes.c_int32),
         ("split_k", ctypes.c_int32), ("k_chunk", _i64), ("group_m", ctypes.c_int32),
-        ("grid", _i64), ("workspace_bytes", _sz),
+        ("num_tiles", _i64), ("grid", _i64), ("workspace_bytes", _sz),
     ]
 
 
@@ -140,7 +140,7 @@ def plan(M, N, K, num_cus=256, **kw):
 
 
 def tile_of(args, wg, split=0, num_cus=256):
-    """(status, tile_m, tile_n, k_begin, k_end) for workgroup wg (mi_gemm_tile_of)."""
+    """(status, tile_m, tile_n, k_begin, k_end) of work item wg (mi_gemm_tile_of)."""
     tm, tn = ctypes.c_int32(), ctypes.c_int32()
     kb, ke = _i64(), _i64()
     rc = lib().mi_gemm_tile_of(ctypes.byref(args), num_cus, wg, split, ctypes.byref(tm),

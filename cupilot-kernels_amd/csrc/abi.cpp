@@ -93,25 +93,35 @@ int mi_gemm_plan(const mi_gemm_args* args, int32_t num_cus, mi_plan* out) {
     return plan_gemm(*args, num_cus, *out, nullptr);
 }
 
-int mi_gemm_tile_of(const mi_gemm_args* args, int32_t num_cus, int64_t wg, int32_t split,
+int mi_gemm_tile_of(const mi_gemm_args* args, int32_t num_cus, int64_t item, int32_t split,
                     int32_t* tile_m, int32_t* tile_n, int64_t* k_begin, int64_t* k_end) {
     if (!args || !tile_m || !tile_n || !k_begin || !k_end) return MI_ERR_NULL_POINTER;
     mi_plan p{};
     GemmLaunch g{};
     const int rc = plan_gemm(*args, num_cus, p, &g);
     if (rc != MI_OK) return rc;
-    if (wg < 0 || wg >= g.grid_x || split < 0 || split >= g.split_k) return MI_ERR_BAD_SIZE;
+    if (item < 0 || item >= g.num_tiles || split < 0 || split >= g.split_k) return MI_ERR_BAD_SIZE;
     const GemmParams kp = make_params(g);
     int tm = 0, tn = 0, kb = 0, ke = 0;
     bool compute;
-    const int bid = (int)wg, nb = g.grid_x;
+    if (is_panel_cfg(g.cfg)) {
+        // panel kernel: tile item = row-major (tm, tn); every tile reduces all of K
+        *tile_m = (int32_t)(item / g.tiles_n);
+        *tile_n = (int32_t)(item % g.tiles_n);
+        *k_begin = 0;
+        *k_end = g.K;
+        return 1;
+    }
+    const int bid = (int)item, nb = g.num_tiles;
 #define MI_TILE_OF(BMN)                                                                        \
     (g.structure == kLower  ? tile_of<BMN, BMN, kLower>(kp, bid, nb, split, tm, tn, kb, ke)  \
      : g.structure == kUpper ? tile_of<BMN, BMN, kUpper>(kp, bid, nb, split, tm, tn, kb, ke) \
                              : tile_of<BMN, BMN, kDense>(kp, bid, nb, split, tm, tn, kb, ke))
     switch (g.cfg) {
         case kCfg64: compute = MI_TILE_OF(64); break;
-        case kCfg128: compute = MI_TILE_OF(128); break;
+        case kCfg128:
+        case kCfg128K32:
+        case kCfg128K64: compute = MI_TILE_OF(128); break;
         default: compute = MI_TILE_OF(256); break;
     }
 #undef MI_TILE_OF

@@ -33,17 +33,25 @@
 
 namespace mi {
 
-template <int BM_, int BN_, int WM_, int WN_>
+template <int BM_, int BN_, int WM_, int WN_, int BK_, int WAVES_PER_SIMD_, int STAGES_ = 2>
 struct Tile {
-    static constexpr int BM = BM_, BN = BN_, BK = 16, WM = WM_, WN = WN_;
+    static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
+    // LDS buffers per operand: 2 = double-buffered K loop; 1 = the whole K of
+    // a tile fits one slice (small-K configs), halving the LDS footprint.
+    static constexpr int STAGES = STAGES_;
+    // occupancy the build is held to, so the persistent grid (the scheduler's
+    // resident workgroups per CU) matches what the hardware can hold
+    static constexpr int WAVES_PER_SIMD = WAVES_PER_SIMD_;
     static constexpr int WAVES_M = BM / WM, WAVES_N = BN / WN;
     static constexpr int NW = WAVES_M * WAVES_N, NT = NW * 64;
     static constexpr int TM = WM / 32, TN = WN / 32;
 };
 
-using Tile64 = Tile<64, 64, 32, 32>;
-using Tile128 = Tile<128, 128, 64, 64>;
-using Tile256 = Tile<256, 256, 128, 64>;
+using Tile64 = Tile<64, 64, 32, 32, 16, 8>;      // 8 workgroups of 4 waves per CU
+using Tile128 = Tile<128, 128, 64, 64, 16, 3>;   // 3 workgroups of 4 waves per CU
+using Tile256 = Tile<256, 256, 128, 64, 32, 2>;  // 1 workgroup of 8 waves per CU
+using Tile128K32 = Tile<128, 128, 64, 64, 32, 3, 1>;  // K <= 32 in one slice, 3 WGs per CU
+using Tile128K64 = Tile<128, 128, 64, 64, 64, 2, 1>;  // K <= 64 in one slice, 2 WGs per CU
 
 enum { kDense = 0, kLower = 1, kUpper = 2 };
 
@@ -180,95 +188,89 @@ __host__ __device__ __forceinline__ bool tile_of(const GemmParams& p, int bid, i
     return true;
 }
 
+// One output tile's assignment, uniform across the workgroup.
+struct TileWork {
+    int tm, tn, k_begin, k_end, nk;
+    bool compute;
+};
+
+template <class T, int MODE>
+__device__ __forceinline__ TileWork decode_tile(const GemmParams& p, int tile) {
+    TileWork w;
+    w.compute = tile_of<T::BM, T::BN, MODE>(p, tile, p.num_tiles, blockIdx.y, w.tm, w.tn,
+                                            w.k_begin, w.k_end);
+    w.nk = w.compute && w.k_end > w.k_begin ? (w.k_end - w.k_begin + T::BK - 1) / T::BK : 0;
+    return w;
+}
+
+// Store one finished tile from its accumulators (zeros for a tile with no K
+// work).  Block (i, j) holds C^T: lane l owns row l%32 of the 32x32 block and
+// accumulator registers 4g..4g+3 its columns 8g + 4*(l/32) .. +3, so every
+// register group is one 16-byte store.  Triangular modes write +0.0 on the
+// wrong side of the diagonal.
+template <class T, int MODE>
+__device__ __forceinline__ void store_tile(const GemmParams& p, float* C, int64_t ldc, bool c_vec,
+                                           const TileWork& w, const f16v (&acc)[T::TM][T::TN],
+                                           bool zero, int wm, int wn, int lane) {
+    const int m0 = w.tm * T::BM, n0 = w.tn * T::BN;
+    const int half = lane >> 5;
+#pragma unroll
+    for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < T::TN; ++j)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int row = m0 + wm * T::WM + i * 32 + (lane & 31);
+                const int col = n0 + wn * T::WN + j * 32 + g * 8 + half * 4;
+                if (row >= p.M) continue;
+                f4 v;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float x = zero ? 0.f : acc[i][j][4 * g + e];
+                    if (MODE == kLower && col + e > row) x = 0.f;
+                    if (MODE == kUpper && col + e < row) x = 0.f;
+                    v[e] = x;
+                }
+                float* dst = C + (int64_t)row * ldc + col;
+                if (c_vec && col + 3 < p.N) {
+                    *reinterpret_cast<f4*>(dst) = v;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (col + e < p.N) dst[e] = v[e];
+                }
+            }
+}
+
+// Persistent over tiles (workgroup b owns tiles b, b + gridDim.x, ...) and
+// software-pipelined over the sequence of (tile, K slice): while the MFMAs of
+// one slice run, the global loads of the next slice -- of the same tile, or
+// the first slice of the next tile -- are in flight; they are written to the
+// other LDS buffer, and only then are a finished tile's stores issued.  vmcnt
+// counts in issue order and the stores sit behind data-dependent branches, so
+// any wait for a prefetch also waits for every store issued before it; with
+// this order those are the previous tile's stores, which have had at least a
+// slice of MFMAs to drain.
 template <class T, bool AT, bool BT, int VEC, int MODE>
-__global__ void __launch_bounds__(T::NT) gemm_f32_kernel(const GemmParams p) {
+__global__ void __launch_bounds__(T::NT)
+    __attribute__((amdgpu_waves_per_eu(T::WAVES_PER_SIMD, T::WAVES_PER_SIMD)))
+    gemm_f32_kernel(const GemmParams p) {
     constexpr bool A_KC = !AT;  // A row-major (M x K) is contiguous along K
     constexpr bool B_KC = BT;   // B stored N x K is contiguous along K
     using LA = TileLoader<T::BM, T::BK, T::NT, A_KC, VEC>;
     using LB = TileLoader<T::BN, T::BK, T::NT, B_KC, VEC>;
-    __shared__ __attribute__((aligned(16))) float sA[2][LA::ELEMS];
-    __shared__ __attribute__((aligned(16))) float sB[2][LB::ELEMS];
+    __shared__ __attribute__((aligned(16))) float sA[T::STAGES][LA::ELEMS];
+    __shared__ __attribute__((aligned(16))) float sB[T::STAGES][LB::ELEMS];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int wm = wave / T::WAVES_N;
     const int wn = wave % T::WAVES_N;
-
-    int tm, tn, k_begin, k_end;
-    const bool compute =
-        tile_of<T::BM, T::BN, MODE>(p, blockIdx.x, gridDim.x, blockIdx.y, tm, tn, k_begin, k_end);
-    const int m0 = tm * T::BM, n0 = tn * T::BN;
     const int batch = blockIdx.z;
-
-    if (!compute) {
-        float* C = p.C + (int64_t)batch * p.sc;
-        for (int e = tid; e < T::BM * T::BN; e += T::NT) {
-            const int row = m0 + e / T::BN, col = n0 + e % T::BN;
-            if (row < p.M && col < p.N) C[(int64_t)row * p.ldc + col] = 0.f;
-        }
-        return;
-    }
 
     const float* __restrict__ A = p.A + (int64_t)batch * p.sa;
     const float* __restrict__ B = p.B + (int64_t)batch * p.sb;
-
-    f16v acc[T::TM][T::TN];
-#pragma unroll
-    for (int i = 0; i < T::TM; ++i)
-#pragma unroll
-        for (int j = 0; j < T::TN; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-
-    const int nk = k_end > k_begin ? (k_end - k_begin + T::BK - 1) / T::BK : 0;
-    if (nk > 0) {
-        LA la;
-        LB lb;
-        la.load(A, p.lda, m0, p.M, k_begin, k_end, tid);
-        lb.load(B, p.ldb, n0, p.N, k_begin, k_end, tid);
-        la.template mask<MODE, true>(m0, k_begin, tid);
-        lb.template mask<MODE, false>(n0, k_begin, tid);
-        la.store(sA[0], tid);
-        lb.store(sB[0], tid);
-        __syncthreads();
-
-        for (int it = 0; it < nk; ++it) {
-            const int cur = it & 1;
-            const bool more = it + 1 < nk;
-            if (more) {
-                const int k0 = k_begin + (it + 1) * T::BK;
-                la.load(A, p.lda, m0, p.M, k0, k_end, tid);
-                lb.load(B, p.ldb, n0, p.N, k0, k_end, tid);
-                la.template mask<MODE, true>(m0, k0, tid);
-                lb.template mask<MODE, false>(n0, k0, tid);
-            }
-            const float* As = sA[cur];
-            const float* Bs = sB[cur];
-#pragma unroll
-            for (int kb = 0; kb < T::BK / 8; ++kb) {
-                float a[T::TM][4], b[T::TN][4];
-#pragma unroll
-                for (int i = 0; i < T::TM; ++i) LA::frag(As, wm * T::WM + i * 32, kb, lane, a[i]);
-#pragma unroll
-                for (int j = 0; j < T::TN; ++j) LB::frag(Bs, wn * T::WN + j * 32, kb, lane, b[j]);
-#pragma unroll
-                for (int s = 0; s < 4; ++s)
-#pragma unroll
-                    for (int i = 0; i < T::TM; ++i)
-#pragma unroll
-                        for (int j = 0; j < T::TN; ++j)
-                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s], b[j][s],
-                                                                             acc[i][j], 0, 0, 0);
-            }
-            if (more) {
-                la.store(sA[cur ^ 1], tid);
-                lb.store(sB[cur ^ 1], tid);
-            }
-            __syncthreads();
-        }
-    }
-
     float* C;
     int64_t ldc;
     if (p.split_k > 1) {
@@ -278,22 +280,115 @@ __global__ void __launch_bounds__(T::NT) gemm_f32_kernel(const GemmParams p) {
         C = p.C + (int64_t)batch * p.sc;
         ldc = p.ldc;
     }
-    const int half = lane >> 5;
+    // 16-byte output stores need every row start 16-byte aligned
+    const bool c_vec = (ldc % 4 == 0) && ((reinterpret_cast<uintptr_t>(C) & 15u) == 0);
+
+    f16v acc[T::TM][T::TN];
 #pragma unroll
     for (int i = 0; i < T::TM; ++i)
 #pragma unroll
         for (int j = 0; j < T::TN; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = m0 + wm * T::WM + i * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
-                const int col = n0 + wn * T::WN + j * 32 + (lane & 31);
-                if (row < p.M && col < p.N) {
-                    float v = acc[i][j][r];
-                    if (MODE == kLower && col > row) v = 0.f;
-                    if (MODE == kUpper && col < row) v = 0.f;
-                    C[(int64_t)row * ldc + col] = v;
-                }
-            }
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    // Next tile at or after t (stride gridDim.x) that has K work; tiles
+    // without any (triangular off-structure tiles) are written with zeros on
+    // the way.  Uniform across the workgroup.
+    auto next_work = [&](int& t, TileWork& w) -> bool {
+        while (t < p.num_tiles) {
+            w = decode_tile<T, MODE>(p, t);
+            if (w.nk > 0) return true;
+            store_tile<T, MODE>(p, C, ldc, c_vec, w, acc, true, wm, wn, lane);
+            t += gridDim.x;
+        }
+        return false;
+    };
+    auto load_slice = [&](LA& la, LB& lb, const TileWork& w, int it) {
+        const int k0 = w.k_begin + it * T::BK;
+        la.load(A, p.lda, w.tm * T::BM, p.M, k0, w.k_end, tid);
+        lb.load(B, p.ldb, w.tn * T::BN, p.N, k0, w.k_end, tid);
+        la.template mask<MODE, true>(w.tm * T::BM, k0, tid);
+        lb.template mask<MODE, false>(w.tn * T::BN, k0, tid);
+    };
+
+    // MFMAs of the slice in LDS buffer cb into acc
+    auto compute = [&](int cb) {
+        const float* As = sA[cb];
+        const float* Bs = sB[cb];
+#pragma unroll
+        for (int kb = 0; kb < T::BK / 8; ++kb) {
+            float a[T::TM][4], b[T::TN][4];
+#pragma unroll
+            for (int i = 0; i < T::TM; ++i) LA::frag(As, wm * T::WM + i * 32, kb, lane, a[i]);
+#pragma unroll
+            for (int j = 0; j < T::TN; ++j) LB::frag(Bs, wn * T::WN + j * 32, kb, lane, b[j]);
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < T::TN; ++j)
+                        // B fragment as the row operand: the 32x32 result is
+                        // the block of C^T (see store_tile)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(b[j][s], a[i][s],
+                                                                         acc[i][j], 0, 0, 0);
+        }
+    };
+
+    int t = blockIdx.x;
+    TileWork cur;
+    if (!next_work(t, cur)) return;
+
+    LA la;
+    LB lb;
+    load_slice(la, lb, cur, 0);
+    la.store(sA[0], tid);
+    lb.store(sB[0], tid);
+    __syncthreads();
+
+    int cb = 0;
+    for (;;) {
+        // Inner slices of the tile: the next slice is always this tile's, so
+        // the prefetch and its LDS write are unconditional and every load is
+        // awaited in the iteration that issued it.
+        for (int it = 0; it + 1 < cur.nk; ++it) {
+            load_slice(la, lb, cur, it + 1);
+            compute(cb);
+            if (T::STAGES == 1) __syncthreads();  // the one buffer is free only now
+            const int nb = T::STAGES == 2 ? (cb ^ 1) : 0;
+            la.store(sA[nb], tid);
+            lb.store(sB[nb], tid);
+            __syncthreads();
+            cb = nb;
+        }
+
+        // Last slice: prefetch the first slice of the next tile (or, after the
+        // last tile, re-read the current slice, never used), write it to LDS,
+        // and only then issue this tile's stores -- vmcnt counts in issue
+        // order, so a wait for the prefetch never covers fresh stores.
+        int nt = t + gridDim.x;
+        TileWork nw;
+        const bool has_next = next_work(nt, nw);
+        if (has_next) load_slice(la, lb, nw, 0);
+        else load_slice(la, lb, cur, cur.nk - 1);
+        compute(cb);
+        if (T::STAGES == 1) __syncthreads();
+        const int nb = T::STAGES == 2 ? (cb ^ 1) : 0;
+        la.store(sA[nb], tid);
+        lb.store(sB[nb], tid);
+        store_tile<T, MODE>(p, C, ldc, c_vec, cur, acc, false, wm, wn, lane);
+#pragma unroll
+        for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+            for (int j = 0; j < T::TN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+        __syncthreads();
+        if (!has_next) break;
+        t = nt;
+        cur = nw;
+        cb = nb;
+    }
 }
 
 inline GemmParams make_params(const GemmLaunch& g) {
@@ -316,6 +411,8 @@ inline GemmParams make_params(const GemmLaunch& g) {
     p.sa = g.sa;
     p.sb = g.sb;
     p.sc = g.sc;
+    p.num_tiles = g.num_tiles;
+    p.col_splits = g.col_splits;
     p.ws_batch_stride = (int64_t)g.M * g.N;
     p.ws_split_stride = p.ws_batch_stride * g.batch;
     return p;
@@ -325,6 +422,7 @@ template <class T, bool AT, bool BT, int VEC, int MODE>
 hipError_t launch_one(const GemmLaunch& g, hipStream_t s) {
     const GemmParams p = make_params(g);
     dim3 grid((unsigned)g.grid_x, (unsigned)g.split_k, (unsigned)g.batch);
+    // grid_x <= num_tiles workgroups walk the tile list (persistent)
     hipLaunchKernelGGL((gemm_f32_kernel<T, AT, BT, VEC, MODE>), grid, dim3(T::NT), 0, s, p);
     return hipGetLastError();
 }
@@ -351,6 +449,8 @@ hipError_t launch_layout(const GemmLaunch& g, hipStream_t s) {
         case kCfg64: return launch_cfg<Tile64, AT, BT>(g, s);
         case kCfg128: return launch_cfg<Tile128, AT, BT>(g, s);
         case kCfg256: return launch_cfg<Tile256, AT, BT>(g, s);
+        case kCfg128K32: return launch_cfg<Tile128K32, AT, BT>(g, s);
+        case kCfg128K64: return launch_cfg<Tile128K64, AT, BT>(g, s);
         default: return hipErrorInvalidValue;
     }
 }

@@ -1,7 +1,9 @@
 // gemm_nn.hip -- instantiations of the fp32 MFMA engine for op_a = n, op_b = n
 // (one translation unit per operand layout so they compile in parallel).
-#include "gemm_kernel.hpp"
+#include "gemm_panel.hpp"
 
 namespace mi {
-hipError_t launch_gemm_nn(const GemmLaunch& g, hipStream_t s) { return launch_layout<false, false>(g, s); }
+hipError_t launch_gemm_nn(const GemmLaunch& g, hipStream_t s) {
+    return is_panel_cfg(g.cfg) ? launch_panel<false, false>(g, s) : launch_layout<false, false>(g, s);
+}
 }  // namespace mi

@@ -1,0 +1,172 @@
+// gemm_panel.hpp -- fp32 MFMA contraction for small K (K <= KMAX = 32 or 64):
+// the store-bound shapes of the family (kernels/7_... small K, kernels/9_...
+// tall-skinny), where C is 32x-64x larger than A and B.
+//
+// With the whole K in one slice, the general engine re-reads an A tile and a B
+// tile for every output tile; at K = 64 and 128 x 128 tiles that is as many
+// bytes loaded (from L2/MALL) as stored, and the loads, not the MFMAs or the
+// stores, set the pace.  Here a workgroup instead owns one BM-row panel of A,
+// kept in LDS for its whole life, and walks a run of BN-wide column tiles:
+// per step it loads only the K x BN tile of B (double-buffered in LDS),
+// computes the BM x BN tile and stores it.  The next B tile's global loads run
+// under the current tile's MFMAs and are written to LDS before the current
+// tile's stores are issued: vmcnt counts in issue order, so the wait for those
+// loads covers only the previous tile's stores, which have drained behind a
+// whole tile of MFMAs.  Load traffic falls to ~K/BM of the output (1/4 at K = 64).
+#pragma once
+
+#include "gemm_kernel.hpp"
+
+namespace mi {
+
+template <int BM_, int BN_, int KMAX_>
+struct PanelTile {
+    static constexpr int BM = BM_, BN = BN_, KMAX = KMAX_;
+    static constexpr int WM = 64, WN = 64;  // wave tile: 2 x 2 MFMA blocks
+    static constexpr int WAVES_M = BM / WM, WAVES_N = BN / WN;
+    static constexpr int NW = WAVES_M * WAVES_N, NT = NW * 64;
+    static constexpr int TM = WM / 32, TN = WN / 32;
+};
+
+using Panel32 = PanelTile<256, 128, 32>;
+using Panel64 = PanelTile<256, 128, 64>;
+
+template <class T, bool AT, bool BT, int VEC>
+__global__ void __launch_bounds__(T::NT) gemm_f32_panel_kernel(const GemmParams p) {
+    constexpr bool A_KC = !AT;
+    constexpr bool B_KC = BT;
+    using LA = TileLoader<T::BM, T::KMAX, T::NT, A_KC, VEC>;
+    using LB = TileLoader<T::BN, T::KMAX, T::NT, B_KC, VEC>;
+    __shared__ __attribute__((aligned(16))) float sA[LA::ELEMS];
+    __shared__ __attribute__((aligned(16))) float sB[2][LB::ELEMS];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave / T::WAVES_N;
+    const int wn = wave % T::WAVES_N;
+    const int half = lane >> 5;
+    const int batch = blockIdx.z;
+    const int nkb = (p.K + 7) / 8;  // 8-deep k-blocks that hold data (the rest is zero fill)
+
+    const float* __restrict__ A = p.A + (int64_t)batch * p.sa;
+    const float* __restrict__ B = p.B + (int64_t)batch * p.sb;
+    float* C = p.C + (int64_t)batch * p.sc;
+    const bool c_vec = (p.ldc % 4 == 0) && ((reinterpret_cast<uintptr_t>(p.C) & 15u) == 0) &&
+                       (p.sc % 4 == 0);
+
+    const int items = p.tiles_m * p.col_splits;
+    LA la;
+    LB lb;
+    for (int w = blockIdx.x; w < items; w += gridDim.x) {
+        const int tm = w / p.col_splits;
+        const int cs = w - tm * p.col_splits;
+        const int tn_begin = (int)((int64_t)cs * p.tiles_n / p.col_splits);
+        const int tn_end = (int)((int64_t)(cs + 1) * p.tiles_n / p.col_splits);
+        const int m0 = tm * T::BM;
+
+        // Each item walks its column run starting at its own rotation, so the
+        // workgroups running together store to different columns: in lockstep
+        // from the same start they would hit addresses that differ only in the
+        // row, i.e. the same few HBM channels.
+        const int run = tn_end - tn_begin;
+        const int rot = run > 0 ? w % run : 0;
+        auto col_tile = [&](int step) {
+            const int q = step + rot;
+            return tn_begin + (q >= run ? q - run : q);
+        };
+
+        // every wave is past the previous item's last barrier: LDS is free
+        la.load(A, p.lda, m0, p.M, 0, p.K, tid);
+        la.store(sA, tid);
+        if (run > 0) {
+            lb.load(B, p.ldb, col_tile(0) * T::BN, p.N, 0, p.K, tid);
+            lb.store(sB[0], tid);
+        }
+        __syncthreads();
+
+        for (int step = 0; step < run; ++step) {
+            const int buf = step & 1;
+            const int tn = col_tile(step);
+            // unconditional prefetch (the last step re-reads its own tile, never
+            // used) so each load is awaited in the step that issued it
+            const int tn_next = col_tile(step + 1 < run ? step + 1 : step);
+            lb.load(B, p.ldb, tn_next * T::BN, p.N, 0, p.K, tid);
+
+            f16v acc[T::TM][T::TN];
+#pragma unroll
+            for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+                for (int j = 0; j < T::TN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+#pragma unroll
+            for (int kb = 0; kb < T::KMAX / 8; ++kb) {
+                if (kb < nkb) {
+                    float a[T::TM][4], b[T::TN][4];
+#pragma unroll
+                    for (int i = 0; i < T::TM; ++i) LA::frag(sA, wm * T::WM + i * 32, kb, lane, a[i]);
+#pragma unroll
+                    for (int j = 0; j < T::TN; ++j) LB::frag(sB[buf], wn * T::WN + j * 32, kb, lane, b[j]);
+#pragma unroll
+                    for (int s = 0; s < 4; ++s)
+#pragma unroll
+                        for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+                            for (int j = 0; j < T::TN; ++j)
+                                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(b[j][s], a[i][s],
+                                                                                 acc[i][j], 0, 0, 0);
+                }
+            }
+
+            // the next B tile goes to LDS before this tile's stores are issued
+            // (see the file comment: waits then never cover fresh stores)
+            lb.store(sB[buf ^ 1], tid);
+
+            // block (i, j) holds C^T: lane l owns row l%32, registers 4g..4g+3
+            // its columns 8g + 4*half .. +3
+            const int n0 = tn * T::BN;
+#pragma unroll
+            for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+                for (int j = 0; j < T::TN; ++j)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const int row = m0 + wm * T::WM + i * 32 + (lane & 31);
+                        const int col = n0 + wn * T::WN + j * 32 + g * 8 + half * 4;
+                        if (row >= p.M) continue;
+                        const f4 v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                                      acc[i][j][4 * g + 3]};
+                        float* dst = C + (int64_t)row * p.ldc + col;
+                        if (c_vec && col + 3 < p.N) {
+                            *reinterpret_cast<f4*>(dst) = v;
+                        } else {
+#pragma unroll
+                            for (int e = 0; e < 4; ++e)
+                                if (col + e < p.N) dst[e] = v[e];
+                        }
+                    }
+
+            __syncthreads();
+        }
+    }
+}
+
+template <class T, bool AT, bool BT, int VEC>
+hipError_t launch_panel_one(const GemmLaunch& g, hipStream_t s) {
+    const GemmParams p = make_params(g);
+    dim3 grid((unsigned)g.grid_x, 1u, (unsigned)g.batch);
+    hipLaunchKernelGGL((gemm_f32_panel_kernel<T, AT, BT, VEC>), grid, dim3(T::NT), 0, s, p);
+    return hipGetLastError();
+}
+
+template <bool AT, bool BT>
+hipError_t launch_panel(const GemmLaunch& g, hipStream_t s) {
+    if (g.cfg == kCfgPanel32)
+        return g.vec == 4 ? launch_panel_one<Panel32, AT, BT, 4>(g, s)
+                          : launch_panel_one<Panel32, AT, BT, 1>(g, s);
+    return g.vec == 4 ? launch_panel_one<Panel64, AT, BT, 4>(g, s)
+                      : launch_panel_one<Panel64, AT, BT, 1>(g, s);
+}
+
+}  // namespace mi

@@ -13,8 +13,16 @@ namespace mi {
 //   id  block (BM x BN)  waves  wave tile   LDS (double-buffered)
 //   1   64 x 64          4      32 x 32     ~20 KiB
 //   2   128 x 128        4      64 x 64     ~40 KiB
-//   3   256 x 256        8      128 x 64    ~80 KiB
-enum TileCfgId { kCfg64 = 1, kCfg128 = 2, kCfg256 = 3, kNumCfg = 4 };
+//   3   256 x 256        8      128 x 64    ~140 KiB (32-deep K slices)
+//   4   128 x 128        4      64 x 64     ~35 KiB, one 32-deep slice (K <= 32)
+//   5   128 x 128        4      64 x 64     ~68 KiB, one 64-deep slice (K <= 64)
+//   6   256 x 128 panel  8      64 x 64     A panel resident, K <= 32 (~71 KiB)
+//   7   256 x 128 panel  8      64 x 64     A panel resident, K <= 64 (~137 KiB)
+enum TileCfgId {
+    kCfg64 = 1, kCfg128 = 2, kCfg256 = 3, kCfg128K32 = 4, kCfg128K64 = 5,
+    kCfgPanel32 = 6, kCfgPanel64 = 7, kNumCfg = 8
+};
+inline bool is_panel_cfg(int id) { return id == kCfgPanel32 || id == kCfgPanel64; }
 
 struct CfgInfo {
     int bm, bn, bk, threads;
@@ -23,7 +31,11 @@ inline CfgInfo cfg_info(int id) {
     switch (id) {
         case kCfg64: return {64, 64, 16, 256};
         case kCfg128: return {128, 128, 16, 256};
-        case kCfg256: return {256, 256, 16, 512};
+        case kCfg256: return {256, 256, 32, 512};
+        case kCfg128K32: return {128, 128, 32, 256};
+        case kCfg128K64: return {128, 128, 64, 256};
+        case kCfgPanel32: return {256, 128, 32, 512};
+        case kCfgPanel64: return {256, 128, 64, 512};
         default: return {0, 0, 0, 0};
     }
 }
@@ -45,7 +57,9 @@ struct GemmLaunch {
     int k_chunk;
     int tiles_m, tiles_n;
     int group_m;
-    int grid_x;           // workgroups per (split, batch)
+    int num_tiles;        // output tiles per (split, batch): tiles_m*tiles_n, or tiles_m^2 (triangular)
+    int grid_x;           // workgroups per (split, batch), <= num_tiles; each walks its tiles
+    int col_splits;       // panel configs: column runs per A row panel
 };
 
 // Kernel-side parameter block (passed by value).
@@ -56,6 +70,8 @@ struct GemmParams {
     float* ws;
     int M, N, K;
     int tiles_m, tiles_n, group_m;
+    int num_tiles;
+    int col_splits;
     int k_chunk, split_k;
     int64_t lda, ldb, ldc;
     int64_t sa, sb, sc;

@@ -5,12 +5,16 @@
 // replaces the reference's per-kernel compile-time tilings and shape-specific
 // literals (e.g. kernels/2_...:16-18 and :129-132 hard-code 2048x8192x4096 and a
 // 4x108 persistent grid; kernels/6_...:147-188 splits K over 8 host streams)
-// with one cost model:
-//   rounds(c, s) = ceil(tiles(c) * s / (CUs * resident(c)))
-//   time(c, s)   = rounds * BM*BN*(K/s) * resident(c) / efficiency(c)
-//                  + split-K reduction traffic (s * batch * M * N * 4 B * 2 / HBM)
-// and picks the cheapest (tile config c, split s).  Triangular problems use a
-// square tiling with the compute tiles ordered longest-K first.
+// with one cost model over (tile config c, split s):
+//   t_mfma(c, s)  = ceil(tiles(c) * batch * s / CUs) * 2*BM*BN*(K/s) / (eff(c) * CU peak)
+//   t_store(s)    = output bytes (s partial copies when split) / sustained write bandwidth
+//   time(c, s)    = max(t_mfma, t_store) + (1 - overlap(c)) * min(t_mfma, t_store)
+//                   + split-K reduction traffic
+// and picks the cheapest.  eff and overlap are calibrated on MI355X: the
+// 256-tile runs one workgroup per CU, so its stores overlap its MFMAs only
+// through the next-tile prefetch; the smaller tiles keep 4-8 workgroups per
+// CU in flight.  Triangular problems use a square tiling with the compute
+// tiles ordered longest-K first.
 #include <algorithm>
 #include <cstdint>
 
@@ -23,23 +27,40 @@ namespace {
 
 struct CfgModel {
     int id;
-    double efficiency;  // sustained fraction of the CU's MFMA peak
-    int resident;       // workgroups resident per CU
+    double efficiency;  // sustained fraction of the CU's MFMA peak (measured)
+    double overlap;     // fraction of the shorter of MFMA / store time hidden
 };
 
-// efficiency / residency per tile config (gfx950: 4 SIMDs, 512 VGPRs/lane,
-// 160 KiB LDS per CU).  Efficiency ranks larger tiles higher because each
-// LDS fragment feeds more MFMAs and each HBM byte more flops.
+// Measured on MI355X (8192^3: 256-tile 85 %; 16384x768x2048: 128-tile 78 %,
+// 256-tile 62 % because 192 tiles leave CUs idle; 1024^3: 64-tile best).
+// The single-slice configs only apply when K fits their slice.
 constexpr CfgModel kModels[] = {
-    {kCfg256, 1.00, 1},
-    {kCfg128, 0.85, 2},
-    {kCfg64, 0.55, 4},
+    {kCfg256, 0.86, 0.7},
+    {kCfg128, 0.80, 0.8},
+    {kCfg64, 0.55, 0.8},
+    {kCfg128K32, 0.80, 0.95},
+    {kCfg128K64, 0.80, 0.95},
 };
 
 constexpr double kPeakFlopsPerCuNs = 256.0 * 2.4;  // fp32 MFMA flop per ns per CU
 constexpr double kHbmBytesPerNs = 8000.0;
+constexpr double kWriteBytesPerNs = 5500.0;        // sustained write-only bandwidth (measured)
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Workgroups of each config held on one CU at once; the kernels are built to
+// exactly this occupancy (amdgpu_waves_per_eu): 64-tile 8, 128-tile 3, 256-tile 1.
+int resident_wgs(int cfg) {
+    switch (cfg) {
+        case kCfg256: return 1;
+        case kCfg128: return 3;
+        case kCfg128K32: return 3;
+        case kCfg128K64: return 2;
+        case kCfgPanel32: return 2;
+        case kCfgPanel64: return 1;
+        default: return 8;
+    }
+}
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
@@ -86,34 +107,50 @@ int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
 
     int best_cfg = kCfg128, best_split = 1;
     const int override_cfg = a.plan_override & 0xF;
-    const int override_split = (a.plan_override >> 8) & 0xFFFF;
+    const int override_split = (a.plan_override >> 8) & 0xFFF;
+    const int override_group = (a.plan_override >> 20) & 0x7FF;
 
+    const bool override_ok =
+        override_cfg >= kCfg64 && override_cfg < kNumCfg &&
+        !((override_cfg == kCfg128K32 || override_cfg == kCfg128K64 || is_panel_cfg(override_cfg)) &&
+          a.K > cfg_info(override_cfg).bk) &&
+        !(is_panel_cfg(override_cfg) && a.structure != MI_DENSE);
     if (a.structure != MI_DENSE) {
         best_cfg = a.N > 2048 ? kCfg128 : kCfg64;
-        if (override_cfg >= kCfg64 && override_cfg <= kCfg256) best_cfg = override_cfg;
-    } else if (override_cfg >= kCfg64 && override_cfg <= kCfg256) {
+        if (override_ok) best_cfg = override_cfg;
+    } else if (override_ok) {
         best_cfg = override_cfg;
-        best_split = std::max(1, override_split);
+        best_split = is_panel_cfg(override_cfg) ? 1 : std::max(1, override_split);
+    } else if (a.K <= 64 && cdiv(a.M, 256) * cdiv(a.N, 128) * std::max<int64_t>(1, a.batch) >=
+                                2 * (int64_t)num_cus) {
+        // Small K and a large output: the A-panel kernel cuts operand reloads
+        // to ~K/256 of the output bytes (tall-skinny: 4 GiB instead of 16 GiB).
+        // Measured on MI355X the 64-deep panel is also the faster one at K = 32
+        // (16384^2 x 32: 0.304 ms against 0.433 ms for the 32-deep panel).
+        best_cfg = kCfgPanel64;
     } else {
         double best_t = 1e300;
         const int64_t batch = std::max<int64_t>(1, a.batch);
+        const double out_bytes = 4.0 * (double)batch * a.M * a.N;
         for (const CfgModel& m : kModels) {
             const CfgInfo ci = cfg_info(m.id);
+            if ((m.id == kCfg128K32 || m.id == kCfg128K64) && a.K > ci.bk) continue;
             const int64_t tiles = cdiv(a.M, ci.bm) * cdiv(a.N, ci.bn) * batch;
             for (int s = 1; s <= 1024; s *= 2) {
                 if (s > 1) {
                     // split only to fill the machine, with >= 1024 K per split
-                    if (tiles * (s / 2) >= (int64_t)num_cus * m.resident) break;
+                    if (tiles * (s / 2) >= (int64_t)num_cus) break;
                     if (a.K / s < 1024) break;
                     const size_t need = (size_t)s * batch * a.M * a.N * sizeof(float);
                     if (a.workspace_bytes < need) break;
                 }
-                const int64_t kc = cdiv(cdiv(a.K, s), ci.bk) * ci.bk;
-                const double rounds = (double)cdiv(tiles * s, (int64_t)num_cus * m.resident);
-                double t = rounds * (2.0 * ci.bm * ci.bn * (double)std::max<int64_t>(kc, ci.bk) *
-                                     m.resident) /
-                           (m.efficiency * kPeakFlopsPerCuNs);
-                if (s > 1) t += 2.0 * s * batch * (double)a.M * a.N * 4.0 / kHbmBytesPerNs;
+                const int64_t kc = cdiv(cdiv(std::max<int64_t>(a.K, 1), s), ci.bk) * ci.bk;
+                const double per_cu = (double)cdiv(tiles * s, (int64_t)num_cus);
+                const double t_mfma = per_cu * 2.0 * ci.bm * ci.bn * (double)kc /
+                                      (m.efficiency * kPeakFlopsPerCuNs);
+                const double t_store = out_bytes * s / kWriteBytesPerNs;
+                double t = std::max(t_mfma, t_store) + (1.0 - m.overlap) * std::min(t_mfma, t_store);
+                if (s > 1) t += 2.0 * s * out_bytes / kHbmBytesPerNs;
                 if (t < best_t * 0.999) {
                     best_t = t;
                     best_cfg = m.id;
@@ -130,8 +167,27 @@ int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
     // an override split larger than K allows collapses to what K can feed
     best_split = (int)std::min<int64_t>(best_split, cdiv(std::max<int64_t>(a.K, 1), k_chunk));
     if (best_split > 65535) return MI_ERR_BAD_SIZE;
-    int64_t grid = a.structure != MI_DENSE ? tiles_m * tiles_m : tiles_m * tiles_n;
-    if (grid > INT32_MAX) return MI_ERR_BAD_SIZE;
+    const int64_t num_tiles = a.structure != MI_DENSE ? tiles_m * tiles_m : tiles_m * tiles_n;
+    if (num_tiles > INT32_MAX) return MI_ERR_BAD_SIZE;
+    // Persistent grid: as many workgroups as the CUs hold at once (a multiple
+    // of the 8 XCDs so every workgroup keeps to one XCD), each walking the
+    // tile list with stride grid.
+    const int64_t batch = std::max<int64_t>(1, a.batch);
+    const int64_t slots = (int64_t)num_cus * resident_wgs(best_cfg);
+    int64_t grid = cdiv(slots, (int64_t)best_split * batch);
+    grid = cdiv(grid, 8) * 8;
+    grid = std::min(grid, num_tiles);
+    // Triangular tiles differ in length: one tile per workgroup, and the
+    // hardware's dispatch as slots free up balances them better than a
+    // static stride.
+    if (a.structure != MI_DENSE) grid = num_tiles;
+    // Panel configs: each work item is one A row panel times a run of column
+    // tiles; enough runs per panel to give every resident workgroup one.
+    int64_t col_splits = 1;
+    if (is_panel_cfg(best_cfg)) {
+        col_splits = std::min<int64_t>(tiles_n, std::max<int64_t>(1, cdiv(slots, tiles_m * batch)));
+        grid = std::min<int64_t>(tiles_m * col_splits, std::max<int64_t>(1, slots / batch));
+    }
 
     out.plan_id = best_cfg;
     out.block_m = ci.bm;
@@ -141,11 +197,12 @@ int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
     out.tiles_n = (int32_t)tiles_n;
     out.split_k = best_split;
     out.k_chunk = k_chunk;
-    out.group_m = (int32_t)std::min<int64_t>(tiles_m, 8);
+    out.group_m = (int32_t)std::min<int64_t>(tiles_m, override_group > 0 ? override_group : 8);
     if (out.group_m < 1) out.group_m = 1;
+    out.num_tiles = num_tiles;
     out.grid = grid;
     out.workspace_bytes =
-        best_split > 1 ? (size_t)best_split * std::max<int64_t>(1, a.batch) * a.M * a.N * sizeof(float) : 0;
+        best_split > 1 ? (size_t)best_split * batch * a.M * a.N * sizeof(float) : 0;
 
     if (launch) {
         GemmLaunch& g = *launch;
@@ -173,6 +230,8 @@ int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
         g.tiles_m = (int)tiles_m;
         g.tiles_n = (int)tiles_n;
         g.group_m = out.group_m;
+        g.num_tiles = (int)num_tiles;
+        g.col_splits = (int)col_splits;
         g.grid_x = (int)grid;
     }
     return MI_OK;

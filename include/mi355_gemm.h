@@ -74,7 +74,8 @@ typedef struct {
     int64_t stride_a, stride_b, stride_c;
     int32_t op_a, op_b;       /* mi_op */
     int32_t structure;        /* mi_structure; square, batch 1, N/N layouts */
-    int32_t plan_override;    /* 0 = scheduler's choice; else an mi_plan_id (tests, tuning) */
+    int32_t plan_override;    /* 0 = scheduler's choice; else (tests, tuning) bits 0-3 tile
+                                 config id, bits 8-19 split count, bits 20-30 raster group rows */
     void* workspace;
     size_t workspace_bytes;
 } mi_gemm_args;
@@ -87,7 +88,9 @@ typedef struct {
     int32_t split_k;        /* 1 = no split; else K is cut into split_k chunks */
     int64_t k_chunk;        /* elements of K per split (multiple of block_k) */
     int32_t group_m;        /* tile rows per raster group */
-    int64_t grid;           /* workgroups launched by the contraction kernel */
+    int64_t num_tiles;      /* output tiles per (split, batch) */
+    int64_t grid;           /* workgroups launched per (split, batch); each walks tiles
+                               wg, wg + grid, ... (persistent) */
     size_t workspace_bytes; /* split-K partial tiles */
 } mi_plan;
 
@@ -98,11 +101,12 @@ MI_API size_t mi_gemm_workspace_bytes(const mi_gemm_args* args);
 MI_API int mi_gemm_plan(const mi_gemm_args* args, int32_t num_cus, mi_plan* out);
 
 /* Scheduler introspection (no reference counterpart; for tests and tuning):
- * the output tile (tile_m, tile_n) and K range [k_begin, k_end) that workgroup
- * `wg` of split `split` reduces under the plan mi_gemm_f32 would use on a
- * device with num_cus compute units.  Returns 1 for a compute tile, 0 for a
+ * the output tile (tile_m, tile_n) and K range [k_begin, k_end) of work item
+ * `item` (0 <= item < mi_plan.num_tiles; workgroup w runs items w, w + grid,
+ * ...) of split `split` under the plan mi_gemm_f32 would use on a device with
+ * num_cus compute units.  Returns 1 for a compute tile, 0 for a
  * structural-zero tile (triangular products), a negative mi_status on error. */
-MI_API int mi_gemm_tile_of(const mi_gemm_args* args, int32_t num_cus, int64_t wg, int32_t split,
+MI_API int mi_gemm_tile_of(const mi_gemm_args* args, int32_t num_cus, int64_t item, int32_t split,
                            int32_t* tile_m, int32_t* tile_n, int64_t* k_begin, int64_t* k_end);
 
 /* ---- one entry point per reference operator ------------------------------ */

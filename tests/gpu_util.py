@@ -62,9 +62,10 @@ def run_gemm(ck, args) -> int:
 
 def workspace(ck, args):
     n = ck.abi.lib().mi_gemm_workspace_bytes(ctypes.byref(args))
-    if args.plan_override and (args.plan_override >> 8) > 1:
+    split = (args.plan_override >> 8) & 0xFFF
+    if split > 1:
         # an explicit split needs split * batch * M * N floats
-        n = max(n, (args.plan_override >> 8) * max(args.batch, 1) * args.M * args.N * 4)
+        n = max(n, split * max(args.batch, 1) * args.M * args.N * 4)
     return torch.empty(max(n, 1), dtype=torch.uint8, device="cuda") if n else None
 
 

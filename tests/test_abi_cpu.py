@@ -91,10 +91,16 @@ PLAN_CASES = [
 def test_plan_is_sane(ck, M, N, K, batch):
     rc, p = ck.abi.plan(M, N, K, batch=batch, workspace_bytes=1 << 40)
     assert rc == 0
-    assert p.block_m in (64, 128, 256) and p.block_m == p.block_n and p.block_k == 16
+    assert p.block_m in (64, 128, 256) and p.block_k in (16, 32, 64)
+    assert p.block_m == p.block_n or p.plan_id in (6, 7)
     assert p.tiles_m * p.block_m >= M > (p.tiles_m - 1) * p.block_m
     assert p.tiles_n * p.block_n >= N > (p.tiles_n - 1) * p.block_n
-    assert p.grid == p.tiles_m * p.tiles_n
+    assert p.num_tiles == p.tiles_m * p.tiles_n
+    # persistent grid: no more workgroups than tiles, a multiple of the 8 XCDs
+    # unless the tiles run out first
+    assert 1 <= p.grid <= p.num_tiles
+    if p.plan_id not in (6, 7):  # panel plans size the grid by row panels x column runs
+        assert p.grid % 8 == 0 or p.grid == p.num_tiles
     assert p.k_chunk % p.block_k == 0
     assert p.k_chunk * p.split_k >= K > p.k_chunk * (p.split_k - 1)
     want_ws = p.split_k * batch * M * N * 4 if p.split_k > 1 else 0
@@ -117,7 +123,7 @@ def _cover(ck, args, num_cus=256):
     assert rc == 0
     seen = {}
     for s in range(p.split_k):
-        for wg in range(p.grid):
+        for wg in range(p.num_tiles):
             rc, tm, tn, kb, ke = ck.abi.tile_of(args, wg, s, num_cus)
             assert rc in (0, 1)
             seen.setdefault((tm, tn), []).append((rc, kb, ke))
@@ -146,7 +152,7 @@ def test_triangular_enumeration(ck, structure, n, cfg):
     args = ck.abi.make_args(n, n, n, structure=structure, plan_override=cfg)
     p, seen = _cover(ck, args)
     T = p.tiles_m
-    assert p.grid == T * T
+    assert p.num_tiles == T * T
     assert len(seen) == T * T
     for (tm, tn), parts in seen.items():
         assert len(parts) == 1
@@ -170,11 +176,12 @@ def test_xcd_remap_groups_neighbouring_tiles(ck):
     # (workgroup ids congruent mod 8) form one contiguous block of the raster.
     args = ck.abi.make_args(8192, 8192, 8192)
     rc, p = ck.abi.plan(8192, 8192, 8192)
+    assert p.grid % 8 == 0
     per_xcd = {}
-    for wg in range(p.grid):
+    for wg in range(p.num_tiles):   # work item wg runs on workgroup wg % grid, XCD wg % 8
         _, tm, tn, _, _ = ck.abi.tile_of(args, wg)
         per_xcd.setdefault(wg % 8, set()).add((tm, tn))
-    assert len(per_xcd) == 8 and sum(len(v) for v in per_xcd.values()) == p.grid
+    assert len(per_xcd) == 8 and sum(len(v) for v in per_xcd.values()) == p.num_tiles
     for tiles in per_xcd.values():
         rows = {t[0] for t in tiles}
         cols = {t[1] for t in tiles}

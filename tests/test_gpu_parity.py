@@ -61,8 +61,9 @@ def test_gemm_layouts_auto_plan(ck, orc, dev, op_a, op_b, M, N, K):
 
 
 @pytest.mark.parametrize("op_a,op_b", LAYOUTS)
-@pytest.mark.parametrize("cfg", [1, 2, 3])
-@pytest.mark.parametrize("M,N,K", [(512, 512, 512), (300, 200, 100), (64, 640, 37)])
+@pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5, 6, 7])
+@pytest.mark.parametrize("M,N,K", [(512, 512, 512), (300, 200, 100), (64, 640, 37), (700, 520, 31),
+                                   (130, 1030, 64), (1000, 999, 17), (513, 1027, 1)])
 def test_gemm_every_tile_config(ck, orc, dev, op_a, op_b, cfg, M, N, K):
     a_st, b_st = _host_operands(orc, M, N, K, op_a, op_b, seed=11)
     A, B = to_dev(a_st), to_dev(b_st)
@@ -74,9 +75,9 @@ def test_gemm_every_tile_config(ck, orc, dev, op_a, op_b, cfg, M, N, K):
 
 
 @pytest.mark.parametrize("op_a,op_b", LAYOUTS)
-@pytest.mark.parametrize("cfg", [1, 2, 3])
+@pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5, 6, 7])
 def test_integer_inputs_bitwise(ck, orc, dev, op_a, op_b, cfg):
-    M, N, K = 200, 136, 1000
+    M, N, K = 200, 136, {4: 32, 5: 64, 6: 32, 7: 64}.get(cfg, 1000)
     a_st = orc.integers((K, M) if op_a else (M, K), seed=21)
     b_st = orc.integers((N, K) if op_b else (K, N), seed=22)
     A, B = to_dev(a_st), to_dev(b_st)
@@ -155,13 +156,17 @@ def test_strided_batched_and_broadcast(ck, orc, dev, op_a, op_b):
                  what="broadcast")
 
 
-def test_leading_dimensions_larger_than_rows(ck, orc, dev):
-    M, N, K = 100, 60, 50
+@pytest.mark.parametrize("N,pad_c", [(60, 5), (61, 3), (64, 4)])
+@pytest.mark.parametrize("cfg", [0, 1, 2, 3, 7])
+def test_leading_dimensions_larger_than_rows(ck, orc, dev, N, pad_c, cfg):
+    # ldc = N + pad_c covers the 16-byte store path (ldc % 4 == 0) with a
+    # ragged last column group, and the element-store path (ldc % 4 != 0)
+    M, K = 300, 50
     big_a = orc.uniform((M, K + 13), 61)
     big_b = orc.uniform((K, N + 7), 62)
-    C_big = torch.full((M, N + 5), -7.0, device="cuda")
+    C_big = torch.full((M, N + pad_c), -7.0, device="cuda")
     ck.abi.check(run_gemm(ck, gemm_args(ck, to_dev(big_a), to_dev(big_b), C_big, M, N, K,
-                                        lda=K + 13, ldb=N + 7, ldc=N + 5)))
+                                        lda=K + 13, ldb=N + 7, ldc=N + pad_c, override=cfg)))
     got = to_host(C_big)
     assert_close(orc, got[:, :N], orc.gemm(big_a[:, :K], big_b[:, :N]), K, what="ld")
     assert np.all(got[:, N:] == -7.0), "wrote outside the ldc window"
@@ -169,7 +174,7 @@ def test_leading_dimensions_larger_than_rows(ck, orc, dev):
 
 @pytest.mark.parametrize("structure", [1, 2])
 @pytest.mark.parametrize("n", [1, 5, 64, 100, 257, 640])
-@pytest.mark.parametrize("cfg", [0, 1, 2, 3])
+@pytest.mark.parametrize("cfg", [0, 1, 2, 3, 4, 5])
 def test_triangular_products(ck, orc, dev, structure, n, cfg):
     tri = np.tril if structure == 1 else np.triu
     a = tri(orc.uniform((n, n), 71))
@@ -330,9 +335,9 @@ def test_zero_sizes(ck, dev):
         assert L.mi_matmul_f32(None, None, None, M, 3, N, s) == 0
 
 
-@pytest.mark.parametrize("cfg", [1, 2, 3])
+@pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5, 6, 7])
 def test_repeatability_bitwise(ck, orc, dev, cfg):
-    M, N, K = 512, 384, 1536
+    M, N, K = 512, 384, {4: 32, 5: 64, 6: 32, 7: 64}.get(cfg, 1536)
     A, B = dev_uniform(ck, (M, K), 121), dev_uniform(ck, (K, N), 122)
     first = None
     for _ in range(20):
@@ -343,3 +348,19 @@ def test_repeatability_bitwise(ck, orc, dev, cfg):
             first = h
         else:
             np.testing.assert_array_equal(h, first)
+
+
+@pytest.mark.parametrize("op_a,op_b", LAYOUTS)
+@pytest.mark.parametrize("cfg", [6, 7])
+def test_panel_kernel_batched_and_many_column_runs(ck, orc, dev, op_a, op_b, cfg):
+    # several batches, several A row panels, ragged last panel and column tile
+    batch, M, N, K = 3, 600, 2100, 30 if cfg == 6 else 61
+    a_st = orc.uniform((batch,) + ((K, M) if op_a else (M, K)), 131)
+    b_st = orc.uniform((batch,) + ((N, K) if op_b else (K, N)), 132)
+    A, B = to_dev(a_st), to_dev(b_st)
+    C = torch.full((batch, M, N), float("nan"), device="cuda")
+    ck.abi.check(run_gemm(ck, gemm_args(ck, A, B, C, M, N, K, op_a, op_b, batch=batch,
+                                        sa=a_st[0].size, sb=b_st[0].size, sc=M * N, override=cfg)))
+    la = np.swapaxes(a_st, 1, 2) if op_a else a_st
+    lb = np.swapaxes(b_st, 1, 2) if op_b else b_st
+    assert_close(orc, to_host(C), orc.gemm(la, lb), K, what=f"panel cfg {cfg}")
