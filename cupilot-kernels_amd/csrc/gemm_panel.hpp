@@ -85,6 +85,91 @@ __global__ void __launch_bounds__(T::NT) gemm_f32_panel_kernel(const GemmParams 
         }
         __syncthreads();
 
+        // Fast path: the item's tiles are all interior, K fills every k-block
+        // and rows are 16-byte aligned, so every store is unconditional.  Two
+        // accumulator sets: while tile s is computed, tile s-1 is stored, a
+        // few 16-byte stores after each k-block of MFMAs, so stores and MFMAs
+        // overlap inside each wave instead of alternating.
+        const bool fast = c_vec && nkb == T::KMAX / 8 && m0 + T::BM <= p.M &&
+                          (int64_t)tn_end * T::BN <= p.N && run >= 2;
+        if (fast) {
+            constexpr int KBLK = T::KMAX / 8;
+            constexpr int NST = T::TM * T::TN * 4;   // 16-byte stores per wave per tile
+            constexpr int SPK = (NST + KBLK - 1) / KBLK;
+            f16v acc0[T::TM][T::TN], acc1[T::TM][T::TN];
+
+            auto store_one = [&](const f16v (&acc)[T::TM][T::TN], int q, int tn) {
+                const int i = q / (T::TN * 4), j = (q / 4) % T::TN, g = q % 4;
+                const int row = m0 + wm * T::WM + i * 32 + (lane & 31);
+                const int col = tn * T::BN + wn * T::WN + j * 32 + g * 8 + half * 4;
+                const f4 v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                              acc[i][j][4 * g + 3]};
+                *reinterpret_cast<f4*>(C + (int64_t)row * p.ldc + col) = v;
+            };
+            // MFMAs of one tile from LDS buffer `buf` into acc_c; with
+            // STORE, the previous tile's stores ride along, SPK per k-block.
+            auto tile_step = [&](f16v (&acc_c)[T::TM][T::TN], const float* Bs,
+                                 const f16v (&acc_s)[T::TM][T::TN], int tn_s, bool store) {
+#pragma unroll
+                for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < T::TN; ++j)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) acc_c[i][j][r] = 0.f;
+#pragma unroll
+                for (int kb = 0; kb < KBLK; ++kb) {
+                    float a[T::TM][4], b[T::TN][4];
+#pragma unroll
+                    for (int i = 0; i < T::TM; ++i) LA::frag(sA, wm * T::WM + i * 32, kb, lane, a[i]);
+#pragma unroll
+                    for (int j = 0; j < T::TN; ++j) LB::frag(Bs, wn * T::WN + j * 32, kb, lane, b[j]);
+#pragma unroll
+                    for (int s = 0; s < 4; ++s)
+#pragma unroll
+                        for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+                            for (int j = 0; j < T::TN; ++j)
+                                acc_c[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(b[j][s], a[i][s],
+                                                                                   acc_c[i][j], 0, 0, 0);
+                    if (store) {
+#pragma unroll
+                        for (int qq = 0; qq < SPK; ++qq)
+                            if (kb * SPK + qq < NST) store_one(acc_s, kb * SPK + qq, tn_s);
+                        // keep these stores among this k-block's MFMAs: only
+                        // MFMAs (0x8) and LDS reads (0x100) may move across
+                        __builtin_amdgcn_sched_barrier(0x108);
+                    }
+                }
+            };
+            // one step: prefetch the next B tile, compute (and store the
+            // previous tile), then put the prefetched tile in the other buffer
+            auto step_fn = [&](int step, f16v (&acc_c)[T::TM][T::TN],
+                               const f16v (&acc_s)[T::TM][T::TN], bool store) {
+                const int buf = step & 1;
+                const int tn_next = col_tile(step + 1 < run ? step + 1 : step);
+                lb.load(B, p.ldb, tn_next * T::BN, p.N, 0, p.K, tid);
+                tile_step(acc_c, sB[buf], acc_s, store ? col_tile(step - 1) : 0, store);
+                lb.store(sB[buf ^ 1], tid);
+                __syncthreads();
+            };
+
+            step_fn(0, acc0, acc1, false);
+            int step = 1;
+            for (; step + 1 < run; step += 2) {
+                step_fn(step, acc1, acc0, true);
+                step_fn(step + 1, acc0, acc1, true);
+            }
+            if (step < run) {
+                step_fn(step, acc1, acc0, true);
+#pragma unroll
+                for (int q = 0; q < NST; ++q) store_one(acc1, q, col_tile(step));
+            } else {
+#pragma unroll
+                for (int q = 0; q < NST; ++q) store_one(acc0, q, col_tile(run - 1));
+            }
+            continue;
+        }
+
         for (int step = 0; step < run; ++step) {
             const int buf = step & 1;
             const int tn = col_tile(step);

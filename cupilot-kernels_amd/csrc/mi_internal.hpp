@@ -16,7 +16,7 @@ namespace mi {
 //   3   256 x 256        8      128 x 64    ~140 KiB (32-deep K slices)
 //   4   128 x 128        4      64 x 64     ~35 KiB, one 32-deep slice (K <= 32)
 //   5   128 x 128        4      64 x 64     ~68 KiB, one 64-deep slice (K <= 64)
-//   6   256 x 128 panel  8      64 x 64     A panel resident, K <= 32 (~71 KiB)
+//   6   256 x 128 panel  8      64 x 64     A panel resident, K <= 32 (~71 KiB, 1 WG/CU)
 //   7   256 x 128 panel  8      64 x 64     A panel resident, K <= 64 (~137 KiB)
 enum TileCfgId {
     kCfg64 = 1, kCfg128 = 2, kCfg256 = 3, kCfg128K32 = 4, kCfg128K64 = 5,

@@ -56,7 +56,7 @@ int resident_wgs(int cfg) {
         case kCfg128: return 3;
         case kCfg128K32: return 3;
         case kCfg128K64: return 2;
-        case kCfgPanel32: return 2;
+        case kCfgPanel32: return 1;
         case kCfgPanel64: return 1;
         default: return 8;
     }
