@@ -125,9 +125,10 @@ int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
                                 2 * (int64_t)num_cus) {
         // Small K and a large output: the A-panel kernel cuts operand reloads
         // to ~K/256 of the output bytes (tall-skinny: 4 GiB instead of 16 GiB).
-        // Measured on MI355X the 64-deep panel is also the faster one at K = 32
-        // (16384^2 x 32: 0.304 ms against 0.433 ms for the 32-deep panel).
-        best_cfg = kCfgPanel64;
+        // The panel depth matching K takes the overlapped-store path
+        // (16384^2 x 32: 0.29 ms with the 32-deep panel, 0.34 ms with the
+        // 64-deep one).
+        best_cfg = a.K <= 32 ? kCfgPanel32 : kCfgPanel64;
     } else {
         double best_t = 1e300;
         const int64_t batch = std::max<int64_t>(1, a.batch);

@@ -4,9 +4,10 @@
 //   gemv_kernel    y = A.x (kernels/4_Matrix_vector_multiplication_best_kernel.cu:6-80
 //                  is the reference's version).  Every wave owns ROWS rows and
 //                  walks K with 16-byte non-temporal loads of A (A is read
-//                  exactly once, so it should not evict x from L2); each x
-//                  float4 it loads is used for all ROWS rows, cutting the x
-//                  traffic to 1/ROWS of A's.  The per-lane partial sums are
+//                  exactly once, so it should not evict x from L2; plain
+//                  loads measured 13 % slower); each x float4 it loads is
+//                  used for all ROWS rows, cutting the x traffic to 1/ROWS of
+//                  A's.  The per-lane partial sums are
 //                  reduced across the wave with xor shuffles at the end.
 //                  Optional split over K writes per-split partial sums that a
 //                  second pass adds in fixed order.
@@ -63,6 +64,10 @@ __global__ void __launch_bounds__(kGemvThreads)
                 for (int r = 0; r < ROWS; ++r)
                     av[u][r] = __builtin_nontemporal_load(reinterpret_cast<const f4*>(arow[r] + k + u * 256));
             }
+            // all UNROLL * ROWS loads are issued before the first FMA waits on
+            // one (left to itself the scheduler may pair each load with its
+            // FMAs, which serialises the loads on their latency)
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int u = 0; u < UNROLL; ++u)
 #pragma unroll
@@ -117,12 +122,17 @@ __global__ void gemv_reduce_kernel(const float* __restrict__ ws, float* __restri
     y[i] = s;
 }
 
-constexpr int kGemvRows = 8;
 constexpr int kGemvUnroll = 2;
 
 GemvPlan gemv_plan(int64_t M, int64_t K, bool aligned) {
     GemvPlan p;
-    p.rows_per_wg = kGemvWaves * kGemvRows;
+    // Rows per wave: each x float4 a wave loads serves all its rows, so more
+    // rows mean less x traffic; measured on MI355X at 32768 x 65536 with
+    // 16-byte non-temporal A loads: 16 rows 7.04 TB/s, 8 rows 6.89 TB/s,
+    // 4 rows 6.87 TB/s (2 and 1 rows lose to the x re-reads).  Fewer rows for
+    // smaller M keep >= 2048 waves in flight.
+    const int rows = M >= 16 * 2048 ? 16 : M >= 8 * 2048 ? 8 : 4;
+    p.rows_per_wg = kGemvWaves * rows;
     p.vec = aligned ? 4 : 1;
     const int64_t wgs = (M + p.rows_per_wg - 1) / p.rows_per_wg;
     // Split K only when the rows alone give fewer than 2 workgroups per CU
@@ -143,12 +153,20 @@ hipError_t launch_gemv(const GemvPlan& p, const float* A, const float* x, float*
                        int M, int K, int64_t lda, hipStream_t s) {
     const int wgs = (M + p.rows_per_wg - 1) / p.rows_per_wg;
     dim3 grid(wgs, p.split_k);
-    if (p.vec == 4)
-        hipLaunchKernelGGL((gemv_kernel<kGemvRows, kGemvUnroll, true>), grid, dim3(kGemvThreads), 0, s,
-                           A, x, y, ws, M, K, lda, p.k_chunk, p.split_k);
-    else
-        hipLaunchKernelGGL((gemv_kernel<kGemvRows, kGemvUnroll, false>), grid, dim3(kGemvThreads), 0,
-                           s, A, x, y, ws, M, K, lda, p.k_chunk, p.split_k);
+    const int rows = p.rows_per_wg / kGemvWaves;
+#define MI_GEMV_LAUNCH(R, V)                                                                      \
+    hipLaunchKernelGGL((gemv_kernel<R, kGemvUnroll, V>), grid, dim3(kGemvThreads), 0, s, A, x, y, \
+                       ws, M, K, lda, p.k_chunk, p.split_k)
+    if (p.vec == 4) {
+        if (rows == 16) MI_GEMV_LAUNCH(16, true);
+        else if (rows == 8) MI_GEMV_LAUNCH(8, true);
+        else MI_GEMV_LAUNCH(4, true);
+    } else {
+        if (rows == 16) MI_GEMV_LAUNCH(16, false);
+        else if (rows == 8) MI_GEMV_LAUNCH(8, false);
+        else MI_GEMV_LAUNCH(4, false);
+    }
+#undef MI_GEMV_LAUNCH
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || p.split_k == 1) return e;
     hipLaunchKernelGGL(gemv_reduce_kernel, dim3((M + 255) / 256), dim3(256), 0, s, ws, y, M, p.split_k);
@@ -170,10 +188,21 @@ __global__ void __launch_bounds__(kDiagThreads)
         float* dst = out + i * M;
         if (VEC) {
             const int64_t m4 = M / 4;
-            for (int64_t c = threadIdx.x; c < m4; c += kDiagThreads) {
-                const f4 v = __builtin_nontemporal_load(reinterpret_cast<const f4*>(src) + c);
-                __builtin_nontemporal_store(v * s, reinterpret_cast<f4*>(dst) + c);
+            const f4* s4 = reinterpret_cast<const f4*>(src);
+            f4* d4 = reinterpret_cast<f4*>(dst);
+            // 8 independent 16-byte loads in flight per thread before the
+            // stores, then a remainder loop
+            constexpr int U = 8;
+            int64_t c = threadIdx.x;
+            for (; c + (U - 1) * kDiagThreads < m4; c += U * kDiagThreads) {
+                f4 v[U];
+#pragma unroll
+                for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(s4 + c + u * kDiagThreads);
+#pragma unroll
+                for (int u = 0; u < U; ++u) __builtin_nontemporal_store(v[u] * s, d4 + c + u * kDiagThreads);
             }
+            for (; c < m4; c += kDiagThreads)
+                __builtin_nontemporal_store(__builtin_nontemporal_load(s4 + c) * s, d4 + c);
         } else {
             for (int64_t c = threadIdx.x; c < M; c += kDiagThreads)
                 __builtin_nontemporal_store(__builtin_nontemporal_load(src + c) * s, dst + c);
