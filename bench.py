@@ -61,6 +61,26 @@ def read_traffic():
     return float(m.group(1)) if m else None
 
 
+# tile configuration of each scheduler plan id (mi_plan.plan_id), as named in
+# the kernel symbols rocprofv3 reports
+PLAN_KERNELS = {
+    1: "gemm_f32_kernel<Tile<64,64,32,32,16,8,2>>",
+    2: "gemm_f32_kernel<Tile<128,128,64,64,16,3,2>>",
+    3: "gemm_f32_kernel<Tile<256,256,128,64,32,2,2>>",
+    4: "gemm_f32_kernel<Tile<128,128,64,64,32,3,1>>",
+    5: "gemm_f32_kernel<Tile<128,128,64,64,64,2,1>>",
+    6: "gemm_f32_panel_kernel<PanelTile<256,128,32>>",
+    7: "gemm_f32_panel_kernel<PanelTile<256,128,64>>",
+}
+
+
+def nn_kernel_name(ck) -> str:
+    """Kernel the scheduler picks for the NN 8192^3 launch."""
+    rc, plan = ck.abi.plan(N, N, N)
+    ck.abi.check(rc, "mi_gemm_plan")
+    return f"mi::{PLAN_KERNELS.get(plan.plan_id, plan.plan_id)}, NN, vec4, dense (split_k {plan.split_k})"
+
+
 def _time(fn, stream, reps, warm):
     import torch
     for _ in range(warm):
@@ -216,7 +236,7 @@ def main() -> int:
         nn_ms = out["gemm"]["per_layout_ms"]["NN"]
         out["roofline"] = {
             "bound": "mfma",
-            "kernel": "mi::gemm_f32_kernel<Tile<256,256,128,64>, NN, vec4, dense>",
+            "kernel": nn_kernel_name(ck),
             "achieved": flops / (nn_ms * 1e-3) / 1e12,
             "peak": PEAK_TFLOPS,
             "unit": "TFLOP/s",
