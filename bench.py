@@ -136,6 +136,19 @@ def run_configs(ck, fill, dev, stream):
     rec("diag_8192", _time(lambda i: ck.p12.diag_mult_cuda(a2[i % 2], B2[i % 2]), stream, 20, 4),
         None, 4 * (8192 + 2 * 8192 * 8192))
     del a2, B2
+    # PID 5 matrix-scalar (no BASELINE config names a shape): a 256 MiB matrix,
+    # two alternating inputs for the same reason as diag
+    A2 = [u((16384, 4096), 57), u((16384, 4096), 58)]
+    rec("scalar_16384x4096", _time(lambda i: ck.p05.matrix_scalar_mult_cuda(A2[i % 2], 3.14), stream,
+                                   20, 4), None, 4 * 2 * 16384 * 4096)
+    del A2
+    # PID 87 pointwise conv (no BASELINE config): 16 images of 64 x 256 x 256
+    # to 128 channels, with bias; a batched contraction over the weight
+    X, W, Bi = u((16, 64, 256, 256), 59), u((128, 64, 1, 1), 60), u((128,), 61)
+    rec("pointwise_conv_16x64x128x256x256",
+        _time(lambda i: ck.p87.pointwise_conv_cuda(X, W, Bi), stream, 10, 2),
+        2 * 16 * 128 * 64 * 65536, 4 * (16 * 64 * 65536 + 128 * 64 + 128 + 16 * 128 * 65536))
+    del X, W, Bi
     A, B = u((256, 1 << 20), 64), u((1 << 20, 256), 65)
     rec("large_k_256x256x1048576", _time(lambda i: ck.p06.matmul_cuda(A, B), stream, 10, 2),
         2 * 256 * 256 * (1 << 20))

@@ -1,5 +1,6 @@
 """MI355X (gfx950) GEMM-family operators: a drop-in for the GEMM path of
-champloo2878/cuPilot-Kernels (kernels/1..4, 6..18).
+champloo2878/cuPilot-Kernels (kernels/1..18) and its pointwise convolution
+(kernels/87).
 
     import torch
     from __graft_entry__ import load_package
@@ -29,9 +30,10 @@ except ImportError as e:  # pragma: no cover - exercised when the build is missi
 from . import abi  # noqa: E402
 from .models import ModelNew, PIDS, OPS  # noqa: E402,F401
 
-p01, p02, p03, p04 = _C.p01, _C.p02, _C.p03, _C.p04
+p01, p02, p03, p04, p05 = _C.p01, _C.p02, _C.p03, _C.p04, _C.p05
 p06, p07, p08, p09 = _C.p06, _C.p07, _C.p08, _C.p09
 p10, p11, p12, p13 = _C.p10, _C.p11, _C.p12, _C.p13
 p14, p15, p16, p17, p18 = _C.p14, _C.p15, _C.p16, _C.p17, _C.p18
+p87 = _C.p87
 
 __version__ = _C.version()

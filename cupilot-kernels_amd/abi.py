@@ -42,6 +42,7 @@ class GemmArgs(ctypes.Structure):
         ("op_a", ctypes.c_int32), ("op_b", ctypes.c_int32),
         ("structure", ctypes.c_int32), ("plan_override", ctypes.c_int32),
         ("workspace", _vp), ("workspace_bytes", _sz),
+        ("bias_m", _vp),
     ]
 
 
@@ -75,6 +76,8 @@ SIGNATURES = {
     "mi_tensor3d_matmul_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
     "mi_tensor4d_matmul_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp]),
     "mi_diag_mult_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _vp]),
+    "mi_matrix_scalar_mult_f32": (ctypes.c_int, [_vp, _vp, _i64, ctypes.c_float, _vp]),
+    "mi_pointwise_conv_f32": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
     "mi_symmetric_matmul_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _vp]),
     "mi_upper_tri_matmul_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _vp]),
     "mi_lower_tri_mul_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _vp]),

@@ -152,7 +152,8 @@ int mi_gemm_f32(const mi_gemm_args* args, void* stream) {
     if (empty_out) return MI_OK;
     if (!a.C) return MI_ERR_NULL_POINTER;
     hipStream_t s = as_stream(stream);
-    if (a.K == 0) return hip_rc(launch_fill_zero_2d(a.C, a.M, a.N, a.ldc, a.batch, a.stride_c, s));
+    if (a.K == 0)
+        return hip_rc(launch_fill_zero_2d(a.C, a.M, a.N, a.ldc, a.batch, a.stride_c, s, a.bias_m));
     if (!a.A || !a.B) return MI_ERR_NULL_POINTER;
 
     int st = MI_OK;
@@ -172,7 +173,8 @@ int mi_gemm_f32(const mi_gemm_args* args, void* stream) {
     else e = launch_gemm_tt(g, s);
     if (e != hipSuccess) return hip_rc(e);
     if (g.split_k > 1)
-        e = launch_splitk_reduce(g.ws, a.C, g.M, g.N, g.batch, g.split_k, a.ldc, a.stride_c, s);
+        e = launch_splitk_reduce(g.ws, a.C, g.M, g.N, g.batch, g.split_k, a.ldc, a.stride_c,
+                                 a.bias_m, s);
     return hip_rc(e);
 }
 
@@ -269,6 +271,28 @@ int mi_diag_mult_f32(const float* a, const float* B, float* out, int64_t N, int6
     if (N == 0 || M == 0) return MI_OK;
     if (!a || !B || !out) return MI_ERR_NULL_POINTER;
     return hip_rc(launch_diag(a, B, out, N, M, as_stream(stream)));
+}
+
+int mi_matrix_scalar_mult_f32(const float* A, float* C, int64_t n, float s, void* stream) {
+    if (n < 0) return MI_ERR_BAD_SIZE;
+    if (n == 0) return MI_OK;
+    if (!A || !C) return MI_ERR_NULL_POINTER;
+    return hip_rc(launch_scale(A, C, n, s, as_stream(stream)));
+}
+
+int mi_pointwise_conv_f32(const float* input, const float* weight, const float* bias,
+                          float* output, int64_t batch, int64_t in_channels, int64_t out_channels,
+                          int64_t hw, void* stream) {
+    if (batch < 0 || in_channels < 0 || out_channels < 0 || hw < 0) return MI_ERR_BAD_SIZE;
+    // per image: out (Cout x HW) = W (Cout x Cin) . X (Cin x HW) + bias
+    mi_gemm_args a = dense_args(weight, input, output, out_channels, in_channels, hw, MI_OP_N,
+                                MI_OP_N);
+    a.batch = batch;
+    a.stride_a = 0;
+    a.stride_b = in_channels * hw;
+    a.stride_c = out_channels * hw;
+    a.bias_m = bias;
+    return mi_gemm_f32(&a, stream);
 }
 
 int mi_symmetric_matmul_f32(const float* A, const float* B, float* C, int64_t N, void* stream) {

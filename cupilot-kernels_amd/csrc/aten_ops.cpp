@@ -312,6 +312,53 @@ at::Tensor diag_mult(const at::Tensor& A, const at::Tensor& B) {
     return out;
 }
 
+// kernels/5_Matrix_scalar_multiplication_best_kernel.cu:47-71 (the 3 checks;
+// output empty_like(A), no launch for an empty A)
+at::Tensor matrix_scalar_mult(const at::Tensor& A, double s) {
+    TORCH_CHECK(A.is_cuda(), "A must be a CUDA tensor");
+    TORCH_CHECK(A.scalar_type() == at::kFloat, "A must be float32");
+    TORCH_CHECK(A.is_contiguous(), "A must be contiguous");
+    at::Tensor C = at::empty_like(A);
+    if (A.numel() == 0) return C;
+    check_rc(mi_matrix_scalar_mult_f32(A.data_ptr<float>(), C.data_ptr<float>(), A.numel(),
+                                       static_cast<float>(s), current_stream(A)),
+             "matrix_scalar_mult_cuda");
+    return C;
+}
+
+// kernels/87_conv_pointwise_2D_best_kernel.cu:451-492.  The reference checks
+// nothing and dispatches fp32/fp64/fp16/bf16; this operator is the fp32 path
+// and rejects the rest, and checks the shapes the reference assumes (weight
+// Cout x Cin [x 1 x 1], bias Cout).  Output: empty {N, Cout, H, W}.
+at::Tensor pointwise_conv(const at::Tensor& input, const at::Tensor& weight,
+                          const c10::optional<at::Tensor>& bias_opt) {
+    TORCH_CHECK(input.dim() == 4, "input must be 4D (N, C_in, H, W)");
+    TORCH_CHECK(weight.dim() == 2 || (weight.dim() == 4 && weight.size(2) == 1 && weight.size(3) == 1),
+                "weight must be (C_out, C_in) or (C_out, C_in, 1, 1)");
+    check_tensor(input, "input");
+    check_tensor(weight, "weight");
+    TORCH_CHECK(input.device() == weight.device(), "input and weight must be on the same device");
+    const int64_t n = input.size(0), cin = input.size(1), h = input.size(2), w = input.size(3);
+    const int64_t cout = weight.size(0);
+    TORCH_CHECK(weight.size(1) == cin, "weight.size(1) must equal the input channels");
+    at::Tensor bias;
+    if (bias_opt.has_value() && bias_opt->defined()) {
+        bias = *bias_opt;
+        check_tensor(bias, "bias");
+        TORCH_CHECK(bias.device() == input.device(), "bias must be on the input's device");
+        TORCH_CHECK(bias.numel() == cout, "bias must have C_out elements");
+        bias = bias.contiguous();
+    }
+    at::Tensor out = at::empty({n, cout, h, w}, input.options());
+    if (out.numel() == 0) return out;
+    at::Tensor x = input.contiguous(), wt = weight.contiguous();
+    check_rc(mi_pointwise_conv_f32(x.data_ptr<float>(), wt.data_ptr<float>(),
+                                   bias.defined() ? bias.data_ptr<float>() : nullptr,
+                                   out.data_ptr<float>(), n, cin, cout, h * w, current_stream(input)),
+             "pointwise_conv_cuda");
+    return out;
+}
+
 // kernels/13_Matmul_for_symmetric_matrices_best_kernel.cu:134-151
 at::Tensor symmetric_matmul(const at::Tensor& A, const at::Tensor& B) {
     TORCH_CHECK(A.dim() == 2, "A must be 2D");
@@ -389,7 +436,7 @@ at::Tensor matmul_transposed_both(const at::Tensor& A, const at::Tensor& B) {
 // function name (the names collide across files: matmul_cuda is PIDs 1, 2, 6,
 // 8 and 17; matmul_transposed_cuda is 16 and 18; batched_matmul_cuda is 3 and 10).
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
-    m.doc() = "MI355X GEMM-family operators (drop-in for cuPilot-Kernels PIDs 1-4, 6-18)";
+    m.doc() = "MI355X GEMM-family operators (drop-in for cuPilot-Kernels PIDs 1-18 and 87)";
     struct Entry {
         const char* sub;
         const char* name;
@@ -418,6 +465,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         auto sub = m.def_submodule(e.sub);
         sub.def(e.name, e.fn, pybind11::arg("A"), pybind11::arg("B"));
     }
+    // PID 5 takes (Tensor A, float s); PID 87 (input, weight, optional bias)
+    m.def_submodule("p05").def("matrix_scalar_mult_cuda", &mi355::matrix_scalar_mult,
+                               pybind11::arg("A"), pybind11::arg("s"));
+    m.def_submodule("p87").def("pointwise_conv_cuda", &mi355::pointwise_conv, pybind11::arg("input"),
+                               pybind11::arg("weight"), pybind11::arg("bias_opt") = pybind11::none());
     m.def("square_matmul", &mi355::square_matmul);
     m.def("matmul", &mi355::matmul);
     m.def("batched_matmul", &mi355::batched_matmul);
@@ -428,6 +480,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("tensor3d_matmul", &mi355::tensor3d_matmul);
     m.def("tensor4d_matmul", &mi355::tensor4d_matmul);
     m.def("diag_mult", &mi355::diag_mult);
+    m.def("matrix_scalar_mult", &mi355::matrix_scalar_mult);
+    m.def("pointwise_conv", &mi355::pointwise_conv);
     m.def("symmetric_matmul", &mi355::symmetric_matmul);
     m.def("upper_tri_matmul", &mi355::upper_tri_matmul);
     m.def("lower_tri_mul", &mi355::lower_tri_mul);

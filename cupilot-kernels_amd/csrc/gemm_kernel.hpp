@@ -207,26 +207,32 @@ __device__ __forceinline__ TileWork decode_tile(const GemmParams& p, int tile) {
 // work).  Block (i, j) holds C^T: lane l owns row l%32 of the 32x32 block and
 // accumulator registers 4g..4g+3 its columns 8g + 4*(l/32) .. +3, so every
 // register group is one 16-byte store.  Triangular modes write +0.0 on the
-// wrong side of the diagonal.
-template <class T, int MODE>
+// wrong side of the diagonal.  A per-row bias (dense only) is added here when
+// the tile holds the full sum; split-K partials get it in the reduction.
+template <class T, int MODE, bool BIAS>
 __device__ __forceinline__ void store_tile(const GemmParams& p, float* C, int64_t ldc, bool c_vec,
                                            const TileWork& w, const f16v (&acc)[T::TM][T::TN],
                                            bool zero, int wm, int wn, int lane) {
     const int m0 = w.tm * T::BM, n0 = w.tn * T::BN;
     const int half = lane >> 5;
+    // (a separate instantiation, so the plain epilogue carries no bias code)
+    const bool add_bias = BIAS && MODE == kDense && p.split_k == 1;
 #pragma unroll
-    for (int i = 0; i < T::TM; ++i)
+    for (int i = 0; i < T::TM; ++i) {
+        const int brow = m0 + wm * T::WM + i * 32 + (lane & 31);
+        const float bv = add_bias && brow < p.M ? p.bias[brow] : 0.f;
 #pragma unroll
         for (int j = 0; j < T::TN; ++j)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                const int row = m0 + wm * T::WM + i * 32 + (lane & 31);
+                const int row = brow;
                 const int col = n0 + wn * T::WN + j * 32 + g * 8 + half * 4;
                 if (row >= p.M) continue;
                 f4 v;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     float x = zero ? 0.f : acc[i][j][4 * g + e];
+                    if (add_bias) x += bv;
                     if (MODE == kLower && col + e > row) x = 0.f;
                     if (MODE == kUpper && col + e < row) x = 0.f;
                     v[e] = x;
@@ -240,6 +246,7 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, float* C, int64_
                         if (col + e < p.N) dst[e] = v[e];
                 }
             }
+    }
 }
 
 // Persistent over tiles (workgroup b owns tiles b, b + gridDim.x, ...) and
@@ -251,7 +258,7 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, float* C, int64_
 // any wait for a prefetch also waits for every store issued before it; with
 // this order those are the previous tile's stores, which have had at least a
 // slice of MFMAs to drain.
-template <class T, bool AT, bool BT, int VEC, int MODE>
+template <class T, bool AT, bool BT, int VEC, int MODE, bool BIAS>
 __global__ void __launch_bounds__(T::NT)
     __attribute__((amdgpu_waves_per_eu(T::WAVES_PER_SIMD, T::WAVES_PER_SIMD)))
     gemm_f32_kernel(const GemmParams p) {
@@ -298,7 +305,7 @@ __global__ void __launch_bounds__(T::NT)
         while (t < p.num_tiles) {
             w = decode_tile<T, MODE>(p, t);
             if (w.nk > 0) return true;
-            store_tile<T, MODE>(p, C, ldc, c_vec, w, acc, true, wm, wn, lane);
+            store_tile<T, MODE, BIAS>(p, C, ldc, c_vec, w, acc, true, wm, wn, lane);
             t += gridDim.x;
         }
         return false;
@@ -376,7 +383,7 @@ __global__ void __launch_bounds__(T::NT)
         const int nb = T::STAGES == 2 ? (cb ^ 1) : 0;
         la.store(sA[nb], tid);
         lb.store(sB[nb], tid);
-        store_tile<T, MODE>(p, C, ldc, c_vec, cur, acc, false, wm, wn, lane);
+        store_tile<T, MODE, BIAS>(p, C, ldc, c_vec, cur, acc, false, wm, wn, lane);
 #pragma unroll
         for (int i = 0; i < T::TM; ++i)
 #pragma unroll
@@ -397,6 +404,7 @@ inline GemmParams make_params(const GemmLaunch& g) {
     p.B = g.B;
     p.C = g.C;
     p.ws = g.ws;
+    p.bias = g.bias;
     p.M = g.M;
     p.N = g.N;
     p.K = g.K;
@@ -418,17 +426,24 @@ inline GemmParams make_params(const GemmLaunch& g) {
     return p;
 }
 
-template <class T, bool AT, bool BT, int VEC, int MODE>
+template <class T, bool AT, bool BT, int VEC, int MODE, bool BIAS = false>
 hipError_t launch_one(const GemmLaunch& g, hipStream_t s) {
     const GemmParams p = make_params(g);
     dim3 grid((unsigned)g.grid_x, (unsigned)g.split_k, (unsigned)g.batch);
     // grid_x <= num_tiles workgroups walk the tile list (persistent)
-    hipLaunchKernelGGL((gemm_f32_kernel<T, AT, BT, VEC, MODE>), grid, dim3(T::NT), 0, s, p);
+    hipLaunchKernelGGL((gemm_f32_kernel<T, AT, BT, VEC, MODE, BIAS>), grid, dim3(T::NT), 0, s, p);
     return hipGetLastError();
 }
 
 template <class T, bool AT, bool BT>
 hipError_t launch_cfg(const GemmLaunch& g, hipStream_t s) {
+    // the per-row bias epilogue exists for the N/N layout only (the scheduler
+    // rejects bias with any other)
+    if constexpr (!AT && !BT) {
+        if (g.structure == kDense && g.bias != nullptr && g.split_k == 1)
+            return g.vec == 4 ? launch_one<T, AT, BT, 4, kDense, true>(g, s)
+                              : launch_one<T, AT, BT, 1, kDense, true>(g, s);
+    }
     if (g.structure == kDense) {
         return g.vec == 4 ? launch_one<T, AT, BT, 4, kDense>(g, s)
                           : launch_one<T, AT, BT, 1, kDense>(g, s);

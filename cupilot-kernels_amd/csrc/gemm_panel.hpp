@@ -31,7 +31,7 @@ struct PanelTile {
 using Panel32 = PanelTile<256, 128, 32>;
 using Panel64 = PanelTile<256, 128, 64>;
 
-template <class T, bool AT, bool BT, int VEC>
+template <class T, bool AT, bool BT, int VEC, bool BIAS>
 __global__ void __launch_bounds__(T::NT) gemm_f32_panel_kernel(const GemmParams p) {
     constexpr bool A_KC = !AT;
     constexpr bool B_KC = BT;
@@ -56,6 +56,9 @@ __global__ void __launch_bounds__(T::NT) gemm_f32_panel_kernel(const GemmParams 
                        (p.sc % 4 == 0);
 
     const int items = p.tiles_m * p.col_splits;
+    // bias (the panel kernel never splits K) is a separate instantiation, so
+    // the plain store path carries no bias code
+    constexpr bool add_bias = BIAS;
     LA la;
     LB lb;
     for (int w = blockIdx.x; w < items; w += gridDim.x) {
@@ -64,6 +67,14 @@ __global__ void __launch_bounds__(T::NT) gemm_f32_panel_kernel(const GemmParams 
         const int tn_begin = (int)((int64_t)cs * p.tiles_n / p.col_splits);
         const int tn_end = (int)((int64_t)(cs + 1) * p.tiles_n / p.col_splits);
         const int m0 = tm * T::BM;
+        // per-row bias of this lane's TM output rows, read once per item
+        float bias_r[T::TM];
+#pragma unroll
+        for (int i = 0; i < T::TM; ++i) {
+            const int row = m0 + wm * T::WM + i * 32 + (lane & 31);
+            bias_r[i] = 0.f;
+            if (add_bias && row < p.M) bias_r[i] = p.bias[row];
+        }
 
         // Each item walks its column run starting at its own rotation, so the
         // workgroups running together store to different columns: in lockstep
@@ -102,8 +113,9 @@ __global__ void __launch_bounds__(T::NT) gemm_f32_panel_kernel(const GemmParams 
                 const int i = q / (T::TN * 4), j = (q / 4) % T::TN, g = q % 4;
                 const int row = m0 + wm * T::WM + i * 32 + (lane & 31);
                 const int col = tn * T::BN + wn * T::WN + j * 32 + g * 8 + half * 4;
-                const f4 v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
-                              acc[i][j][4 * g + 3]};
+                f4 v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                        acc[i][j][4 * g + 3]};
+                if (add_bias) v += bias_r[i];
                 *reinterpret_cast<f4*>(C + (int64_t)row * p.ldc + col) = v;
             };
             // MFMAs of one tile from LDS buffer `buf` into acc_c; with
@@ -220,8 +232,9 @@ __global__ void __launch_bounds__(T::NT) gemm_f32_panel_kernel(const GemmParams 
                         const int row = m0 + wm * T::WM + i * 32 + (lane & 31);
                         const int col = n0 + wn * T::WN + j * 32 + g * 8 + half * 4;
                         if (row >= p.M) continue;
-                        const f4 v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
-                                      acc[i][j][4 * g + 3]};
+                        f4 v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                                acc[i][j][4 * g + 3]};
+                        if (add_bias) v += bias_r[i];
                         float* dst = C + (int64_t)row * p.ldc + col;
                         if (c_vec && col + 3 < p.N) {
                             *reinterpret_cast<f4*>(dst) = v;
@@ -237,16 +250,25 @@ __global__ void __launch_bounds__(T::NT) gemm_f32_panel_kernel(const GemmParams 
     }
 }
 
-template <class T, bool AT, bool BT, int VEC>
+template <class T, bool AT, bool BT, int VEC, bool BIAS = false>
 hipError_t launch_panel_one(const GemmLaunch& g, hipStream_t s) {
     const GemmParams p = make_params(g);
     dim3 grid((unsigned)g.grid_x, 1u, (unsigned)g.batch);
-    hipLaunchKernelGGL((gemm_f32_panel_kernel<T, AT, BT, VEC>), grid, dim3(T::NT), 0, s, p);
+    hipLaunchKernelGGL((gemm_f32_panel_kernel<T, AT, BT, VEC, BIAS>), grid, dim3(T::NT), 0, s, p);
     return hipGetLastError();
 }
 
 template <bool AT, bool BT>
 hipError_t launch_panel(const GemmLaunch& g, hipStream_t s) {
+    if constexpr (!AT && !BT) {
+        if (g.bias != nullptr) {
+            if (g.cfg == kCfgPanel32)
+                return g.vec == 4 ? launch_panel_one<Panel32, AT, BT, 4, true>(g, s)
+                                  : launch_panel_one<Panel32, AT, BT, 1, true>(g, s);
+            return g.vec == 4 ? launch_panel_one<Panel64, AT, BT, 4, true>(g, s)
+                              : launch_panel_one<Panel64, AT, BT, 1, true>(g, s);
+        }
+    }
     if (g.cfg == kCfgPanel32)
         return g.vec == 4 ? launch_panel_one<Panel32, AT, BT, 4>(g, s)
                           : launch_panel_one<Panel32, AT, BT, 1>(g, s);

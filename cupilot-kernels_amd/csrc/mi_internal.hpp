@@ -46,6 +46,7 @@ struct GemmLaunch {
     const float* B;
     float* C;
     float* ws;            // split-K partials: split_k x batch x M x N (ld = N)
+    const float* bias;    // NULL or M per-row values added after the full sum
     int M, N, K, batch;
     int64_t lda, ldb, ldc;
     int64_t sa, sb, sc;
@@ -68,6 +69,7 @@ struct GemmParams {
     const float* B;
     float* C;
     float* ws;
+    const float* bias;        // NULL or M values; added by the kernel only when split_k == 1
     int M, N, K;
     int tiles_m, tiles_n, group_m;
     int num_tiles;
@@ -85,12 +87,14 @@ hipError_t launch_gemm_nt(const GemmLaunch& g, hipStream_t s);
 hipError_t launch_gemm_tt(const GemmLaunch& g, hipStream_t s);
 
 hipError_t launch_splitk_reduce(const float* ws, float* C, int M, int N, int batch, int split_k,
-                                int64_t ldc, int64_t sc, hipStream_t s);
+                                int64_t ldc, int64_t sc, const float* bias, hipStream_t s);
+// C[b][r][c] = bias ? bias[r] : 0 (a contraction with K = 0)
 hipError_t launch_fill_zero_2d(float* C, int64_t rows, int64_t cols, int64_t ld, int64_t batch,
-                               int64_t batch_stride, hipStream_t s);
+                               int64_t batch_stride, hipStream_t s, const float* bias = nullptr);
 hipError_t launch_fill_uniform(float* out, int64_t n, uint64_t seed, int64_t offset, hipStream_t s);
 hipError_t launch_diag(const float* a, const float* B, float* out, int64_t N, int64_t M,
                        hipStream_t s);
+hipError_t launch_scale(const float* A, float* C, int64_t n, float s, hipStream_t st);
 
 struct GemvPlan {
     int split_k;

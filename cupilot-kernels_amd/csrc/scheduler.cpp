@@ -87,7 +87,9 @@ int validate_shape(const mi_gemm_args& a) {
     if (a.op_a != MI_OP_N && a.op_a != MI_OP_T) return MI_ERR_BAD_LAYOUT;
     if (a.op_b != MI_OP_N && a.op_b != MI_OP_T) return MI_ERR_BAD_LAYOUT;
     if (a.structure < MI_DENSE || a.structure > MI_UPPER) return MI_ERR_BAD_LAYOUT;
+    if (a.bias_m && (a.op_a != MI_OP_N || a.op_b != MI_OP_N)) return MI_ERR_BAD_LAYOUT;
     if (a.structure != MI_DENSE) {
+        if (a.bias_m) return MI_ERR_BAD_LAYOUT;
         if (a.M != a.N || a.N != a.K) return MI_ERR_NOT_SQUARE;
         if (a.op_a != MI_OP_N || a.op_b != MI_OP_N || a.batch > 1) return MI_ERR_BAD_LAYOUT;
     }
@@ -121,10 +123,13 @@ int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
     } else if (override_ok) {
         best_cfg = override_cfg;
         best_split = is_panel_cfg(override_cfg) ? 1 : std::max(1, override_split);
-    } else if (a.K <= 64 && cdiv(a.M, 256) * cdiv(a.N, 128) * std::max<int64_t>(1, a.batch) >=
-                                2 * (int64_t)num_cus) {
+    } else if (a.K <= 64 && (a.M % 256 == 0 || a.M >= 2048) &&
+               cdiv(a.M, 256) * cdiv(a.N, 128) * std::max<int64_t>(1, a.batch) >=
+                   2 * (int64_t)num_cus) {
         // Small K and a large output: the A-panel kernel cuts operand reloads
         // to ~K/256 of the output bytes (tall-skinny: 4 GiB instead of 16 GiB).
+        // Its panels are 256 rows: M must fill them (at most 1/8 padding), or
+        // the padded rows cost MFMA time for nothing (M = 128: half).
         // The panel depth matching K takes the overlapped-store path
         // (16384^2 x 32: 0.29 ms with the 32-deep panel, 0.34 ms with the
         // 64-deep one).
@@ -211,6 +216,7 @@ int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
         g.B = a.B;
         g.C = a.C;
         g.ws = static_cast<float*>(a.workspace);
+        g.bias = a.bias_m;
         g.M = (int)a.M;
         g.N = (int)a.N;
         g.K = (int)a.K;

@@ -14,6 +14,9 @@
 //   diag_kernel    out[i,j] = a[i] * B[i,j]
 //                  (kernels/12_Matmul_with_diagonal_matrices_best_kernel.cu:9-38):
 //                  a pure 16-byte streaming copy-scale, one row per iteration.
+//   scale_kernel   C[i] = A[i] * s over a flat array
+//                  (kernels/5_Matrix_scalar_multiplication_best_kernel.cu:10-42):
+//                  the same stream over fixed 32 KiB chunks of the array.
 //   splitk_reduce  C = sum over splits of the partial tiles, in split order.
 //   fill kernels   zero fill and the counter-based uniform generator.
 #include "mi_device.hpp"
@@ -222,11 +225,63 @@ hipError_t launch_diag(const float* a, const float* B, float* out, int64_t N, in
 }
 
 // ---------------------------------------------------------------------------
+// C = s * A over a flat array
+// ---------------------------------------------------------------------------
+constexpr int kScaleThreads = 256;
+constexpr int kScaleUnroll = 8;  // 16-byte loads in flight per thread
+constexpr int64_t kScaleChunk = (int64_t)kScaleUnroll * kScaleThreads;  // float4s per chunk
+
+// Workgroup b streams chunks b, b + grid, ... of kScaleChunk float4s: all 8
+// loads of a thread are issued before its 8 stores.  The one partial chunk at
+// the end of the float4 range belongs to exactly one workgroup, which finishes
+// it element by element; workgroup 0 also does the last n % 4 floats.
+template <bool VEC>
+__global__ void __launch_bounds__(kScaleThreads)
+    scale_kernel(const float* __restrict__ A, float* __restrict__ C, float s, int64_t n) {
+    if (VEC) {
+        const int64_t n4 = n / 4;
+        const f4* a4 = reinterpret_cast<const f4*>(A);
+        f4* c4 = reinterpret_cast<f4*>(C);
+        int64_t base = (int64_t)blockIdx.x * kScaleChunk;
+        for (; base + kScaleChunk <= n4; base += (int64_t)gridDim.x * kScaleChunk) {
+            f4 v[kScaleUnroll];
+#pragma unroll
+            for (int u = 0; u < kScaleUnroll; ++u)
+                v[u] = __builtin_nontemporal_load(a4 + base + threadIdx.x + u * kScaleThreads);
+#pragma unroll
+            for (int u = 0; u < kScaleUnroll; ++u)
+                __builtin_nontemporal_store(v[u] * s, c4 + base + threadIdx.x + u * kScaleThreads);
+        }
+        for (int64_t i = base + threadIdx.x; i < n4; i += kScaleThreads) c4[i] = a4[i] * s;
+        const int64_t tail = n - n4 * 4;
+        if (blockIdx.x == 0 && threadIdx.x < tail) C[n4 * 4 + threadIdx.x] = A[n4 * 4 + threadIdx.x] * s;
+    } else {
+        for (int64_t i = (int64_t)blockIdx.x * kScaleThreads + threadIdx.x; i < n;
+             i += (int64_t)gridDim.x * kScaleThreads)
+            C[i] = A[i] * s;
+    }
+}
+
+hipError_t launch_scale(const float* A, float* C, int64_t n, float s, hipStream_t st) {
+    const bool vec = ((uintptr_t)A % 16 == 0) && ((uintptr_t)C % 16 == 0);
+    if (vec) {
+        int64_t grid = (n / 4 + kScaleChunk - 1) / kScaleChunk;
+        grid = grid < 1 ? 1 : (grid > 65536 ? 65536 : grid);
+        hipLaunchKernelGGL((scale_kernel<true>), dim3((unsigned)grid), dim3(kScaleThreads), 0, st, A, C, s, n);
+    } else {
+        int64_t grid = (n + kScaleThreads - 1) / kScaleThreads;
+        grid = grid > 65536 ? 65536 : grid;
+        hipLaunchKernelGGL((scale_kernel<false>), dim3((unsigned)grid), dim3(kScaleThreads), 0, st, A, C, s, n);
+    }
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // split-K reduction and fills
 // ---------------------------------------------------------------------------
 __global__ void splitk_reduce_kernel(const float* __restrict__ ws, float* __restrict__ C, int M,
                                      int N, int split_k, int64_t ldc, int64_t sc,
-                                     int64_t split_stride) {
+                                     int64_t split_stride, const float* __restrict__ bias) {
     const int64_t per_batch = (int64_t)M * N;
     const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int b = blockIdx.y;
@@ -235,37 +290,38 @@ __global__ void splitk_reduce_kernel(const float* __restrict__ ws, float* __rest
     float s = 0.f;
     for (int t = 0; t < split_k; ++t) s += src[(int64_t)t * split_stride];
     const int64_t row = e / N, col = e % N;
+    if (bias) s += bias[row];
     C[(int64_t)b * sc + row * ldc + col] = s;
 }
 
 hipError_t launch_splitk_reduce(const float* ws, float* C, int M, int N, int batch, int split_k,
-                                int64_t ldc, int64_t sc, hipStream_t s) {
+                                int64_t ldc, int64_t sc, const float* bias, hipStream_t s) {
     const int64_t per_batch = (int64_t)M * N;
     dim3 grid((unsigned)((per_batch + 255) / 256), (unsigned)batch);
     hipLaunchKernelGGL(splitk_reduce_kernel, grid, dim3(256), 0, s, ws, C, M, N, split_k, ldc, sc,
-                       per_batch * batch);
+                       per_batch * batch, bias);
     return hipGetLastError();
 }
 
 __global__ void fill_zero_kernel(float* __restrict__ C, int64_t rows, int64_t cols, int64_t ld,
-                                 int64_t batch_stride) {
+                                 int64_t batch_stride, const float* __restrict__ bias) {
     const int64_t per = rows * cols;
     const int64_t b = blockIdx.y;
     for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < per;
          e += (int64_t)gridDim.x * blockDim.x) {
         const int64_t r = e / cols, c = e % cols;
-        C[b * batch_stride + r * ld + c] = 0.f;
+        C[b * batch_stride + r * ld + c] = bias ? bias[r] : 0.f;
     }
 }
 
 hipError_t launch_fill_zero_2d(float* C, int64_t rows, int64_t cols, int64_t ld, int64_t batch,
-                               int64_t batch_stride, hipStream_t s) {
+                               int64_t batch_stride, hipStream_t s, const float* bias) {
     const int64_t per = rows * cols;
     if (per == 0 || batch == 0) return hipSuccess;
     int64_t blocks = (per + 255) / 256;
     if (blocks > 65536) blocks = 65536;
     hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)blocks, (unsigned)batch), dim3(256), 0, s, C,
-                       rows, cols, ld, batch_stride);
+                       rows, cols, ld, batch_stride, bias);
     return hipGetLastError();
 }
 

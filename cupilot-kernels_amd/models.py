@@ -19,6 +19,7 @@ OPS = {
     2: ("p02", "matmul_cuda", "kernels/2_Standard_matrix_multiplication_best_kernel.cu"),
     3: ("p03", "batched_matmul_cuda", "kernels/3_Batched_matrix_multiplication_best_kernel.cu"),
     4: ("p04", "gemv_cuda", "kernels/4_Matrix_vector_multiplication_best_kernel.cu"),
+    5: ("p05", "matrix_scalar_mult_cuda", "kernels/5_Matrix_scalar_multiplication_best_kernel.cu"),
     6: ("p06", "matmul_cuda", "kernels/6_Matmul_with_large_K_dimension_best_kernel.cu"),
     7: ("p07", "gemm_cuda", "kernels/7_Matmul_with_small_K_dimension_best_kernel.cu"),
     8: ("p08", "matmul_cuda", "kernels/8_Matmul_with_irregular_shapes_best_kernel.cu"),
@@ -32,6 +33,7 @@ OPS = {
     16: ("p16", "matmul_transposed_cuda", "kernels/16_Matmul_with_transposed_A_best_kernel.cu"),
     17: ("p17", "matmul_cuda", "kernels/17_Matmul_with_transposed_B_best_kernel.cu"),
     18: ("p18", "matmul_transposed_cuda", "kernels/18_Matmul_with_transposed_both_best_kernel.cu"),
+    87: ("p87", "pointwise_conv_cuda", "kernels/87_conv_pointwise_2D_best_kernel.cu"),
 }
 PIDS = tuple(sorted(OPS))
 
@@ -42,7 +44,13 @@ def op(pid: int):
 
 
 class ModelNew(torch.nn.Module):
-    """``forward(A, B)`` runs reference operator ``pid`` on the MI355X kernels."""
+    """``forward(A, B)`` runs reference operator ``pid`` on the MI355X kernels.
+
+    For PID 5 the second argument is the scalar ``s`` of
+    ``matrix_scalar_mult_cuda(A, float s)`` (a Python number or a 0-d tensor).
+    PID 87 is ``forward(input, weight, bias=None)`` of
+    ``pointwise_conv_cuda(input, weight, bias_opt)``.
+    """
 
     def __init__(self, pid: int):
         super().__init__()
@@ -51,7 +59,11 @@ class ModelNew(torch.nn.Module):
         self.pid = pid
         self._fn = op(pid)
 
-    def forward(self, A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
+    def forward(self, A: torch.Tensor, B, bias=None) -> torch.Tensor:
+        if self.pid == 5:
+            return self._fn(A, float(B))
+        if self.pid == 87:
+            return self._fn(A, B, bias)
         return self._fn(A, B)
 
     def extra_repr(self) -> str:

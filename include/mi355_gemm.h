@@ -78,6 +78,9 @@ typedef struct {
                                  config id, bits 8-19 split count, bits 20-30 raster group rows */
     void* workspace;
     size_t workspace_bytes;
+    const float* bias_m;      /* NULL, or M floats: C[b][i][j] = (sum over k) + bias_m[i],
+                                 one fp32 add after the full sum, the same for every
+                                 batch; dense structure and op_a = op_b = N only */
 } mi_gemm_args;
 
 /* Scheduler decision for one contraction (host-only, no device access). */
@@ -167,6 +170,23 @@ MI_API int mi_tensor4d_matmul_f32(const float* A, const float* B, float* out,
  * out (N x M) = diag(a) . B, a has length N; one fp32 multiply per element. */
 MI_API int mi_diag_mult_f32(const float* a, const float* B, float* out,
                      int64_t N, int64_t M, void* stream);
+
+/* kernels/5_Matrix_scalar_multiplication_best_kernel.cu:47 matrix_scalar_mult_cuda:
+ * C[i] = A[i] * s for the n floats of a contiguous array; one fp32 multiply
+ * per element. */
+MI_API int mi_matrix_scalar_mult_f32(const float* A, float* C, int64_t n, float s,
+                              void* stream);
+
+/* kernels/87_conv_pointwise_2D_best_kernel.cu:451 pointwise_conv_cuda (a 1x1
+ * convolution; the reference computes it at :174-446):
+ *   output[n][o][p] = sum_c weight[o][c] * input[n][c][p] + bias[o]
+ * with input N x Cin x HW, weight Cout x Cin (a Cout x Cin x 1 x 1 tensor),
+ * output N x Cout x HW, all contiguous, bias NULL or Cout floats (added once,
+ * after the full sum).  One batched contraction, the weight broadcast over
+ * the images. */
+MI_API int mi_pointwise_conv_f32(const float* input, const float* weight, const float* bias,
+                          float* output, int64_t batch, int64_t in_channels,
+                          int64_t out_channels, int64_t hw, void* stream);
 
 /* kernels/13_Matmul_for_symmetric_matrices_best_kernel.cu:134
  * symmetric_matmul_cuda: C = A . B for symmetric N x N A and B.  The kernel

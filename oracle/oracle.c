@@ -25,6 +25,15 @@
  *   orc_gemv_f64      y = A.x -- kernels/4_...:84-92 (B is Kx1, output Mx1)
  *   orc_diag_f32      out[i,j] = a[i]*B[i,j] -- kernels/12_...:43-62 (one fp32
  *                     multiply per element, so bitwise-exact)
+ *   orc_scale_f32     C[i] = A[i]*s -- kernels/5_...:10-42 (kernel: float4 body
+ *                     at :24-35, scalar tail at :36-40), :47-71 (wrapper: C is
+ *                     empty_like(A), n = A.numel()); one fp32 multiply per element
+ *   orc_pointwise_conv_f64
+ *                     out[n][o][p] = sum_c w[o][c]*x[n][c][p] + bias[o] --
+ *                     kernels/87_...:451-492 (wrapper: output N x Cout x H x W,
+ *                     weight indexed out_c * in_channels + c at :308,:321, bias
+ *                     optional at :452) and :373-388 (bias added once after the
+ *                     channel sum)
  *   orc_fill_uniform_f32 / orc_fill_int_f32
  *                     counter-based splitmix64 input generator shared with the
  *                     device fill kernel, so any element can be regenerated on
@@ -202,6 +211,29 @@ ORC_EXPORT void orc_diag_f32(const float* a, const float* B, float* out, int64_t
 #pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < N; ++i)
         for (int64_t j = 0; j < M; ++j) out[i * M + j] = a[i] * B[i * M + j];
+}
+
+ORC_EXPORT void orc_scale_f32(const float* A, float* C, int64_t n, float s) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) C[i] = A[i] * s;
+}
+
+ORC_EXPORT void orc_pointwise_conv_f64(const float* x, const float* w, const float* bias,
+                                       double* out, int64_t n, int64_t cin, int64_t cout,
+                                       int64_t hw) {
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int64_t b = 0; b < n; ++b)
+        for (int64_t o = 0; o < cout; ++o) {
+            double* dst = out + (b * cout + o) * hw;
+            for (int64_t p = 0; p < hw; ++p) dst[p] = 0.0;
+            for (int64_t c = 0; c < cin; ++c) {
+                const double wv = (double)w[o * cin + c];
+                const float* src = x + (b * cin + c) * hw;
+                for (int64_t p = 0; p < hw; ++p) dst[p] += wv * (double)src[p];
+            }
+            if (bias)
+                for (int64_t p = 0; p < hw; ++p) dst[p] += (double)bias[o];
+        }
 }
 
 /* max_t |got[t] - ref[t]| over n elements (fp32 result vs fp64 reference). */

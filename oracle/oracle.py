@@ -54,6 +54,8 @@ def lib():
         L.orc_gemv_f64.argtypes = [_f32p, _f32p, _f64p, _i64, _i64, _i64, _i64p, _i64]
         L.orc_gemv_generated_f64.argtypes = [_u64, _f32p, _f64p, _i64, _i64p, _i64]
         L.orc_diag_f32.argtypes = [_f32p, _f32p, _f32p, _i64, _i64]
+        L.orc_scale_f32.argtypes = [_f32p, _f32p, _i64, ctypes.c_float]
+        L.orc_pointwise_conv_f64.argtypes = [_f32p, _f32p, _f32p, _f64p, _i64, _i64, _i64, _i64]
         L.orc_max_abs_diff.restype = ctypes.c_double
         L.orc_max_abs_diff.argtypes = [_f32p, _f64p, _i64]
         L.orc_num_threads.restype = ctypes.c_int
@@ -193,6 +195,30 @@ def diag_mult(a: np.ndarray, b: np.ndarray) -> np.ndarray:
     assert a.shape == (N,)
     out = np.empty_like(b)
     lib().orc_diag_f32(_fp(a), _fp(b), _fp(out), N, M)
+    return out
+
+
+def scale(a: np.ndarray, s: float) -> np.ndarray:
+    """fp32 ``a * s`` elementwise (kernels/5_...:10-42, :47-71), same shape as ``a``."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    out = np.empty_like(a)
+    lib().orc_scale_f32(_fp(a), _fp(out), a.size, float(s))
+    return out
+
+
+def pointwise_conv(x: np.ndarray, w: np.ndarray, bias: Optional[np.ndarray] = None) -> np.ndarray:
+    """fp64-accumulated 1x1 convolution (kernels/87_...:451-492): x is
+    N x Cin x H x W, w is Cout x Cin (or Cout x Cin x 1 x 1), bias Cout or
+    None; returns N x Cout x H x W float64."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n, cin, h, wd = x.shape
+    w2 = np.ascontiguousarray(w, dtype=np.float32).reshape(w.shape[0], -1)
+    cout = w2.shape[0]
+    assert w2.shape[1] == cin
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32).reshape(cout)
+    out = np.empty((n, cout, h, wd), dtype=np.float64)
+    lib().orc_pointwise_conv_f64(_fp(x), _fp(w2), None if b is None else _fp(b), _dp(out),
+                                 n, cin, cout, h * wd)
     return out
 
 

@@ -1,5 +1,6 @@
 """Writes tests/golden/gemm_family_int.npz: small known-answer cases for every
-operator semantic of the GEMM-family path (reference kernels/1..4, 6..18).
+operator semantic of the GEMM-family path (reference kernels/1..18 and the
+pointwise convolution of kernels/87).
 
 The reference ships no tests, fixtures or golden vectors, so these are built
 from closed forms: integer-valued fp32 inputs in [-3, 3] whose products and
@@ -81,6 +82,18 @@ def main():
     # kernels/18_...:156-160 both stored transposed
     a, b = ints(rng, (6, 4)), ints(rng, (5, 6))
     add("p18_transposed_both", A=a, B=b, C=a.T @ b.T)
+
+    # kernels/5_...:47-71 matrix-scalar: C = A * s (B holds s); s = -5/2 keeps
+    # every product exact, the expected value is (-5 * A) / 2 in int64 first
+    a = ints(rng, (5, 7))
+    add("p05_scalar", A=a, B=np.array([-2.5], dtype=np.float32),
+        C=((-5 * a).astype(np.float64) / 2.0))
+
+    # kernels/87_...:451-492 pointwise (1x1) convolution, with bias:
+    # out[n,o,h,w] = sum_c weight[o,c] * input[n,c,h,w] + bias[o]
+    x, w, bias = ints(rng, (2, 5, 3, 4)), ints(rng, (6, 5, 1, 1)), ints(rng, (6,))
+    add("p87_pointwise", A=x, B=w, bias=bias,
+        C=np.einsum("oc,nchw->nohw", w[:, :, 0, 0], x) + bias[None, :, None, None])
 
     np.savez_compressed(OUT, **cases)
     print(f"wrote {OUT}: {len(cases) // 3} cases")

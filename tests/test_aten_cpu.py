@@ -30,6 +30,26 @@ CASES = [
 ]
 
 
+@pytest.mark.parametrize("A,msg", [
+    (_f(4, 4), "A must be a CUDA tensor"),                                  # 5_...:48
+])
+def test_matrix_scalar_messages(ck, A, msg):
+    with pytest.raises(RuntimeError, match=msg):
+        ck.p05.matrix_scalar_mult_cuda(A, 2.0)
+    with pytest.raises(RuntimeError, match=msg):
+        ck.ModelNew(5)(A, 2.0)
+
+
+@pytest.mark.parametrize("x,w,b,msg", [
+    (_f(2, 3, 4), _f(5, 3), None, "input must be 4D"),
+    (_f(2, 3, 4, 4), _f(5, 3, 3, 3), None, "weight must be"),
+    (_f(2, 3, 4, 4), _f(5, 3, 1, 1), None, "input must be a CUDA tensor"),
+])
+def test_pointwise_conv_checks(ck, x, w, b, msg):
+    with pytest.raises(RuntimeError, match=msg):
+        ck.p87.pointwise_conv_cuda(x, w, b)
+
+
 @pytest.mark.parametrize("sub,name,A,B,msg", CASES)
 def test_reference_error_messages(ck, sub, name, A, B, msg):
     fn = getattr(getattr(ck, sub), name)
@@ -54,12 +74,13 @@ def test_dtype_is_checked(ck):
 
 
 def test_model_new_registry(ck):
-    assert ck.PIDS == (1, 2, 3, 4, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18)
+    assert ck.PIDS == tuple(range(1, 19)) + (87,)
     for pid in ck.PIDS:
         m = ck.ModelNew(pid)
         assert isinstance(m, torch.nn.Module) and ck.OPS[pid][1] in repr(m)
-    with pytest.raises(ValueError):
-        ck.ModelNew(5)   # matrix-scalar is not part of this path
+    for pid in (0, 19, 86, 97):
+        with pytest.raises(ValueError):
+            ck.ModelNew(pid)
 
 
 def test_package_refuses_to_load_without_extension(tmp_path):

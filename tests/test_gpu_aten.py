@@ -89,7 +89,7 @@ def test_model_new_wrappers(ck, orc, dev):
     out = ck.ModelNew(2)(to_dev(a), to_dev(b))
     assert_close(orc, to_host(out), orc.gemm(a, b), 48, what="ModelNew(2)")
     with pytest.raises(ValueError):
-        ck.ModelNew(5)
+        ck.ModelNew(97)
 
 
 def test_zero_size_inputs(ck, dev):
@@ -115,6 +115,66 @@ def test_runs_on_current_stream(ck, orc, dev):
     assert_close(orc, C.cpu().numpy(), orc.gemm(a, b), 256, what="side stream")
 
 
+def test_matrix_scalar_operator(ck, orc, dev):
+    """PID 5 matrix_scalar_mult_cuda(A, float s) (kernels/5_...:47-71): the
+    output is empty_like(A) (any shape), bitwise the fp32 product, an empty A
+    returns an empty C, and the reference's three checks."""
+    a = _u(orc, (3, 50, 71), 30)
+    A = to_dev(a)
+    for fn in (lambda x: ck.p05.matrix_scalar_mult_cuda(x, 3.14),
+               lambda x: ck.ModelNew(5)(x, 3.14), lambda x: ck.ModelNew(5)(x, torch.tensor(3.14))):
+        C = fn(A)
+        assert C.shape == A.shape and C.dtype == torch.float32
+        np.testing.assert_array_equal(to_host(C).view(np.uint32), orc.scale(a, 3.14).view(np.uint32))
+    e = ck.p05.matrix_scalar_mult_cuda(torch.empty((0, 5), device="cuda"), 2.0)
+    assert tuple(e.shape) == (0, 5)
+    with pytest.raises(RuntimeError, match="A must be float32"):
+        ck.p05.matrix_scalar_mult_cuda(A.double(), 2.0)
+    with pytest.raises(RuntimeError, match="A must be contiguous"):
+        ck.p05.matrix_scalar_mult_cuda(A.transpose(1, 2), 2.0)
+
+
+@pytest.mark.parametrize("n,cin,cout,h,w,with_bias", [
+    (2, 3, 64, 17, 17, True),      # K = 3: element-load path, odd H*W
+    (4, 64, 128, 32, 32, True),    # single-slice K = 64
+    (4, 64, 128, 32, 32, False),
+    (1, 256, 96, 40, 40, True),    # several K slices
+    (2, 32, 2048, 64, 64, True),   # M = 2048: the A-panel kernel
+    (3, 0, 8, 5, 5, True),         # no input channels: out = bias
+    (3, 0, 8, 5, 5, False),        # ... or zeros
+])
+def test_pointwise_conv_operator(ck, orc, dev, n, cin, cout, h, w, with_bias):
+    """PID 87 pointwise_conv_cuda(input, weight, bias) (kernels/87_...:451-492)
+    against the fp64 oracle: output N x Cout x H x W, bias added once."""
+    x = _u(orc, (n, cin, h, w), 40)
+    wt = _u(orc, (cout, cin, 1, 1), 41)
+    b = _u(orc, (cout,), 42) if with_bias else None
+    out = ck.p87.pointwise_conv_cuda(to_dev(x), to_dev(wt), None if b is None else to_dev(b))
+    assert tuple(out.shape) == (n, cout, h, w)
+    ref = orc.pointwise_conv(x, wt, b)
+    if cin == 0:
+        np.testing.assert_array_equal(to_host(out), ref.astype(np.float32))
+    else:
+        assert_close(orc, to_host(out).reshape(-1), ref.reshape(-1), cin,
+                     what=f"conv {n}x{cin}x{cout}x{h}x{w} bias={with_bias}")
+    # ModelNew(87) and a 2-D weight give the same result
+    again = ck.ModelNew(87)(to_dev(x), to_dev(wt[:, :, 0, 0]), None if b is None else to_dev(b))
+    np.testing.assert_array_equal(to_host(again), to_host(out))
+
+
+def test_pointwise_conv_empty_and_checks(ck, dev):
+    out = ck.p87.pointwise_conv_cuda(torch.empty((0, 4, 3, 3), device="cuda"),
+                                     torch.empty((5, 4, 1, 1), device="cuda"))
+    assert tuple(out.shape) == (0, 5, 3, 3)
+    x = torch.zeros((1, 4, 3, 3), device="cuda")
+    with pytest.raises(RuntimeError, match="weight.size"):
+        ck.p87.pointwise_conv_cuda(x, torch.zeros((5, 3), device="cuda"))
+    with pytest.raises(RuntimeError, match="bias must have C_out"):
+        ck.p87.pointwise_conv_cuda(x, torch.zeros((5, 4), device="cuda"), torch.zeros(4, device="cuda"))
+    with pytest.raises(RuntimeError, match="float32"):
+        ck.p87.pointwise_conv_cuda(x.double(), torch.zeros((5, 4), device="cuda", dtype=torch.float64))
+
+
 def test_golden_fixtures_bitwise(ck, dev):
     """Every operator on the committed integer known-answer cases
     (tests/golden/gemm_family_int.npz): exact arithmetic, so bitwise equal."""
@@ -131,6 +191,9 @@ def test_golden_fixtures_bitwise(ck, dev):
         "p14_upper": ck.p14.upper_tri_matmul_cuda, "p15_lower": ck.p15.lower_tri_mul_cuda,
         "p16_transposed_a": ck.p16.matmul_transposed_cuda, "p17_transposed_b": ck.p17.matmul_cuda,
         "p18_transposed_both": ck.p18.matmul_transposed_cuda,
+        "p05_scalar": lambda A, B: ck.p05.matrix_scalar_mult_cuda(A, float(B[0])),
+        "p87_pointwise": lambda A, B: ck.p87.pointwise_conv_cuda(
+            A, B, to_dev(z["p87_pointwise.bias"])),
     }
     assert set(fn) == set(names)
     for name in names:

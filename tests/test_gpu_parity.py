@@ -239,6 +239,97 @@ def test_diag_mult_bitwise(ck, orc, dev, N, M):
     np.testing.assert_array_equal(to_host(out), orc.diag_mult(a, b))
 
 
+@pytest.mark.parametrize("n", [1, 3, 4, 5, 2047, 8192, 8192 * 4 + 3, (1 << 22) + 7,
+                               16384 * 4096])
+@pytest.mark.parametrize("misalign", [0, 1])
+def test_matrix_scalar_bitwise(ck, orc, dev, n, misalign):
+    """C = A * s (mi_matrix_scalar_mult_f32): one fp32 multiply per element, so
+    bitwise equal to the oracle, on the float4 path (chunk multiples, a partial
+    chunk, an n % 4 tail) and, with both pointers one float off 16-byte
+    alignment, on the scalar path."""
+    if misalign and n > (1 << 23):
+        pytest.skip("the scalar path is covered by the smaller sizes")
+    a = orc.uniform((n + misalign,), 93)
+    da = to_dev(a)
+    out = torch.empty((n + misalign,), device="cuda")
+    L = ck.abi.lib()
+    for s in (3.14159, -0.0, 2.0 ** -3):
+        out.fill_(7.0)
+        ck.abi.check(L.mi_matrix_scalar_mult_f32(ctypes.c_void_p(da.data_ptr() + 4 * misalign),
+                                                 ctypes.c_void_p(out.data_ptr() + 4 * misalign),
+                                                 n, s, cur_stream()))
+        got = to_host(out)
+        ref = orc.scale(a[misalign:], s)
+        np.testing.assert_array_equal(got[misalign:].view(np.uint32), ref.view(np.uint32),
+                                      err_msg=f"n={n} s={s}")
+        if misalign:
+            assert got[0] == 7.0  # nothing written before the array
+
+
+def test_matrix_scalar_zero_and_errors(ck, dev):
+    L = ck.abi.lib()
+    assert L.mi_matrix_scalar_mult_f32(None, None, 0, 2.0, cur_stream()) == 0
+    assert L.mi_matrix_scalar_mult_f32(None, None, -1, 2.0, cur_stream()) != 0
+    assert L.mi_matrix_scalar_mult_f32(None, None, 5, 2.0, cur_stream()) != 0
+
+
+@pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5, 6, 7])
+def test_row_bias_every_config(ck, orc, dev, cfg):
+    """mi_gemm_args.bias_m: C = A.B + bias[row], one add after the full sum, in
+    every tile config's epilogue (ragged M and N, so edge tiles too)."""
+    M, N, K = 300, 260, 32
+    a, b, bias = orc.uniform((M, K), 94), orc.uniform((K, N), 95), orc.uniform((M,), 96)
+    A, B, Bi = to_dev(a), to_dev(b), to_dev(bias)
+    C = torch.empty((M, N), device="cuda")
+    args = gemm_args(ck, A, B, C, M, N, K, override=cfg)
+    args.bias_m = Bi.data_ptr()
+    ck.abi.check(run_gemm(ck, args))
+    ref = orc.gemm(a, b) + bias.astype(np.float64)[:, None]
+    assert_close(orc, to_host(C), ref, K, what=f"bias cfg {cfg}")
+
+
+def test_row_bias_split_k_zero_k_and_batched(ck, orc, dev):
+    """bias with split-K (added once, in the reduction), with K = 0 (C = bias),
+    on a batched call, and rejected for triangular structure."""
+    M, N, K = 64, 48, 65536
+    a, b, bias = orc.uniform((M, K), 97), orc.uniform((K, N), 98), orc.uniform((M,), 99)
+    A, B, Bi = to_dev(a), to_dev(b), to_dev(bias)
+    C = torch.empty((M, N), device="cuda")
+    args = gemm_args(ck, A, B, C, M, N, K, override=3 | (16 << 8))
+    args.bias_m = Bi.data_ptr()
+    ws = workspace(ck, args)
+    args.workspace, args.workspace_bytes = ws.data_ptr(), ws.numel()
+    ck.abi.check(run_gemm(ck, args))
+    assert_close(orc, to_host(C), orc.gemm(a, b) + bias.astype(np.float64)[:, None], K,
+                 what="bias split-K")
+
+    C0 = torch.full((M, N), 5.0, device="cuda")
+    args0 = gemm_args(ck, A, B, C0, M, N, 0)
+    args0.bias_m = Bi.data_ptr()
+    ck.abi.check(run_gemm(ck, args0))
+    np.testing.assert_array_equal(to_host(C0), np.broadcast_to(bias[:, None], (M, N)))
+
+    nb, Mb, Nb, Kb = 3, 70, 90, 40
+    a3, b3 = orc.uniform((nb, Mb, Kb), 100), orc.uniform((nb, Kb, Nb), 101)
+    bias3 = orc.uniform((Mb,), 102)
+    A3, B3, Bi3 = to_dev(a3), to_dev(b3), to_dev(bias3)
+    C3 = torch.empty((nb, Mb, Nb), device="cuda")
+    args3 = gemm_args(ck, A3, B3, C3, Mb, Nb, Kb, batch=nb, sa=Mb * Kb, sb=Kb * Nb, sc=Mb * Nb)
+    args3.bias_m = Bi3.data_ptr()
+    ck.abi.check(run_gemm(ck, args3))
+    assert_close(orc, to_host(C3), orc.gemm(a3, b3) + bias3.astype(np.float64)[None, :, None], Kb,
+                 what="bias batched")
+
+    T = torch.empty((64, 64), device="cuda")
+    argst = gemm_args(ck, T, T, T, 64, 64, 64, structure=1)
+    argst.bias_m = Bi.data_ptr()
+    assert run_gemm(ck, argst) != 0
+    for op_a, op_b in ((1, 0), (0, 1), (1, 1)):  # the bias epilogue is N/N only
+        argsl = gemm_args(ck, T, T, T, 64, 64, 64, op_a=op_a, op_b=op_b)
+        argsl.bias_m = Bi.data_ptr()
+        assert run_gemm(ck, argsl) != 0
+
+
 def test_named_entry_points(ck, orc, dev):
     """Every per-operator C entry point against the oracle on a moderate shape."""
     L = ck.abi.lib()

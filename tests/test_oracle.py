@@ -76,6 +76,8 @@ def _oracle_for(orc, name, A, B):
         return orc.gemm(A.reshape(-1, A.shape[-1]), B).reshape(A.shape[:-1] + (B.shape[1],))
     if name == "p12_diag":
         return orc.diag_mult(A, B)
+    if name == "p05_scalar":
+        return orc.scale(A, float(B[0]))
     if name == "p14_upper":
         return orc.gemm(A, B, orc.UPPER)
     if name == "p15_lower":
@@ -92,14 +94,17 @@ def _oracle_for(orc, name, A, B):
 def test_golden_fixtures_cover_every_pid():
     _, names = _golden()
     pids = sorted(int(n[1:3]) for n in names)
-    assert pids == [1, 2, 3, 4, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18]
+    assert pids == list(range(1, 19)) + [87]
 
 
 @pytest.mark.parametrize("name", _golden()[1])
 def test_oracle_matches_golden_exactly(orc, name):
     z, _ = _golden()
     A, B, C = z[f"{name}.A"], z[f"{name}.B"], z[f"{name}.C"]
-    got = _oracle_for(orc, name, A, B)
+    if name == "p87_pointwise":
+        got = orc.pointwise_conv(A, B, z[f"{name}.bias"])
+    else:
+        got = _oracle_for(orc, name, A, B)
     np.testing.assert_array_equal(np.asarray(got, dtype=np.float64), C.astype(np.float64))
 
 
@@ -158,6 +163,64 @@ def test_gemv_and_generated_rows(orc):
 def test_diag_is_one_fp32_multiply(orc):
     a, b = orc.uniform((33,), 21), orc.uniform((33, 19), 22)
     np.testing.assert_array_equal(orc.diag_mult(a, b), a[:, None] * b)
+
+
+def test_scale_pins(orc):
+    """C = A * s (kernels/5_...:10-42): powers of two are exact (ldexp), s = 1
+    is the identity, s = -1 flips every sign bit, s = 0 gives zeros carrying
+    the sign of A, and a non-finite A stays non-finite.  A planted mistake (s
+    applied twice, an off-by-one element) fails these."""
+    a = orc.uniform((1001,), 24)
+    bits = lambda x: np.asarray(x, dtype=np.float32).view(np.uint32)
+    for e in (-3, 0, 5):
+        np.testing.assert_array_equal(orc.scale(a, 2.0 ** e), np.ldexp(a, e).astype(np.float32))
+    np.testing.assert_array_equal(bits(orc.scale(a, 1.0)), bits(a))
+    np.testing.assert_array_equal(bits(orc.scale(a, -1.0)), bits(a) ^ np.uint32(0x80000000))
+    z = orc.scale(a, 0.0)
+    np.testing.assert_array_equal(np.signbit(z), np.signbit(a))
+    assert not np.any(z)
+    special = np.array([np.inf, -np.inf, np.nan, 1.0], dtype=np.float32)
+    out = orc.scale(special, 0.0)
+    assert np.isnan(out[:3]).all() and out[3] == 0.0
+    # shape-preserving, 2-D input (the operator's output is empty_like(A))
+    m = orc.uniform((17, 9), 25)
+    assert orc.scale(m, 3.0).shape == (17, 9)
+    wrong = orc.scale(orc.scale(m, 3.0), 3.0)  # planted: s applied twice
+    assert not np.array_equal(wrong, orc.scale(m, 3.0))
+
+
+def test_pointwise_conv_pins(orc):
+    """1x1 convolution (kernels/87_...:451-492) against numpy float64 einsum
+    (independent), the identity weight (out = x + bias exactly), a zero weight
+    (out = bias broadcast), and planted mistakes: weight transposed, bias
+    dropped, bias added per input channel instead of once."""
+    x = orc.uniform((3, 7, 5, 6), 26)
+    w = orc.uniform((9, 7, 1, 1), 27)
+    b = orc.uniform((9,), 28)
+    ref = np.einsum("oc,nchw->nohw", w[:, :, 0, 0].astype(np.float64), x.astype(np.float64))
+    ref += b.astype(np.float64)[None, :, None, None]
+    got = orc.pointwise_conv(x, w, b)
+    assert got.shape == (3, 9, 5, 6)
+    assert np.max(np.abs(got - ref)) <= 1e-12
+    # a Cout x Cin weight and its Cout x Cin x 1 x 1 form are the same operator
+    np.testing.assert_array_equal(orc.pointwise_conv(x, w[:, :, 0, 0], None),
+                                  orc.pointwise_conv(x, w, None))
+    eye = np.eye(7, dtype=np.float32)
+    bi = orc.uniform((7,), 29)
+    np.testing.assert_array_equal(orc.pointwise_conv(x, eye, bi),
+                                  x.astype(np.float64) + bi.astype(np.float64)[None, :, None, None])
+    z = orc.pointwise_conv(x, np.zeros((9, 7), np.float32), b)
+    np.testing.assert_array_equal(z, np.broadcast_to(b.astype(np.float64)[None, :, None, None], z.shape))
+    sq = orc.uniform((7, 7), 30)
+    planted = [
+        orc.pointwise_conv(x, sq.T.copy(), None),                 # transposed weight
+        orc.pointwise_conv(x, sq, None),                          # bias dropped
+        orc.pointwise_conv(x, sq, bi) + 6 * bi.astype(np.float64)[None, :, None, None],  # bias per channel
+    ]
+    want = np.einsum("oc,nchw->nohw", sq.astype(np.float64), x.astype(np.float64)) + \
+        bi.astype(np.float64)[None, :, None, None]
+    for bad in planted:
+        assert np.max(np.abs(bad - want)) > 1e-3
 
 
 # ---- closed forms ------------------------------------------------------------------
