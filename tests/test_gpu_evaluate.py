@@ -1,0 +1,24 @@
+"""GPU test of the evaluation runner on its small preset: every operator runs
+beside its torch eager counterpart, agrees with it within the north-star
+bound, and the reference-schema table is written."""
+import csv
+import importlib
+import math
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def test_runner_small_preset(ck, dev, tmp_path):
+    ev = importlib.import_module(ck.__name__ + ".evaluate")
+    rows = ev.run(preset="small", warmup=1, reps=2, log=lambda m: print(m, flush=True))
+    assert sorted(r["Problem_ID"] for r in rows) == sorted(ck.PIDS)
+    for r in rows:
+        for k in ("Target_PyTorch_Latency(ms)", "Generated_Kernel_Latency(ms)", "Ratio_to_Target"):
+            assert math.isfinite(r[k]) and r[k] > 0, (r["Problem_ID"], k)
+        assert r["Max_Norm_Diff_vs_Torch"] <= 1e-4, r
+    out = tmp_path / "latency.csv"
+    ev.write_csv(rows, str(out))
+    table = list(csv.DictReader(open(out)))
+    assert len(table) == len(rows) and list(table[0].keys()) == ev.HEADER
