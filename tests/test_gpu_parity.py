@@ -126,6 +126,26 @@ def test_split_k_partition_and_determinism(ck, orc, dev, split, cfg):
         np.testing.assert_array_equal(o, outs[0])
 
 
+@pytest.mark.parametrize("M,N,K,batch", [(300, 520, 1056, 1), (257, 255, 2048, 1), (513, 260, 1024, 3),
+                                         (256, 256, 4096, 1)])
+def test_direct_staging_nn(ck, orc, dev, M, N, K, batch):
+    """The 256-tile N/N path with global->LDS direct loads (K % 32 == 0,
+    K >= 1024): edge rows and columns are loaded from the last valid
+    row/column and must not leak into stored outputs; batched and biased."""
+    a = orc.uniform((batch, M, K), 131)
+    b = orc.uniform((batch, K, N), 132)
+    bias = orc.uniform((M,), 133)
+    A, B, Bi = to_dev(a), to_dev(b), to_dev(bias)
+    for with_bias in (False, True):
+        C = torch.full((batch, M, N), float("nan"), device="cuda")
+        args = gemm_args(ck, A, B, C, M, N, K, batch=batch, sa=M * K, sb=K * N, sc=M * N, override=3)
+        if with_bias:
+            args.bias_m = Bi.data_ptr()
+        ck.abi.check(run_gemm(ck, args))
+        ref = orc.gemm(a, b) + (bias.astype(np.float64)[None, :, None] if with_bias else 0.0)
+        assert_close(orc, to_host(C), ref, K, what=f"direct {M}x{N}x{K}x{batch} bias={with_bias}")
+
+
 def test_split_k_without_workspace_is_rejected(ck, dev):
     M, N, K = 64, 64, 8192
     A = torch.zeros((M, K), device="cuda")
