@@ -28,6 +28,7 @@ import time
 REPO = os.path.dirname(os.path.abspath(__file__))
 METRIC = "fp32 TFLOP/s (% MFMA peak) @8192³ GEMM; GB/s (% HBM peak) on GEMV"
 PEAK_TFLOPS = 157.3   # MI355X dense fp32 MFMA
+PEAK_FP16_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E
 N = 8192
 GEMV_M, GEMV_K = 32768, 65536
@@ -101,11 +102,11 @@ def run_configs(ck, fill, dev, stream):
     import torch
     res = {}
 
-    def rec(name, ms, flops=None, nbytes=None):
+    def rec(name, ms, flops=None, nbytes=None, peak=PEAK_TFLOPS):
         r = {"ms": round(ms, 4)}
         if flops is not None:
             r["tflops"] = round(flops / (ms * 1e-3) / 1e12, 2)
-            r["frac_mfma"] = round(r["tflops"] / PEAK_TFLOPS, 4)
+            r["frac_mfma"] = round(r["tflops"] / peak, 4)
         if nbytes is not None:
             r["gbps"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
             r["frac_hbm"] = round(r["gbps"] / PEAK_HBM_GBS, 4)
@@ -149,6 +150,15 @@ def run_configs(ck, fill, dev, stream):
         _time(lambda i: ck.p87.pointwise_conv_cuda(X, W, Bi), stream, 10, 2),
         2 * 16 * 128 * 64 * 65536, 4 * (16 * 64 * 65536 + 128 * 64 + 128 + 16 * 128 * 65536))
     del X, W, Bi
+    # PID 97 attention (no BASELINE config): fp16 Q, K, V of 32 x 32 heads x
+    # 512 x 1024 (the reference's limits); algorithmic 4 B H S^2 E flops against
+    # the fp16 dense MFMA peak
+    at = (32, 32, 512, 1024)
+    Q, Kt, V = (u(at, 62 + i).half() for i in range(3))
+    rec("attention_fp16_32x32x512x1024", _time(lambda i: ck.p97.fused_attention_cuda(Q, Kt, V), stream, 5, 2),
+        4.0 * at[0] * at[1] * at[2] ** 2 * at[3], None, PEAK_FP16_TFLOPS)
+    del Q, Kt, V
+    torch.cuda.empty_cache()
     A, B = u((256, 1 << 20), 64), u((1 << 20, 256), 65)
     rec("large_k_256x256x1048576", _time(lambda i: ck.p06.matmul_cuda(A, B), stream, 10, 2),
         2 * 256 * 256 * (1 << 20))

@@ -1,6 +1,6 @@
 """MI355X (gfx950) GEMM-family operators: a drop-in for the GEMM path of
-champloo2878/cuPilot-Kernels (kernels/1..18) and its pointwise convolution
-(kernels/87).
+champloo2878/cuPilot-Kernels (kernels/1..18), its pointwise convolution
+(kernels/87) and its scaled dot-product attention (kernels/97).
 
     import torch
     from __graft_entry__ import load_package
@@ -34,6 +34,6 @@ p01, p02, p03, p04, p05 = _C.p01, _C.p02, _C.p03, _C.p04, _C.p05
 p06, p07, p08, p09 = _C.p06, _C.p07, _C.p08, _C.p09
 p10, p11, p12, p13 = _C.p10, _C.p11, _C.p12, _C.p13
 p14, p15, p16, p17, p18 = _C.p14, _C.p15, _C.p16, _C.p17, _C.p18
-p87 = _C.p87
+p87, p97 = _C.p87, _C.p97
 
 __version__ = _C.version()

@@ -22,6 +22,7 @@ MI_ERR_BAD_LD = -4
 MI_ERR_NOT_SQUARE = -5
 MI_ERR_WORKSPACE = -6
 MI_ERR_NO_DEVICE = -7
+MI_ERR_ALIGNMENT = -8
 
 MI_OP_N, MI_OP_T = 0, 1
 MI_DENSE, MI_LOWER, MI_UPPER = 0, 1, 2
@@ -78,6 +79,8 @@ SIGNATURES = {
     "mi_diag_mult_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _vp]),
     "mi_matrix_scalar_mult_f32": (ctypes.c_int, [_vp, _vp, _i64, ctypes.c_float, _vp]),
     "mi_pointwise_conv_f32": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
+    "mi_sdpa_workspace_bytes": (_sz, [_i64, _i64, _i64]),
+    "mi_sdpa_f16": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _sz, _vp]),
     "mi_symmetric_matmul_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _vp]),
     "mi_upper_tri_matmul_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _vp]),
     "mi_lower_tri_mul_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _vp]),

@@ -80,6 +80,7 @@ const char* mi_status_string(int status) {
         case MI_ERR_NOT_SQUARE: return "structured (triangular) product needs square operands";
         case MI_ERR_WORKSPACE: return "workspace missing or too small";
         case MI_ERR_NO_DEVICE: return "no HIP device available";
+        case MI_ERR_ALIGNMENT: return "pointer not 16-byte aligned";
         default: break;
     }
     if (status > 0) return hipGetErrorString(static_cast<hipError_t>(status));
@@ -293,6 +294,28 @@ int mi_pointwise_conv_f32(const float* input, const float* weight, const float* 
     a.stride_c = out_channels * hw;
     a.bias_m = bias;
     return mi_gemm_f32(&a, stream);
+}
+
+size_t mi_sdpa_workspace_bytes(int64_t batch_heads, int64_t seq, int64_t embed) {
+    if (batch_heads <= 0 || seq <= 0 || embed <= 0 || seq > 32768 || embed > 65536) return 0;
+    return sdpa_workspace_bytes(batch_heads, (int)seq, (int)embed);
+}
+
+int mi_sdpa_f16(const void* Q, const void* K, const void* V, void* O, int64_t batch_heads,
+                int64_t seq, int64_t embed, void* workspace, size_t workspace_bytes, void* stream) {
+    if (batch_heads < 0 || seq < 0 || embed < 0 || seq > 32768 || embed > 65536)
+        return MI_ERR_BAD_SIZE;
+    if (batch_heads == 0 || seq == 0 || embed == 0) return MI_OK;
+    if (embed % 64 != 0) return MI_ERR_BAD_SIZE;
+    if (!Q || !K || !V || !O) return MI_ERR_NULL_POINTER;
+    for (const void* p : {Q, K, V, static_cast<const void*>(O)})
+        if (((uintptr_t)p & 15u) != 0) return MI_ERR_ALIGNMENT;
+    if (!workspace || workspace_bytes < sdpa_workspace_bytes(batch_heads, (int)seq, (int)embed))
+        return MI_ERR_WORKSPACE;
+    if (((uintptr_t)workspace & 15u) != 0) return MI_ERR_ALIGNMENT;
+    return hip_rc(launch_sdpa(static_cast<const _Float16*>(Q), static_cast<const _Float16*>(K),
+                              static_cast<const _Float16*>(V), static_cast<_Float16*>(O), batch_heads,
+                              (int)seq, (int)embed, workspace, as_stream(stream)));
 }
 
 int mi_symmetric_matmul_f32(const float* A, const float* B, float* C, int64_t N, void* stream) {

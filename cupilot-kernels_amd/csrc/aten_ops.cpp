@@ -359,6 +359,33 @@ at::Tensor pointwise_conv(const at::Tensor& input, const at::Tensor& weight,
     return out;
 }
 
+// kernels/97_ScaledDotProductAttention_best_kernel.cu:256-296: Q, K, V are
+// (batch, heads, seq, embed) fp16; the reference's three checks (:267-269)
+// come first, then the ones its raw-pointer access assumes (shapes equal,
+// fp16, CUDA).  Output empty_like(Q); workspace from the caching allocator.
+at::Tensor fused_attention(const at::Tensor& Q, const at::Tensor& K, const at::Tensor& V) {
+    TORCH_CHECK(Q.dim() == 4, "Q must be 4D (batch, heads, seq, embed)");
+    const int64_t batch = Q.size(0), heads = Q.size(1), seq = Q.size(2), embed = Q.size(3);
+    TORCH_CHECK(seq <= 512, "Sequence length exceeds MAX_SEQ_LENGTH.");
+    TORCH_CHECK(embed == 1024, "Embedding dimension must be 1024.");
+    TORCH_CHECK(embed % 32 == 0, "Embedding dimension must be divisible by warp size.");
+    TORCH_CHECK(K.sizes() == Q.sizes() && V.sizes() == Q.sizes(), "Q, K and V must have the same shape");
+    for (const at::Tensor* t : {&Q, &K, &V}) {
+        TORCH_CHECK(t->is_cuda(), "Q, K and V must be CUDA tensors");
+        TORCH_CHECK(t->scalar_type() == at::kHalf, "Q, K and V must be float16");
+        TORCH_CHECK(t->device() == Q.device(), "Q, K and V must be on the same device");
+    }
+    at::Tensor out = at::empty_like(Q, at::MemoryFormat::Contiguous);
+    if (out.numel() == 0) return out;
+    at::Tensor q = Q.contiguous(), k = K.contiguous(), v = V.contiguous();
+    const size_t ws_bytes = mi_sdpa_workspace_bytes(batch * heads, seq, embed);
+    at::Tensor ws = at::empty({(int64_t)ws_bytes}, Q.options().dtype(at::kByte));
+    check_rc(mi_sdpa_f16(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), batch * heads, seq,
+                         embed, ws.data_ptr(), ws_bytes, current_stream(Q)),
+             "fused_attention_cuda");
+    return out;
+}
+
 // kernels/13_Matmul_for_symmetric_matrices_best_kernel.cu:134-151
 at::Tensor symmetric_matmul(const at::Tensor& A, const at::Tensor& B) {
     TORCH_CHECK(A.dim() == 2, "A must be 2D");
@@ -436,7 +463,7 @@ at::Tensor matmul_transposed_both(const at::Tensor& A, const at::Tensor& B) {
 // function name (the names collide across files: matmul_cuda is PIDs 1, 2, 6,
 // 8 and 17; matmul_transposed_cuda is 16 and 18; batched_matmul_cuda is 3 and 10).
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
-    m.doc() = "MI355X GEMM-family operators (drop-in for cuPilot-Kernels PIDs 1-18 and 87)";
+    m.doc() = "MI355X GEMM-family operators (drop-in for cuPilot-Kernels PIDs 1-18, 87 and 97)";
     struct Entry {
         const char* sub;
         const char* name;
@@ -470,6 +497,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
                                pybind11::arg("A"), pybind11::arg("s"));
     m.def_submodule("p87").def("pointwise_conv_cuda", &mi355::pointwise_conv, pybind11::arg("input"),
                                pybind11::arg("weight"), pybind11::arg("bias_opt") = pybind11::none());
+    // PID 97 takes (Q, K, V)
+    m.def_submodule("p97").def("fused_attention_cuda", &mi355::fused_attention, pybind11::arg("Q"),
+                               pybind11::arg("K"), pybind11::arg("V"));
     m.def("square_matmul", &mi355::square_matmul);
     m.def("matmul", &mi355::matmul);
     m.def("batched_matmul", &mi355::batched_matmul);
@@ -482,6 +512,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("diag_mult", &mi355::diag_mult);
     m.def("matrix_scalar_mult", &mi355::matrix_scalar_mult);
     m.def("pointwise_conv", &mi355::pointwise_conv);
+    m.def("fused_attention", &mi355::fused_attention);
     m.def("symmetric_matmul", &mi355::symmetric_matmul);
     m.def("upper_tri_matmul", &mi355::upper_tri_matmul);
     m.def("lower_tri_mul", &mi355::lower_tri_mul);

@@ -96,6 +96,13 @@ hipError_t launch_diag(const float* a, const float* B, float* out, int64_t N, in
                        hipStream_t s);
 hipError_t launch_scale(const float* A, float* C, int64_t n, float s, hipStream_t st);
 
+// scaled dot-product attention (attention.hip): heads per workspace chunk
+constexpr int64_t kSdpaChunkHeads = 128;
+int64_t sdpa_chunk_heads(int64_t heads);
+size_t sdpa_workspace_bytes(int64_t heads, int seq, int embed);
+hipError_t launch_sdpa(const _Float16* Q, const _Float16* K, const _Float16* V, _Float16* O,
+                       int64_t heads, int seq, int embed, void* ws, hipStream_t s);
+
 struct GemvPlan {
     int split_k;
     int k_chunk;

@@ -160,6 +160,15 @@ def _problems(ck, preset: str) -> List[Problem]:
                      4.0 * (cv[0] * cv[1] * cv[3] * cv[4] + cv[2] * cv[1] + cv[2]
                             + cv[0] * cv[2] * cv[3] * cv[4]),
                      k_norm=cv[1], note="synthetic (no BASELINE config)"))
+
+    at = (2, 2, 128, 1024) if small else (32, 32, 512, 1024)      # batch, heads, seq, embed
+
+    def make_attn(u):
+        return tuple(u(at, 1552 + i).half() for i in range(3))
+    P.append(Problem(97, "x".join(map(str, at)), make_attn, ck.p97.fused_attention_cuda,
+                     lambda q, k, v: F.scaled_dot_product_attention(q, k, v),
+                     4.0 * at[0] * at[1] * at[2] * at[2] * at[3], k_norm=1,
+                     note="fp16; shape within the reference's limits (seq <= 512, embed 1024)"))
     return P
 
 

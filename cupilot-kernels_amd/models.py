@@ -34,6 +34,7 @@ OPS = {
     17: ("p17", "matmul_cuda", "kernels/17_Matmul_with_transposed_B_best_kernel.cu"),
     18: ("p18", "matmul_transposed_cuda", "kernels/18_Matmul_with_transposed_both_best_kernel.cu"),
     87: ("p87", "pointwise_conv_cuda", "kernels/87_conv_pointwise_2D_best_kernel.cu"),
+    97: ("p97", "fused_attention_cuda", "kernels/97_ScaledDotProductAttention_best_kernel.cu"),
 }
 PIDS = tuple(sorted(OPS))
 
@@ -49,7 +50,8 @@ class ModelNew(torch.nn.Module):
     For PID 5 the second argument is the scalar ``s`` of
     ``matrix_scalar_mult_cuda(A, float s)`` (a Python number or a 0-d tensor).
     PID 87 is ``forward(input, weight, bias=None)`` of
-    ``pointwise_conv_cuda(input, weight, bias_opt)``.
+    ``pointwise_conv_cuda(input, weight, bias_opt)``; PID 97 is
+    ``forward(Q, K, V)`` of ``fused_attention_cuda(Q, K, V)``.
     """
 
     def __init__(self, pid: int):
@@ -59,11 +61,13 @@ class ModelNew(torch.nn.Module):
         self.pid = pid
         self._fn = op(pid)
 
-    def forward(self, A: torch.Tensor, B, bias=None) -> torch.Tensor:
+    def forward(self, A: torch.Tensor, B, C=None) -> torch.Tensor:
+        """C is the third input where the operator has one (PID 87's bias,
+        PID 97's V)."""
         if self.pid == 5:
             return self._fn(A, float(B))
-        if self.pid == 87:
-            return self._fn(A, B, bias)
+        if self.pid in (87, 97):
+            return self._fn(A, B, C)
         return self._fn(A, B)
 
     def extra_repr(self) -> str:

@@ -46,7 +46,8 @@ typedef enum {
     MI_ERR_BAD_LD = -4,         /* leading dimension smaller than the row */
     MI_ERR_NOT_SQUARE = -5,     /* structured op on a non-square problem */
     MI_ERR_WORKSPACE = -6,      /* workspace missing or too small */
-    MI_ERR_NO_DEVICE = -7       /* no HIP device / device query failed */
+    MI_ERR_NO_DEVICE = -7,      /* no HIP device / device query failed */
+    MI_ERR_ALIGNMENT = -8       /* a pointer is not 16-byte aligned where required */
 } mi_status;
 
 typedef enum { MI_OP_N = 0, MI_OP_T = 1 } mi_op;
@@ -187,6 +188,19 @@ MI_API int mi_matrix_scalar_mult_f32(const float* A, float* C, int64_t n, float 
 MI_API int mi_pointwise_conv_f32(const float* input, const float* weight, const float* bias,
                           float* output, int64_t batch, int64_t in_channels,
                           int64_t out_channels, int64_t hw, void* stream);
+
+/* kernels/97_ScaledDotProductAttention_best_kernel.cu:256 fused_attention_cuda
+ * (reference kernel :136-250): for each of batch_heads (batch x heads) heads,
+ *   O = softmax(Q . K^T / sqrt(embed)) . V
+ * with Q, K, V, O contiguous fp16 (IEEE binary16) arrays of batch_heads x seq
+ * x embed, fp32 arithmetic inside, one rounding to fp16 at the end.  embed
+ * must be a multiple of 64 and the four pointers 16-byte aligned.  The
+ * workspace (device memory, mi_sdpa_workspace_bytes) holds the scores and
+ * attention weights of up to 128 heads at a time. */
+MI_API size_t mi_sdpa_workspace_bytes(int64_t batch_heads, int64_t seq, int64_t embed);
+MI_API int mi_sdpa_f16(const void* Q, const void* K, const void* V, void* O, int64_t batch_heads,
+                int64_t seq, int64_t embed, void* workspace, size_t workspace_bytes,
+                void* stream);
 
 /* kernels/13_Matmul_for_symmetric_matrices_best_kernel.cu:134
  * symmetric_matmul_cuda: C = A . B for symmetric N x N A and B.  The kernel

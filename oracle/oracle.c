@@ -34,6 +34,12 @@
  *                     weight indexed out_c * in_channels + c at :308,:321, bias
  *                     optional at :452) and :373-388 (bias added once after the
  *                     channel sum)
+ *   orc_half_to_double / orc_sdpa_f64
+ *                     out = softmax(q.k^T * scale) . v per head, in fp64 from
+ *                     binary16 inputs -- kernels/97_...:256-296 (wrapper: Q, K, V
+ *                     batch x heads x seq x embed fp16, scale 1/sqrt(embed)
+ *                     at :275, output empty_like(Q)) and :136-250 (scores, row
+ *                     softmax with max subtraction, weighted sum of V rows)
  *   orc_fill_uniform_f32 / orc_fill_int_f32
  *                     counter-based splitmix64 input generator shared with the
  *                     device fill kernel, so any element can be regenerated on
@@ -233,6 +239,47 @@ ORC_EXPORT void orc_pointwise_conv_f64(const float* x, const float* w, const flo
             }
             if (bias)
                 for (int64_t p = 0; p < hw; ++p) dst[p] += (double)bias[o];
+        }
+}
+
+/* IEEE binary16 bit pattern -> double (normal, subnormal, zero, inf, NaN). */
+ORC_EXPORT double orc_half_to_double(uint16_t h) {
+    const int sign = h >> 15, exp = (h >> 10) & 0x1F, frac = h & 0x3FF;
+    double v;
+    if (exp == 0) v = ldexp((double)frac, -24);
+    else if (exp == 31) v = frac ? NAN : INFINITY;
+    else v = ldexp((double)(frac | 0x400), exp - 25);
+    return sign ? -v : v;
+}
+
+ORC_EXPORT void orc_sdpa_f64(const uint16_t* q, const uint16_t* k, const uint16_t* v, double* out,
+                             int64_t heads, int64_t seq, int64_t embed, double scale) {
+#pragma omp parallel for collapse(2) schedule(dynamic, 4)
+    for (int64_t h = 0; h < heads; ++h)
+        for (int64_t i = 0; i < seq; ++i) {
+            const uint16_t* qi = q + (h * seq + i) * embed;
+            double* s = (double*)malloc((size_t)seq * sizeof(double));
+            double mx = -INFINITY;
+            for (int64_t j = 0; j < seq; ++j) {
+                const uint16_t* kj = k + (h * seq + j) * embed;
+                double d = 0.0;
+                for (int64_t e = 0; e < embed; ++e) d += orc_half_to_double(qi[e]) * orc_half_to_double(kj[e]);
+                s[j] = d * scale;
+                if (s[j] > mx) mx = s[j];
+            }
+            double sum = 0.0;
+            for (int64_t j = 0; j < seq; ++j) {
+                s[j] = exp(s[j] - mx);
+                sum += s[j];
+            }
+            double* o = out + (h * seq + i) * embed;
+            for (int64_t e = 0; e < embed; ++e) o[e] = 0.0;
+            for (int64_t j = 0; j < seq; ++j) {
+                const double w = s[j] / sum;
+                const uint16_t* vj = v + (h * seq + j) * embed;
+                for (int64_t e = 0; e < embed; ++e) o[e] += w * orc_half_to_double(vj[e]);
+            }
+            free(s);
         }
 }
 

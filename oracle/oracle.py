@@ -56,6 +56,10 @@ def lib():
         L.orc_diag_f32.argtypes = [_f32p, _f32p, _f32p, _i64, _i64]
         L.orc_scale_f32.argtypes = [_f32p, _f32p, _i64, ctypes.c_float]
         L.orc_pointwise_conv_f64.argtypes = [_f32p, _f32p, _f32p, _f64p, _i64, _i64, _i64, _i64]
+        L.orc_half_to_double.argtypes = [ctypes.c_uint16]
+        L.orc_half_to_double.restype = ctypes.c_double
+        _u16p = ctypes.POINTER(ctypes.c_uint16)
+        L.orc_sdpa_f64.argtypes = [_u16p, _u16p, _u16p, _f64p, _i64, _i64, _i64, ctypes.c_double]
         L.orc_max_abs_diff.restype = ctypes.c_double
         L.orc_max_abs_diff.argtypes = [_f32p, _f64p, _i64]
         L.orc_num_threads.restype = ctypes.c_int
@@ -220,6 +224,28 @@ def pointwise_conv(x: np.ndarray, w: np.ndarray, bias: Optional[np.ndarray] = No
     lib().orc_pointwise_conv_f64(_fp(x), _fp(w2), None if b is None else _fp(b), _dp(out),
                                  n, cin, cout, h * wd)
     return out
+
+
+def sdpa(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: Optional[float] = None) -> np.ndarray:
+    """fp64 scaled dot-product attention (kernels/97_...:136-296) of float16
+    arrays (..., seq, embed); returns float64 of the same shape.  scale
+    defaults to 1/sqrt(embed) (kernels/97_...:275)."""
+    q, k, v = (np.ascontiguousarray(x, dtype=np.float16) for x in (q, k, v))
+    assert q.shape == k.shape == v.shape
+    seq, embed = q.shape[-2:]
+    heads = int(np.prod(q.shape[:-2])) if q.ndim > 2 else 1
+    out = np.empty(q.shape, dtype=np.float64)
+    u16 = ctypes.POINTER(ctypes.c_uint16)
+    lib().orc_sdpa_f64(q.ctypes.data_as(u16), k.ctypes.data_as(u16), v.ctypes.data_as(u16), _dp(out),
+                       heads, seq, embed, (1.0 / math.sqrt(embed)) if scale is None else scale)
+    return out
+
+
+def half_ulp(x: np.ndarray) -> np.ndarray:
+    """Spacing of IEEE binary16 values at |x| (subnormal spacing 2^-24 below 2^-14)."""
+    ax = np.abs(np.asarray(x, dtype=np.float64))
+    e = np.floor(np.log2(np.maximum(ax, 2.0 ** -14)))
+    return np.exp2(e - 10)
 
 
 # ---- tolerance ----------------------------------------------------------------

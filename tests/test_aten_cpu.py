@@ -50,6 +50,21 @@ def test_pointwise_conv_checks(ck, x, w, b, msg):
         ck.p87.pointwise_conv_cuda(x, w, b)
 
 
+def _h(*shape):
+    return torch.zeros(shape, dtype=torch.float16)
+
+
+@pytest.mark.parametrize("q,msg", [
+    (_h(1, 1, 600, 1024), "Sequence length exceeds MAX_SEQ_LENGTH."),      # 97_...:267
+    (_h(1, 1, 64, 512), "Embedding dimension must be 1024."),              # 97_...:268
+    (_h(64, 1024), "must be 4D"),
+    (_h(1, 1, 64, 1024), "CUDA tensors"),
+])
+def test_fused_attention_checks(ck, q, msg):
+    with pytest.raises(RuntimeError, match=msg):
+        ck.p97.fused_attention_cuda(q, q, q)
+
+
 @pytest.mark.parametrize("sub,name,A,B,msg", CASES)
 def test_reference_error_messages(ck, sub, name, A, B, msg):
     fn = getattr(getattr(ck, sub), name)
@@ -74,11 +89,11 @@ def test_dtype_is_checked(ck):
 
 
 def test_model_new_registry(ck):
-    assert ck.PIDS == tuple(range(1, 19)) + (87,)
+    assert ck.PIDS == tuple(range(1, 19)) + (87, 97)
     for pid in ck.PIDS:
         m = ck.ModelNew(pid)
         assert isinstance(m, torch.nn.Module) and ck.OPS[pid][1] in repr(m)
-    for pid in (0, 19, 86, 97):
+    for pid in (0, 19, 86, 98):
         with pytest.raises(ValueError):
             ck.ModelNew(pid)
 

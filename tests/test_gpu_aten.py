@@ -89,7 +89,7 @@ def test_model_new_wrappers(ck, orc, dev):
     out = ck.ModelNew(2)(to_dev(a), to_dev(b))
     assert_close(orc, to_host(out), orc.gemm(a, b), 48, what="ModelNew(2)")
     with pytest.raises(ValueError):
-        ck.ModelNew(97)
+        ck.ModelNew(98)
 
 
 def test_zero_size_inputs(ck, dev):

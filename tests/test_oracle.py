@@ -223,6 +223,64 @@ def test_pointwise_conv_pins(orc):
         assert np.max(np.abs(bad - want)) > 1e-3
 
 
+def test_half_decoder_exhaustive(orc):
+    """orc_half_to_double on all 65536 binary16 patterns equals numpy's
+    float16 -> float64 conversion (NaN patterns decode to NaN)."""
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    want = bits.view(np.float16).astype(np.float64)
+    f = orc.lib().orc_half_to_double
+    got = np.array([f(int(b)) for b in bits], dtype=np.float64)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    np.testing.assert_array_equal(got[~nan], want[~nan])
+
+
+def _np_sdpa(q, k, v, scale):
+    q, k, v = (x.astype(np.float64) for x in (q, k, v))
+    s = np.matmul(q, np.swapaxes(k, -1, -2)) * scale
+    s -= s.max(axis=-1, keepdims=True)
+    w = np.exp(s)
+    w /= w.sum(axis=-1, keepdims=True)
+    return np.matmul(w, v)
+
+
+def test_sdpa_pins(orc):
+    """Attention (kernels/97_...:136-296) against an independent numpy float64
+    implementation, the closed forms of identical keys (uniform weights: the
+    mean of V) and of one dominant key (its V row), and planted mistakes
+    (no scale, softmax over queries, V transposed per head)."""
+    shape = (2, 3, 9, 16)
+    q = orc.uniform(shape, 31).astype(np.float16)
+    k = orc.uniform(shape, 32).astype(np.float16)
+    v = orc.uniform(shape, 33).astype(np.float16)
+    scale = 1.0 / 4.0
+    got = orc.sdpa(q, k, v)
+    ref = _np_sdpa(q, k, v, scale)
+    assert got.shape == shape and np.max(np.abs(got - ref)) <= 1e-12
+    same_k = np.broadcast_to(k[:, :, :1, :], shape).copy()
+    np.testing.assert_allclose(orc.sdpa(q, same_k, v), np.broadcast_to(
+        v.astype(np.float64).mean(axis=-2, keepdims=True), shape), rtol=0, atol=1e-12)
+    # one key aligned with every query and 8x longer: its weight -> 1
+    k1 = np.zeros((1, 1, 4, 16), np.float16)
+    k1[0, 0, 2, 0] = 8.0
+    q1 = np.zeros((1, 1, 4, 16), np.float16)
+    q1[..., 0] = 8.0
+    v1 = orc.uniform((1, 1, 4, 16), 34).astype(np.float16)
+    o1 = orc.sdpa(q1, k1, v1, scale=1.0)
+    np.testing.assert_allclose(o1, np.broadcast_to(v1[0, 0, 2].astype(np.float64), o1.shape), atol=1e-12)
+    planted = [_np_sdpa(q, k, v, 1.0),
+               np.swapaxes(_np_sdpa(np.swapaxes(q, -1, -2), np.swapaxes(k, -1, -2),
+                                    np.swapaxes(v, -1, -2), scale), -1, -2),
+               _np_sdpa(q, k, np.swapaxes(v[..., :9, :9], -1, -2).copy(), scale)]
+    for bad in planted:
+        assert bad.shape != got.shape or np.max(np.abs(bad - got)) > 1e-3
+
+
+def test_half_ulp(orc):
+    np.testing.assert_array_equal(orc.half_ulp(np.array([1.0, 1.5, 2.0, 0.04, 0.0, 2.0 ** -20])),
+                                  [2.0 ** -10, 2.0 ** -10, 2.0 ** -9, 2.0 ** -15, 2.0 ** -24, 2.0 ** -24])
+
+
 # ---- closed forms ------------------------------------------------------------------
 
 def test_closed_forms(orc):
