@@ -17,7 +17,10 @@ def test_runner_small_preset(ck, dev, tmp_path):
     for r in rows:
         for k in ("Target_PyTorch_Latency(ms)", "Generated_Kernel_Latency(ms)", "Ratio_to_Target"):
             assert math.isfinite(r[k]) and r[k] > 0, (r["Problem_ID"], k)
-        assert r["Max_Norm_Diff_vs_Torch"] <= 1e-4, r
+        # fp32 problems: the north-star bound; PID 97 returns fp16, and torch's
+        # fp16 attention differs from it by a few binary16 spacings (2^-10 at |O| ~ 1)
+        bound = 4 * 2.0 ** -10 if r["Problem_ID"] == 97 else 1e-4
+        assert r["Max_Norm_Diff_vs_Torch"] <= bound, r
     out = tmp_path / "latency.csv"
     ev.write_csv(rows, str(out))
     table = list(csv.DictReader(open(out)))
