@@ -9,9 +9,10 @@
 //                                        fp32 accumulation and output
 //   2. P = softmax_rows(S)               fp32, written as two scaled fp16 terms
 //                                        2^14 P = H + 2^-11 L, side by side
-//   3. Vt2 = [V^T | V^T]                 E x 2*Sp (zero padded to Sp keys)
-//   4. O = 2^-14 (H.V + 2^-11 L.V)       fp16 MFMA over [H | L] . Vt2^T, fp32
-//                                        accumulation, fp16 out
+//   3. Vt = V^T                          E x Sp (zero padded to Sp keys)
+//   4. O = 2^-14 (H.V + 2^-11 L.V)       fp16 MFMA over [H | L] . [Vt | Vt]^T
+//                                        (the B operand wraps around Vt),
+//                                        fp32 accumulation, fp16 out
 // Step 4 is one contraction of depth 2*Sp whose accumulator is multiplied by
 // 2^11 where the H half ends, so the attention weights keep ~22 bits
 // (fp32-like) although the MFMA takes fp16.  The 2^14 and 2^11 scalings keep
@@ -53,6 +54,7 @@ struct HgemmParams {
     int tiles_n;
     int k_switch;         // slice index at which the accumulator is multiplied by switch_mul
     float switch_mul;
+    int b_kwrap;          // > 0: B holds K / 2 columns, read twice (k -> k - b_kwrap past it)
     int64_t lda, ldb, ldc;
     int64_t sa, sb, sc;   // batch strides (elements)
     float alpha;
@@ -78,13 +80,14 @@ __global__ void __launch_bounds__(kHgThreads) __attribute__((amdgpu_waves_per_eu
     constexpr int NS = kHgBM * (kHgBK / 8) / kHgThreads;
     h8 ra[NS], rb[NS];
     auto load = [&](int k0) {
+        const int kb0 = (p.b_kwrap > 0 && k0 >= p.b_kwrap) ? k0 - p.b_kwrap : k0;
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
             const int c = tid + s * kHgThreads;
             const int row = c >> 3, kc = (c & 7) * 8;
             const int am = m0 + row, bn = n0 + row;
             ra[s] = am < p.M ? *reinterpret_cast<const h8*>(A + (int64_t)am * p.lda + k0 + kc) : h8{};
-            rb[s] = bn < p.N ? *reinterpret_cast<const h8*>(B + (int64_t)bn * p.ldb + k0 + kc) : h8{};
+            rb[s] = bn < p.N ? *reinterpret_cast<const h8*>(B + (int64_t)bn * p.ldb + kb0 + kc) : h8{};
         }
     };
     auto store = [&](int buf) {
@@ -170,8 +173,10 @@ __global__ void __launch_bounds__(kHgThreads) __attribute__((amdgpu_waves_per_eu
 // ---------------------------------------------------------------------------
 // Row softmax with the two-term fp16 split.  One wave per row of S (n values,
 // row stride lds floats); writes the P' row (2 * sp halves) [H | 0 pad | L | 0 pad]
-// with 2^14 p = H + 2^-11 L.
+// with 2^14 p = H + 2^-11 L.  Rows up to 64 * VPL values stay in registers
+// (one read of S); longer rows take three passes over S.
 // ---------------------------------------------------------------------------
+template <int VPL>
 __global__ void __launch_bounds__(256)
     softmax_split_kernel(const float* __restrict__ S, _Float16* __restrict__ P, int64_t rows, int n,
                          int sp, int64_t lds) {
@@ -180,6 +185,39 @@ __global__ void __launch_bounds__(256)
     if (row >= rows) return;
     const float* s = S + row * lds;
     _Float16* out = P + row * (2 * (int64_t)sp);
+    auto emit = [&](int c, float e, float scale) {
+        const float pv = e * scale;  // 2^14 p <= 2^14
+        const _Float16 hi = (_Float16)pv;
+        out[c] = hi;
+        out[sp + c] = (_Float16)((pv - (float)hi) * 2048.0f);
+    };
+    if (VPL > 0) {
+        float x[VPL > 0 ? VPL : 1];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            const int c = lane + 64 * i;
+            x[i] = c < n ? s[c] : -INFINITY;
+            mx = fmaxf(mx, x[i]);
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+        float sum = 0.f;
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            x[i] = lane + 64 * i < n ? expf(x[i] - mx) : 0.f;
+            sum += x[i];
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+        const float scale = 16384.0f / sum;
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            const int c = lane + 64 * i;
+            if (c < sp) emit(c, x[i], scale);
+        }
+        return;
+    }
     float mx = -INFINITY;
     for (int c = lane; c < n; c += 64) mx = fmaxf(mx, s[c]);
 #pragma unroll
@@ -188,29 +226,21 @@ __global__ void __launch_bounds__(256)
     for (int c = lane; c < n; c += 64) sum += expf(s[c] - mx);
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
-    const float inv = 1.0f / sum;
-    for (int c = lane; c < sp; c += 64) {
-        float pv = 0.f;
-        if (c < n) pv = expf(s[c] - mx) * inv * 16384.0f;  // 2^14 p <= 2^14
-        const _Float16 hi = (_Float16)pv;
-        const _Float16 lo = (_Float16)((pv - (float)hi) * 2048.0f);
-        out[c] = hi;
-        out[sp + c] = lo;
-    }
+    const float scale = 16384.0f / sum;
+    for (int c = lane; c < sp; c += 64) emit(c, c < n ? expf(s[c] - mx) : 0.f, scale);
 }
 
 // ---------------------------------------------------------------------------
-// Vt2[b] (E x 2 sp) = [V[b]^T | V[b]^T], zero for keys >= n.  64 x 64 tiles
-// through LDS so both the read (along E) and the write (along keys) coalesce.
+// Vt[b] (E x sp) = V[b]^T, zero for keys >= n.  64 x 64 tiles through LDS
+// so both the read (along E) and the write (along keys) coalesce.
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(256)
-    transpose_dup_kernel(const _Float16* __restrict__ V, _Float16* __restrict__ Vt, int n, int E,
-                         int sp) {
+    transpose_kernel(const _Float16* __restrict__ V, _Float16* __restrict__ Vt, int n, int E, int sp) {
     __shared__ _Float16 tile[64][65];
     const int b = blockIdx.z;
     const int k0 = blockIdx.y * 64, e0 = blockIdx.x * 64;
     const _Float16* v = V + (int64_t)b * n * E;
-    _Float16* vt = Vt + (int64_t)b * E * (2 * (int64_t)sp);
+    _Float16* vt = Vt + (int64_t)b * E * (int64_t)sp;
     const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
     for (int r = ty; r < 64; r += 4) {
         const int k = k0 + r, e = e0 + tx;
@@ -219,11 +249,7 @@ __global__ void __launch_bounds__(256)
     __syncthreads();
     for (int r = ty; r < 64; r += 4) {
         const int e = e0 + r, k = k0 + tx;
-        if (e < E && k < sp) {
-            const _Float16 x = tile[tx][r];
-            vt[(int64_t)e * 2 * sp + k] = x;
-            vt[(int64_t)e * 2 * sp + sp + k] = x;
-        }
+        if (e < E && k < sp) vt[(int64_t)e * sp + k] = tile[tx][r];
     }
 }
 
@@ -233,7 +259,7 @@ __global__ void __launch_bounds__(256)
 namespace {
 
 int round_up(int x, int m) { return (x + m - 1) / m * m; }
-// keys per half of P' / Vt2 rows: whole 64-deep slices, so the switch from
+// keys per half of a P' row (and per Vt row): whole 64-deep slices, so the switch from
 // the H half to the L half falls between slices
 constexpr int kSdpaKeyPad = 64;
 
@@ -255,7 +281,7 @@ size_t sdpa_workspace_bytes(int64_t heads, int seq, int embed) {
     const int64_t sp = round_up(seq, kSdpaKeyPad);
     return (size_t)hc * (seq * sp * 4       // S (fp32)
                          + seq * 2 * sp * 2  // P' (fp16)
-                         + embed * 2 * sp * 2);  // Vt2 (fp16)
+                         + embed * sp * 2);     // Vt (fp16)
 }
 
 hipError_t launch_sdpa(const _Float16* Q, const _Float16* K, const _Float16* V, _Float16* O,
@@ -288,19 +314,28 @@ hipError_t launch_sdpa(const _Float16* Q, const _Float16* K, const _Float16* V, 
         q.alpha = scale;
         q.k_switch = -1;
         q.switch_mul = 1.0f;
+        q.b_kwrap = 0;
         hipError_t e = launch_hgemm<false>(q, hc, s);
         if (e != hipSuccess) return e;
         // 2. P' = split softmax rows
         const int64_t rows = (int64_t)hc * seq;
-        hipLaunchKernelGGL(softmax_split_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, S,
-                           P, rows, seq, sp, (int64_t)sp);
+        const dim3 sm_grid((unsigned)((rows + 3) / 4));
+        if (sp <= 512)
+            hipLaunchKernelGGL((softmax_split_kernel<8>), sm_grid, dim3(256), 0, s, S, P, rows, seq, sp,
+                               (int64_t)sp);
+        else if (sp <= 1024)
+            hipLaunchKernelGGL((softmax_split_kernel<16>), sm_grid, dim3(256), 0, s, S, P, rows, seq, sp,
+                               (int64_t)sp);
+        else
+            hipLaunchKernelGGL((softmax_split_kernel<0>), sm_grid, dim3(256), 0, s, S, P, rows, seq, sp,
+                               (int64_t)sp);
         if ((e = hipGetLastError()) != hipSuccess) return e;
-        // 3. Vt2 = [V^T | V^T]
-        hipLaunchKernelGGL(transpose_dup_kernel,
+        // 3. Vt = V^T
+        hipLaunchKernelGGL(transpose_kernel,
                            dim3((unsigned)((embed + 63) / 64), (unsigned)((sp + 63) / 64), (unsigned)hc),
                            dim3(256), 0, s, V + h0 * head_elems, Vt, seq, embed, sp);
         if ((e = hipGetLastError()) != hipSuccess) return e;
-        // 4. O = P' . Vt2^T (seq x E, fp16)
+        // 4. O = P' . [Vt | Vt]^T (seq x E, fp16): B wraps around Vt's sp columns
         HgemmParams o{};
         o.A = P;
         o.B = Vt;
@@ -311,10 +346,11 @@ hipError_t launch_sdpa(const _Float16* Q, const _Float16* K, const _Float16* V, 
         o.n_store = embed;
         o.tiles_n = (embed + kHgBN - 1) / kHgBN;
         o.lda = 2 * sp;
-        o.ldb = 2 * sp;
+        o.ldb = sp;
+        o.b_kwrap = sp;
         o.ldc = embed;
         o.sa = (int64_t)seq * 2 * sp;
-        o.sb = (int64_t)embed * 2 * sp;
+        o.sb = (int64_t)embed * sp;
         o.sc = head_elems;
         o.k_switch = sp / kHgBK;       // first slice of the L half
         o.switch_mul = 2048.0f;        // 2^11: H.V -> 2^11 H.V, then + L.V
