@@ -19,6 +19,8 @@
 //                  the same stream over fixed 32 KiB chunks of the array.
 //   splitk_reduce  C = sum over splits of the partial tiles, in split order.
 //   fill kernels   zero fill and the counter-based uniform generator.
+#include <type_traits>
+
 #include "mi_device.hpp"
 #include "mi_internal.hpp"
 
@@ -279,27 +281,68 @@ hipError_t launch_scale(const float* A, float* C, int64_t n, float s, hipStream_
 // ---------------------------------------------------------------------------
 // split-K reduction and fills
 // ---------------------------------------------------------------------------
-__global__ void splitk_reduce_kernel(const float* __restrict__ ws, float* __restrict__ C, int M,
-                                     int N, int split_k, int64_t ldc, int64_t sc,
-                                     int64_t split_stride, const float* __restrict__ bias) {
+// Each output element's split_k partials are summed by kReduceGroups threads,
+// each over a fixed contiguous range of splits (sequentially, 4 loads in
+// flight), and the group sums are added in group order: a fixed partition and
+// order, so the result is the same on every call.  32 elements (VEC: 32
+// float4s) per workgroup of 256 threads.
+constexpr int kReduceGroups = 8;
+
+template <bool VEC>
+__global__ void __launch_bounds__(256)
+    splitk_reduce_kernel(const float* __restrict__ ws, float* __restrict__ C, int M, int N, int split_k,
+                         int64_t ldc, int64_t sc, int64_t split_stride, const float* __restrict__ bias) {
+    using V = typename std::conditional<VEC, f4, float>::type;
+    constexpr int W = VEC ? 4 : 1;
+    __shared__ V part[kReduceGroups][32];
     const int64_t per_batch = (int64_t)M * N;
-    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int lane32 = threadIdx.x & 31, g = threadIdx.x >> 5;
+    const int64_t q = (int64_t)blockIdx.x * 32 + lane32;  // element (VEC: float4) index
     const int b = blockIdx.y;
-    if (e >= per_batch) return;
-    const float* src = ws + (int64_t)b * per_batch + e;
-    float s = 0.f;
-    for (int t = 0; t < split_k; ++t) s += src[(int64_t)t * split_stride];
+    const bool live = q * W < per_batch;
+    V acc = V{};
+    if (live) {
+        const V* src = reinterpret_cast<const V*>(ws + (int64_t)b * per_batch) + q;
+        const int64_t stride = split_stride / W;
+        const int t0 = (int)((int64_t)g * split_k / kReduceGroups);
+        const int t1 = (int)((int64_t)(g + 1) * split_k / kReduceGroups);
+        int t = t0;
+        for (; t + 4 <= t1; t += 4) {
+            V v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[u] = src[(int64_t)(t + u) * stride];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc += v[u];
+        }
+        for (; t < t1; ++t) acc += src[(int64_t)t * stride];
+    }
+    part[g][lane32] = acc;
+    __syncthreads();
+    if (g != 0 || !live) return;
+    V s = part[0][lane32];
+#pragma unroll
+    for (int h = 1; h < kReduceGroups; ++h) s += part[h][lane32];
+    const int64_t e = q * W;
     const int64_t row = e / N, col = e % N;
     if (bias) s += bias[row];
-    C[(int64_t)b * sc + row * ldc + col] = s;
+    float* dst = C + (int64_t)b * sc + row * ldc + col;
+    if constexpr (VEC) *reinterpret_cast<f4*>(dst) = s;
+    else *dst = s;
 }
 
 hipError_t launch_splitk_reduce(const float* ws, float* C, int M, int N, int batch, int split_k,
                                 int64_t ldc, int64_t sc, const float* bias, hipStream_t s) {
     const int64_t per_batch = (int64_t)M * N;
-    dim3 grid((unsigned)((per_batch + 255) / 256), (unsigned)batch);
-    hipLaunchKernelGGL(splitk_reduce_kernel, grid, dim3(256), 0, s, ws, C, M, N, split_k, ldc, sc,
-                       per_batch * batch, bias);
+    const bool vec = N % 4 == 0 && ldc % 4 == 0 && sc % 4 == 0 && ((uintptr_t)C & 15u) == 0 &&
+                     ((uintptr_t)ws & 15u) == 0;
+    const int64_t items = vec ? per_batch / 4 : per_batch;
+    dim3 grid((unsigned)((items + 31) / 32), (unsigned)batch);
+    if (vec)
+        hipLaunchKernelGGL((splitk_reduce_kernel<true>), grid, dim3(256), 0, s, ws, C, M, N, split_k, ldc,
+                           sc, per_batch * batch, bias);
+    else
+        hipLaunchKernelGGL((splitk_reduce_kernel<false>), grid, dim3(256), 0, s, ws, C, M, N, split_k,
+                           ldc, sc, per_batch * batch, bias);
     return hipGetLastError();
 }
 
