@@ -196,3 +196,23 @@ def test_workspace_queries(ck):
     assert L.mi_matmul_large_k_workspace_bytes(8192, 8192, 8192) == 0
     assert L.mi_gemv_workspace_bytes(32768, 65536) == 0
     assert L.mi_gemv_workspace_bytes(64, 1 << 20) > 0
+
+
+def test_header_is_plain_c(tmp_path):
+    """include/mi355_gemm.h is the drop-in C boundary: it must compile as C99
+    (for cgo / JNI / ctypes hosts) and as C++, with no HIP or torch headers."""
+    import os
+    import shutil
+    import subprocess
+    inc = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include")
+    src = tmp_path / "use.c"
+    src.write_text('#include "mi355_gemm.h"\n'
+                   'int main(void) { mi_gemm_args a = {0}; mi_plan p; (void)p;\n'
+                   '  return (int)sizeof(a) + (int)MI_ERR_ALIGNMENT; }\n')
+    for cc, std in (("gcc", "-std=c99"), ("g++", "-std=c++11")):
+        if shutil.which(cc) is None:
+            continue
+        lang = ["-x", "c++"] if cc == "g++" else []
+        r = subprocess.run([cc, std, "-Wall", "-Werror", "-pedantic", "-fsyntax-only", *lang,
+                            f"-I{inc}", str(src)], capture_output=True, text=True)
+        assert r.returncode == 0, r.stderr
