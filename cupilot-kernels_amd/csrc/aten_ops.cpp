@@ -485,6 +485,89 @@ at::Tensor matmul_transposed_both(const at::Tensor& A, const at::Tensor& B) {
 
 }  // namespace mi355
 
+// ---------------------------------------------------------------------------
+// torch.ops.mi355.<op>: the same operators in the dispatcher, for graph use.
+// CUDA (= HIP on ROCm) kernels are the functions above; Meta kernels give the
+// output shape only (tracing, fake tensors).  There is deliberately no CPU
+// kernel: a CPU tensor is an error, never a silent fallback.
+// ---------------------------------------------------------------------------
+namespace {
+
+at::Tensor meta_like(const at::Tensor& t, at::IntArrayRef shape) { return at::empty(shape, t.options()); }
+
+}  // namespace
+
+TORCH_LIBRARY(mi355, m) {
+    m.def("square_matmul(Tensor A, Tensor B) -> Tensor");            // PID 1
+    m.def("matmul(Tensor A, Tensor B) -> Tensor");                   // PIDs 2, 8
+    m.def("batched_matmul(Tensor A, Tensor B) -> Tensor");           // PID 3
+    m.def("gemv(Tensor A, Tensor B) -> Tensor");                     // PID 4
+    m.def("matrix_scalar_mult(Tensor A, float s) -> Tensor");        // PID 5
+    m.def("matmul_large_k(Tensor A, Tensor B) -> Tensor");           // PID 6
+    m.def("gemm_small_k(Tensor A, Tensor B) -> Tensor");             // PID 7
+    m.def("tall_skinny_matmul(Tensor A, Tensor B) -> Tensor");       // PID 9
+    m.def("tensor3d_matmul(Tensor A, Tensor B) -> Tensor");          // PID 10
+    m.def("tensor4d_matmul(Tensor A, Tensor B) -> Tensor");          // PID 11
+    m.def("diag_mult(Tensor A, Tensor B) -> Tensor");                // PID 12
+    m.def("symmetric_matmul(Tensor A, Tensor B) -> Tensor");         // PID 13
+    m.def("upper_tri_matmul(Tensor A, Tensor B) -> Tensor");         // PID 14
+    m.def("lower_tri_mul(Tensor A, Tensor B) -> Tensor");            // PID 15
+    m.def("matmul_transposed_a(Tensor A, Tensor B) -> Tensor");      // PID 16
+    m.def("matmul_transposed_b(Tensor A, Tensor B) -> Tensor");      // PID 17
+    m.def("matmul_transposed_both(Tensor A, Tensor B) -> Tensor");   // PID 18
+    m.def("pointwise_conv(Tensor input, Tensor weight, Tensor? bias=None) -> Tensor");  // PID 87
+    m.def("fused_attention(Tensor Q, Tensor K, Tensor V) -> Tensor");                   // PID 97
+}
+
+TORCH_LIBRARY_IMPL(mi355, CUDA, m) {
+    m.impl("square_matmul", &mi355::square_matmul);
+    m.impl("matmul", &mi355::matmul);
+    m.impl("batched_matmul", &mi355::batched_matmul);
+    m.impl("gemv", &mi355::gemv);
+    m.impl("matrix_scalar_mult", &mi355::matrix_scalar_mult);
+    m.impl("matmul_large_k", &mi355::matmul_large_k);
+    m.impl("gemm_small_k", &mi355::gemm_small_k);
+    m.impl("tall_skinny_matmul", &mi355::tall_skinny_matmul);
+    m.impl("tensor3d_matmul", &mi355::tensor3d_matmul);
+    m.impl("tensor4d_matmul", &mi355::tensor4d_matmul);
+    m.impl("diag_mult", &mi355::diag_mult);
+    m.impl("symmetric_matmul", &mi355::symmetric_matmul);
+    m.impl("upper_tri_matmul", &mi355::upper_tri_matmul);
+    m.impl("lower_tri_mul", &mi355::lower_tri_mul);
+    m.impl("matmul_transposed_a", &mi355::matmul_transposed_a);
+    m.impl("matmul_transposed_b", &mi355::matmul_transposed_b);
+    m.impl("matmul_transposed_both", &mi355::matmul_transposed_both);
+    m.impl("pointwise_conv", &mi355::pointwise_conv);
+    m.impl("fused_attention", &mi355::fused_attention);
+}
+
+TORCH_LIBRARY_IMPL(mi355, Meta, m) {
+    using T = const at::Tensor&;
+    auto mm = [](T A, T B) { return meta_like(A, {A.size(0), B.size(1)}); };
+    m.impl("square_matmul", mm);
+    m.impl("matmul", mm);
+    m.impl("matmul_large_k", mm);
+    m.impl("gemm_small_k", mm);
+    m.impl("tall_skinny_matmul", mm);
+    m.impl("symmetric_matmul", mm);
+    m.impl("upper_tri_matmul", mm);
+    m.impl("lower_tri_mul", mm);
+    m.impl("batched_matmul", [](T A, T B) { return meta_like(A, {A.size(0), A.size(1), B.size(2)}); });
+    m.impl("gemv", [](T A, T B) { return meta_like(A, {A.size(0), 1}); });
+    m.impl("matrix_scalar_mult", [](T A, double) { return at::empty_like(A); });
+    m.impl("tensor3d_matmul", [](T A, T B) { return meta_like(A, {A.size(0), A.size(1), B.size(1)}); });
+    m.impl("tensor4d_matmul",
+           [](T A, T B) { return meta_like(A, {A.size(0), A.size(1), A.size(2), B.size(1)}); });
+    m.impl("diag_mult", [](T A, T B) { return meta_like(B, {A.size(0), B.size(1)}); });
+    m.impl("matmul_transposed_a", [](T A, T B) { return meta_like(A, {A.size(1), B.size(1)}); });
+    m.impl("matmul_transposed_b", [](T A, T B) { return meta_like(A, {A.size(0), B.size(0)}); });
+    m.impl("matmul_transposed_both", [](T A, T B) { return meta_like(A, {A.size(1), B.size(0)}); });
+    m.impl("pointwise_conv", [](T x, T w, const c10::optional<at::Tensor>&) {
+        return meta_like(x, {x.size(0), w.size(0), x.size(2), x.size(3)});
+    });
+    m.impl("fused_attention", [](T Q, T, T) { return at::empty_like(Q); });
+}
+
 // One Python submodule per reference file, exposing the reference's own
 // function name (the names collide across files: matmul_cuda is PIDs 1, 2, 6,
 // 8 and 17; matmul_transposed_cuda is 16 and 18; batched_matmul_cuda is 3 and 10).

@@ -118,3 +118,37 @@ def test_package_refuses_to_load_without_extension(tmp_path):
             spec.loader.exec_module(mod)
     finally:
         sys.modules.pop("ck_nobuild", None)
+
+
+def test_torch_ops_registered_with_meta_shapes(ck):
+    """Every operator is also torch.ops.mi355.<op> (graph use): Meta kernels
+    give the reference output shapes, and a CPU tensor is rejected (no CPU
+    kernel, so no silent fallback)."""
+    import torch
+    ops = torch.ops.mi355
+    m = lambda *s: torch.empty(s, device="meta")
+    cases = {
+        "square_matmul": ((m(8, 8), m(8, 8)), (8, 8)),
+        "matmul": ((m(5, 7), m(7, 3)), (5, 3)),
+        "batched_matmul": ((m(2, 5, 7), m(2, 7, 3)), (2, 5, 3)),
+        "gemv": ((m(5, 7), m(7, 1)), (5, 1)),
+        "matmul_large_k": ((m(4, 4096), m(4096, 6)), (4, 6)),
+        "gemm_small_k": ((m(9, 2), m(2, 11)), (9, 11)),
+        "tall_skinny_matmul": ((m(12, 3), m(3, 12)), (12, 12)),
+        "tensor3d_matmul": ((m(2, 5, 7), m(7, 3)), (2, 5, 3)),
+        "tensor4d_matmul": ((m(2, 3, 4, 7), m(7, 5)), (2, 3, 4, 5)),
+        "diag_mult": ((m(6), m(6, 9)), (6, 9)),
+        "symmetric_matmul": ((m(8, 8), m(8, 8)), (8, 8)),
+        "upper_tri_matmul": ((m(8, 8), m(8, 8)), (8, 8)),
+        "lower_tri_mul": ((m(8, 8), m(8, 8)), (8, 8)),
+        "matmul_transposed_a": ((m(7, 5), m(7, 3)), (5, 3)),
+        "matmul_transposed_b": ((m(5, 7), m(3, 7)), (5, 3)),
+        "matmul_transposed_both": ((m(7, 5), m(3, 7)), (5, 3)),
+        "fused_attention": ((m(1, 2, 16, 1024),) * 3, (1, 2, 16, 1024)),
+    }
+    for name, (args, shape) in cases.items():
+        assert tuple(getattr(ops, name)(*args).shape) == shape, name
+    assert tuple(ops.matrix_scalar_mult(m(3, 4), 2.0).shape) == (3, 4)
+    assert tuple(ops.pointwise_conv(m(2, 3, 5, 5), m(8, 3, 1, 1), None).shape) == (2, 8, 5, 5)
+    with pytest.raises((RuntimeError, NotImplementedError)):
+        ops.matmul(torch.zeros(4, 4), torch.zeros(4, 4))

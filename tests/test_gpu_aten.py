@@ -191,6 +191,17 @@ def test_unaligned_rows_take_padded_copies(ck, orc, dev, M, K, N, ta, tb):
     assert_close(orc, to_host(C), ref, K, what=f"padded {M}x{K}x{N} {ta}{tb}")
 
 
+def test_torch_ops_dispatch_to_the_kernels(ck, orc, dev):
+    """torch.ops.mi355.<op> runs the same HIP kernels as the per-PID modules."""
+    a, b = _u(orc, (130, 96), 80), _u(orc, (96, 70), 81)
+    A, B = to_dev(a), to_dev(b)
+    np.testing.assert_array_equal(to_host(torch.ops.mi355.matmul(A, B)), to_host(ck.p02.matmul_cuda(A, B)))
+    np.testing.assert_array_equal(to_host(torch.ops.mi355.matrix_scalar_mult(A, 2.5)),
+                                  to_host(ck.p05.matrix_scalar_mult_cuda(A, 2.5)))
+    d = to_dev(_u(orc, (130,), 82))
+    np.testing.assert_array_equal(to_host(torch.ops.mi355.diag_mult(d, A)), to_host(ck.p12.diag_mult_cuda(d, A)))
+
+
 def test_golden_fixtures_bitwise(ck, dev):
     """Every operator on the committed integer known-answer cases
     (tests/golden/gemm_family_int.npz): exact arithmetic, so bitwise equal."""
