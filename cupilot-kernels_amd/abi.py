@@ -25,7 +25,7 @@ MI_ERR_NO_DEVICE = -7
 MI_ERR_ALIGNMENT = -8
 
 MI_OP_N, MI_OP_T = 0, 1
-MI_DENSE, MI_LOWER, MI_UPPER = 0, 1, 2
+MI_DENSE, MI_LOWER, MI_UPPER, MI_SYMMETRIC = 0, 1, 2, 3
 CFG64, CFG128, CFG256, CFG128K32, CFG128K64, CFG_PANEL32, CFG_PANEL64 = 1, 2, 3, 4, 5, 6, 7
 
 _i64 = ctypes.c_int64

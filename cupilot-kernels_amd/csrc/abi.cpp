@@ -66,6 +66,18 @@ mi_gemm_args dense_args(const float* A, const float* B, float* C, int64_t M, int
     return a;
 }
 
+// MI_SYMMETRIC is a dense product whose operands may be read either way;
+// rewrite it to the dense form with both operands K-contiguous (the N/T
+// kernel, the fastest measured layout).
+int canonical(mi_gemm_args& a) {
+    if (a.structure != MI_SYMMETRIC) return MI_OK;
+    if (a.M != a.N || a.N != a.K) return MI_ERR_NOT_SQUARE;
+    a.structure = MI_DENSE;
+    a.op_a = MI_OP_N;
+    a.op_b = MI_OP_T;
+    return MI_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -91,15 +103,21 @@ const char* mi_version(void) { return "mi355_gemm 0.1.0 gfx950"; }
 
 int mi_gemm_plan(const mi_gemm_args* args, int32_t num_cus, mi_plan* out) {
     if (!args || !out) return MI_ERR_NULL_POINTER;
-    return plan_gemm(*args, num_cus, *out, nullptr);
+    mi_gemm_args a = *args;
+    const int rc = canonical(a);
+    if (rc != MI_OK) return rc;
+    return plan_gemm(a, num_cus, *out, nullptr);
 }
 
 int mi_gemm_tile_of(const mi_gemm_args* args, int32_t num_cus, int64_t item, int32_t split,
                     int32_t* tile_m, int32_t* tile_n, int64_t* k_begin, int64_t* k_end) {
     if (!args || !tile_m || !tile_n || !k_begin || !k_end) return MI_ERR_NULL_POINTER;
+    mi_gemm_args ca = *args;
+    int rc = canonical(ca);
+    if (rc != MI_OK) return rc;
     mi_plan p{};
     GemmLaunch g{};
-    const int rc = plan_gemm(*args, num_cus, p, &g);
+    rc = plan_gemm(ca, num_cus, p, &g);
     if (rc != MI_OK) return rc;
     if (item < 0 || item >= g.num_tiles || split < 0 || split >= g.split_k) return MI_ERR_BAD_SIZE;
     const GemmParams kp = make_params(g);
@@ -136,6 +154,7 @@ int mi_gemm_tile_of(const mi_gemm_args* args, int32_t num_cus, int64_t item, int
 size_t mi_gemm_workspace_bytes(const mi_gemm_args* args) {
     if (!args) return 0;
     mi_gemm_args a = *args;
+    if (canonical(a) != MI_OK) return 0;
     a.workspace_bytes = SIZE_MAX;  // ask what the preferred plan wants
     int st = MI_OK;
     const int cus = device_cus(&st);
@@ -146,8 +165,10 @@ size_t mi_gemm_workspace_bytes(const mi_gemm_args* args) {
 
 int mi_gemm_f32(const mi_gemm_args* args, void* stream) {
     if (!args) return MI_ERR_NULL_POINTER;
-    const mi_gemm_args& a = *args;
-    int rc = validate_shape(a);
+    mi_gemm_args a = *args;
+    int rc = canonical(a);
+    if (rc != MI_OK) return rc;
+    rc = validate_shape(a);
     if (rc != MI_OK) return rc;
     const bool empty_out = a.M == 0 || a.N == 0 || a.batch == 0;
     if (empty_out) return MI_OK;
@@ -320,8 +341,9 @@ int mi_sdpa_f16(const void* Q, const void* K, const void* V, void* O, int64_t ba
 
 int mi_symmetric_matmul_f32(const float* A, const float* B, float* C, int64_t N, void* stream) {
     // A = A^T and B = B^T, so A . B = A . (B^T) with B read as stored N x K:
-    // both operands are then K-contiguous.
-    mi_gemm_args a = dense_args(A, B, C, N, N, N, MI_OP_N, MI_OP_T);
+    // both operands are then K-contiguous (MI_SYMMETRIC's canonical form).
+    mi_gemm_args a = dense_args(A, B, C, N, N, N, MI_OP_N, MI_OP_N);
+    a.structure = MI_SYMMETRIC;
     return mi_gemm_f32(&a, stream);
 }
 

@@ -216,3 +216,14 @@ def test_header_is_plain_c(tmp_path):
         r = subprocess.run([cc, std, "-Wall", "-Werror", "-pedantic", "-fsyntax-only", *lang,
                             f"-I{inc}", str(src)], capture_output=True, text=True)
         assert r.returncode == 0, r.stderr
+
+
+def test_symmetric_structure_is_the_nt_dense_plan(ck):
+    """MI_SYMMETRIC: square only; planned exactly like the dense N/T product."""
+    L = ck.abi.lib()
+    rc, _ = ck.abi.plan(64, 64, 32, structure=ck.abi.MI_SYMMETRIC)
+    assert rc == ck.abi.MI_ERR_NOT_SQUARE
+    rc, ps = ck.abi.plan(4096, 4096, 4096, structure=ck.abi.MI_SYMMETRIC)
+    rc2, pd = ck.abi.plan(4096, 4096, 4096, op_b=ck.abi.MI_OP_T)
+    assert rc == rc2 == 0
+    assert (ps.plan_id, ps.grid, ps.split_k, ps.tiles_m) == (pd.plan_id, pd.grid, pd.split_k, pd.tiles_m)

@@ -350,6 +350,21 @@ def test_row_bias_split_k_zero_k_and_batched(ck, orc, dev):
         assert run_gemm(ck, argsl) != 0
 
 
+def test_symmetric_structure(ck, orc, dev):
+    """mi_gemm_f32 with MI_SYMMETRIC equals the dense product of symmetric
+    inputs (and the named symmetric entry point, bitwise)."""
+    n = 300
+    r1, r2 = orc.uniform((n, n), 141), orc.uniform((n, n), 142)
+    a, b = (r1 + r1.T) / 2, (r2 + r2.T) / 2
+    A, B = to_dev(a), to_dev(b)
+    C = torch.empty((n, n), device="cuda")
+    ck.abi.check(run_gemm(ck, gemm_args(ck, A, B, C, n, n, n, structure=3)))
+    assert_close(orc, to_host(C), orc.gemm(a, b), n, what="MI_SYMMETRIC")
+    C2 = torch.empty((n, n), device="cuda")
+    ck.abi.check(ck.abi.lib().mi_symmetric_matmul_f32(vp(A), vp(B), vp(C2), n, cur_stream()))
+    np.testing.assert_array_equal(to_host(C), to_host(C2))
+
+
 def test_named_entry_points(ck, orc, dev):
     """Every per-operator C entry point against the oracle on a moderate shape."""
     L = ck.abi.lib()
