@@ -259,16 +259,13 @@ def test_diag_mult_bitwise(ck, orc, dev, N, M):
     np.testing.assert_array_equal(to_host(out), orc.diag_mult(a, b))
 
 
-@pytest.mark.parametrize("n", [1, 3, 4, 5, 2047, 8192, 8192 * 4 + 3, (1 << 22) + 7,
-                               16384 * 4096])
-@pytest.mark.parametrize("misalign", [0, 1])
+@pytest.mark.parametrize("n,misalign", [(n, m) for n in (1, 3, 4, 5, 2047, 8192, 8192 * 4 + 3, (1 << 22) + 7)
+                                         for m in (0, 1)] + [(16384 * 4096, 0)])
 def test_matrix_scalar_bitwise(ck, orc, dev, n, misalign):
     """C = A * s (mi_matrix_scalar_mult_f32): one fp32 multiply per element, so
     bitwise equal to the oracle, on the float4 path (chunk multiples, a partial
     chunk, an n % 4 tail) and, with both pointers one float off 16-byte
     alignment, on the scalar path."""
-    if misalign and n > (1 << 23):
-        pytest.skip("the scalar path is covered by the smaller sizes")
     a = orc.uniform((n + misalign,), 93)
     da = to_dev(a)
     out = torch.empty((n + misalign,), device="cuda")
