@@ -8,9 +8,10 @@
 // Structure of one workgroup:
 //   * a BM x BN output tile; waves arranged WAVES_M x WAVES_N, each owning a
 //     WM x WN sub-tile held as (WM/32) x (WN/32) MFMA accumulators (16 VGPR each);
-//   * K is walked in BK = 16 slices through two LDS buffers (one barrier per
-//     slice: the next slice's global loads are issued before the MFMAs of the
-//     current one and written to the other buffer after them);
+//   * K is walked in BK-deep slices (16 or 32; the small-K configs take the
+//     whole K in one slice) through two LDS buffers (one barrier per slice:
+//     the next slice's global loads are issued before the MFMAs of the current
+//     one and written to the other buffer after them);
 //   * each operand is kept in LDS in the orientation it has in HBM, so every
 //     global load is a coalesced 16-byte load and every LDS store a
 //     ds_write_b128 with no transpose:
@@ -21,9 +22,13 @@
 //     Within a k-block of 8, lane half h = lane / 32 and MFMA step s use
 //     k = 8*kb + 4*h + s for both operands, which is what lets the
 //     K-contiguous side use 16-byte reads.
-//   * epilogue writes straight from the accumulators (row = 8*(r/4) + 4*h +
-//     r%4, col = lane % 32 for accumulator register r), masked at the matrix
-//     edge and, for the triangular modes, on the diagonal.
+//   * the B fragment is the MFMA's row operand, so each accumulator block is
+//     the block of C^T: lane l holds output row l % 32 and, in register group
+//     g, the 4 consecutive columns 8g + 4h .. +3 -> one 16-byte store per
+//     group, masked at the matrix edge and, for the triangular modes, on the
+//     diagonal (+0.0 on the wrong side);
+//   * persistent over tiles and software-pipelined across them (see
+//     gemm_f32_kernel), with an XCD-aware grouped raster.
 // Split-K (used for K >> M, N) writes fp32 partial tiles to a workspace that
 // a second kernel sums in fixed split order, so results are deterministic.
 #pragma once
