@@ -77,11 +77,13 @@ PLAN_KERNELS = {
 
 def nn_kernel_name(ck) -> str:
     """Kernel the scheduler picks for the NN 8192^3 launch (N/N launches of the
-    256 tile with K % 32 == 0 and K >= 1024 take the direct-staging kernel)."""
+    256 tile with K % 32 == 0 and K >= 256 per split take the direct-staging
+    kernel)."""
     rc, plan = ck.abi.plan(N, N, N)
     ck.abi.check(rc, "mi_gemm_plan")
-    if plan.plan_id == 3 and N % 32 == 0 and plan.k_chunk >= 1024:
-        return f"mi::gemm_f32_direct_kernel<Tile<256,256,128,64,32,2,2>, false> (split_k {plan.split_k})"
+    if plan.plan_id == 3 and N % 32 == 0 and plan.k_chunk >= 256:
+        return ("mi::gemm_f32_direct_kernel<Tile<256,256,128,64,32,2,2>, false, false, false> "
+                f"(split_k {plan.split_k})")
     return f"mi::{PLAN_KERNELS.get(plan.plan_id, plan.plan_id)}, NN, vec4, dense (split_k {plan.split_k})"
 
 

@@ -1,10 +1,13 @@
-// gemm_direct.hpp -- the 256 x 256 N/N contraction with global -> LDS direct
-// loads (gfx950 global_load_lds_dwordx4), for dense problems whose slices are
-// all full (K a multiple of 32, 16-byte aligned operands) and long (K >= 1024).
+// gemm_direct.hpp -- the 256 x 256 contraction (all four operand layouts)
+// with global -> LDS direct loads (gfx950 buffer_load_dwordx4 ... lds), for
+// dense problems whose slices are all full (K a multiple of 32, 16-byte
+// aligned operands) and deep enough (direct_ok).
 //
-// Same tile, waves, MFMA order and epilogue as gemm_f32_kernel<Tile256>; what
-// changes is the staging.  Each lane's 16-byte global load lands in LDS at
-// (wave's LDS base + 16 * lane) without passing through VGPRs, so
+// Same tile, waves and MFMA order as gemm_f32_kernel<Tile256> (so the same
+// results, bit for bit); what changes is the staging and, with it, the order
+// of rows / columns within a wave's MN-contiguous blocks.  Each lane's
+// 16-byte global load lands in LDS at (wave's LDS base + 16 * lane) without
+// passing through VGPRs, so
 //   * no VGPRs hold the next slice (32 per lane in the register-staged kernel),
 //   * no ds_write instructions, and no wait for the loads before the MFMAs
 //     of the current slice end: the single barrier per slice (which waits for
@@ -16,7 +19,16 @@
 //     consecutive rows at one chunk then touches 8 different bank groups per
 //     8 lanes (no conflicts) without padding.
 //   MN-contiguous operand: [32][256 + 4], one k-row per wave instruction
-//     (the +4 padding sits between rows, where each instruction's base is free).
+//     (the +4 padding sits between rows, where each instruction's base is
+//     free).  k-row k = 4 g + s sits at LDS row 8 s + g.
+// MN-contiguous fragments are read as pairs of adjacent rows / columns: two
+// 32-wide MFMA blocks are interleaved (block t holds c0 + 2 i + t, i < 32),
+// so one 8-byte read per k gives a lane its value in both blocks.  With the
+// row order above, the reads of one pair are >= 2080 bytes apart, more than
+// a ds_read2_b64 offset reaches, so the compiler cannot merge them (merged
+// reads of this kind were given a full vmcnt(0) wait -- the wait inserter no
+// longer told the buffer being read from the one the next slice's direct
+// loads are writing).
 // Rows / columns past the matrix edge are loaded from the last valid row /
 // column instead (they only feed outputs that are never stored); K has no
 // tail here, so every loaded k is real.
@@ -29,10 +41,20 @@
 namespace mi {
 
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
-typedef __attribute__((address_space(1))) void* global_void_ptr;
 
-__device__ __forceinline__ void load_lds16(const float* g, float* lds) {
-    __builtin_amdgcn_global_load_lds((global_void_ptr)(g), (lds_void_ptr)(lds), 16, 0, 0);
+// Raw buffer descriptor at `base` (dword 3 of the gfx9 format: untyped
+// dwords).  The range check is off (num_records = 2^32 - 1): every offset a
+// caller passes stays inside its operand by construction.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const float* base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, -1, 0x00020000);
+}
+
+// One wave instruction: lane l's 16 bytes at byte offset voff from the
+// descriptor's base land in LDS at lds + 16 l.  (The buffer form, not
+// global_load_lds: a pending FLAT-encoded LDS load forces every LDS-read wait
+// behind it down to lgkmcnt(0).)
+__device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, uint32_t voff, float* lds) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_ptr)(lds), 16, (int)voff, 0, 0, 0);
 }
 
 // One operand of a 256 x 32 slice, staged directly into LDS by NW waves.
@@ -47,48 +69,130 @@ struct DirectLoader {
     static_assert(INSTR % NW == 0, "instructions must split evenly over the waves");
     static constexpr int PER_WAVE = INSTR / NW;
 
-    // Issue this wave's loads of the slice at (mn0, k0) into `lds`.
+    // Issue this wave's loads of the slice at (mn0, k0) into `lds`.  Offsets
+    // are taken from the slice's origin and fit 32 bits (direct_ok bounds ld).
     __device__ __forceinline__ static void load(const float* __restrict__ base, int64_t ld, int mn0,
                                                 int mn_ext, int k0, float* lds, int wave, int lane) {
+        const __amdgpu_buffer_rsrc_t rsrc =
+            raw_rsrc(KCONTIG ? base + (int64_t)mn0 * ld + k0 : base + (int64_t)k0 * ld + mn0);
+        const uint32_t ld4 = (uint32_t)ld * 4u;
 #pragma unroll
         for (int i = 0; i < PER_WAVE; ++i) {
             const int ins = wave * PER_WAVE + i;
             if (KCONTIG) {
                 const int r = ins * 8 + (lane >> 3);          // tile row this lane fills
                 const int q = (lane & 7) ^ (r & 7);           // global chunk for its slot
-                int gr = mn0 + r;
-                gr = gr < mn_ext ? gr : mn_ext - 1;
-                load_lds16(base + (int64_t)gr * ld + k0 + q * 4, lds + ins * 8 * BK);
+                const int rr = mn0 + r < mn_ext ? r : mn_ext - 1 - mn0;
+                load_lds16(rsrc, (uint32_t)rr * ld4 + (uint32_t)q * 16u, lds + ins * 8 * BK);
             } else {
                 const int k = ins;
-                int c = mn0 + lane * 4;
-                c = c + 3 < mn_ext ? c : mn_ext - 4;
-                load_lds16(base + (int64_t)(k0 + k) * ld + c, lds + k * LD);
+                // (mn_ext - mn0 is a positive multiple of 4: vec4 operands)
+                const int c = mn0 + lane * 4 + 3 < mn_ext ? lane * 4 : mn_ext - 4 - mn0;
+                load_lds16(rsrc, (uint32_t)k * ld4 + (uint32_t)c * 4u, lds + row_of(k) * LD);
             }
         }
     }
 
-    // Operand values for the 4 MFMA steps of k-block kb, 32-row group at r0
-    // (same k permutation as TileLoader::frag: k = 8 kb + 4 h + s).
+    // LDS row of k-row k (MN-contiguous layout)
+    __device__ __forceinline__ static constexpr int row_of(int k) { return (k & 3) * 8 + (k >> 2); }
+
+    // K-contiguous operand: values for the 4 MFMA steps of k-block kb,
+    // 32-row group at r0 (same k permutation as TileLoader::frag:
+    // k = 8 kb + 4 h + s).
     __device__ __forceinline__ static void frag(const float* lds, int r0, int kb, int lane,
                                                 float out[4]) {
+        static_assert(KCONTIG, "MN-contiguous fragments are read in pairs");
         const int half = lane >> 5;
         const int l32 = lane & 31;
-        if (KCONTIG) {
-            const int row = r0 + l32;
-            const int q = (2 * kb + half) ^ (l32 & 7);  // r0 % 8 == 0, so row % 8 == l32 % 8
-            const f4 t = *reinterpret_cast<const f4*>(lds + row * BK + q * 4);
-            out[0] = t[0];
-            out[1] = t[1];
-            out[2] = t[2];
-            out[3] = t[3];
-        } else {
-            const float* p = lds + (kb * 8 + half * 4) * LD + r0 + l32;
+        const int row = r0 + l32;
+        const int q = (2 * kb + half) ^ (l32 & 7);  // r0 % 8 == 0, so row % 8 == l32 % 8
+        const f4 t = *reinterpret_cast<const f4*>(lds + row * BK + q * 4);
+        out[0] = t[0];
+        out[1] = t[1];
+        out[2] = t[2];
+        out[3] = t[3];
+    }
+
+    // MN-contiguous operand: values for the 4 MFMA steps of k-block kb in the
+    // two interleaved blocks of the 64 columns at c0 (block t, lane i: column
+    // c0 + 2 i + t).
+    __device__ __forceinline__ static void frag_pair(const float* lds, int c0, int kb, int lane,
+                                                     float out[2][4]) {
+        static_assert(!KCONTIG, "K-contiguous fragments are read one block at a time");
+        const int g = 2 * kb + (lane >> 5);  // k = 4 g + s
+        const float* p = lds + g * LD + c0 + 2 * (lane & 31);
 #pragma unroll
-            for (int s = 0; s < 4; ++s) out[s] = p[s * LD];
+        for (int s = 0; s < 4; ++s) {
+            const f2 t = *reinterpret_cast<const f2*>(p + s * 8 * LD);
+            out[0][s] = t[0];
+            out[1][s] = t[1];
         }
     }
 };
+
+// Epilogue.  An MN-contiguous operand's 32-wide blocks are interleaved in
+// pairs (frag_pair), which moves its rows / columns:
+//   A (rows):    block i = 2 u + t, lane l -> row 64 u + 2 (l % 32) + t;
+//                K-contiguous A: block i, lane l -> row 32 i + l % 32.
+//   B (columns): register r of the swapped-operand MFMA is block column
+//                i' = 8 (r / 4) + 4 (l / 32) + r % 4; interleaved B puts it at
+//                column 2 i' + t of block t, so for each r / 4 a lane holds 8
+//                consecutive columns (two 16-byte stores); K-contiguous B puts
+//                it at 32 j + i' (4 consecutive columns per r / 4).
+template <class T, bool A_IL, bool B_IL, bool BIAS>
+__device__ __forceinline__ void store_tile_direct(const GemmParams& p, float* C, int64_t ldc,
+                                                  bool c_vec, const TileWork& w,
+                                                  const f16v (&acc)[T::TM][T::TN], int wm, int wn,
+                                                  int lane) {
+    static_assert(!B_IL || T::TN == 2, "one interleaved pair of column blocks per wave");
+    static_assert(!A_IL || T::TM % 2 == 0, "row blocks pair up");
+    const int l32 = lane & 31;
+    const int cw = w.tn * T::BN + wn * T::WN + (lane >> 5) * 4;
+    const bool add_bias = BIAS && p.split_k == 1;
+#pragma unroll
+    for (int i = 0; i < T::TM; ++i) {
+        const int row = w.tm * T::BM + wm * T::WM +
+                        (A_IL ? 64 * (i / 2) + 2 * l32 + (i & 1) : 32 * i + l32);
+        if (row >= p.M) continue;
+        const float bv = add_bias ? p.bias[row] : 0.f;
+        float* const crow = C + (int64_t)row * ldc;
+        // one 16-byte group: columns col .. col + 3 get v
+        auto put = [&](int col, f4 v) __attribute__((always_inline)) {
+            if (add_bias) v += bv;
+            if (c_vec && col + 3 < p.N) {
+                *reinterpret_cast<f4*>(crow + col) = v;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (col + e < p.N) crow[col + e] = v[e];
+            }
+        };
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            if (B_IL) {
+                f4 lo, hi;
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    lo[2 * e] = acc[i][0][4 * q + e];
+                    lo[2 * e + 1] = acc[i][1][4 * q + e];
+                    hi[2 * e] = acc[i][0][4 * q + 2 + e];
+                    hi[2 * e + 1] = acc[i][1][4 * q + 2 + e];
+                }
+                const int col = cw + 16 * q + (lane >> 5) * 4;  // 16 q + 8 h
+                put(col, lo);
+                put(col + 4, hi);
+            } else {
+#pragma unroll
+                for (int j = 0; j < T::TN; ++j) {
+                    f4 v;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * q + e];
+                    put(cw + 32 * j + 8 * q, v);
+                }
+            }
+        }
+    }
+}
 
 // Persistent like gemm_f32_kernel; per slice: issue the next slice's direct
 // loads (same tile, the next tile's first slice, or -- after the workgroup's
@@ -97,18 +201,15 @@ struct DirectLoader {
 // a tile's last slice issue its stores.  The two LDS buffers of each operand
 // are separate __shared__ objects and the slice loop is unrolled by two, so
 // each access names its buffer at compile time.
-//
-// Measured against the register-staged kernel at 8192^3 (same process,
-// interleaved): N/N 136.7-136.9 vs 135.0-135.3 TFLOP/s; large-K and batched
-// also gain ~1-2 %, but 4-D (K = 256) loses 5 % and the other layouts lose
-// 2-7 %, so only N/N with K >= 1024 takes this path.
-template <class T, bool BIAS>
+template <class T, bool AT, bool BT, bool BIAS>
 __global__ void __launch_bounds__(T::NT)
     __attribute__((amdgpu_waves_per_eu(T::WAVES_PER_SIMD, T::WAVES_PER_SIMD)))
     gemm_f32_direct_kernel(const GemmParams p) {
     static_assert(T::BM == 256 && T::BN == 256 && T::BK == 32, "direct staging is built for Tile256");
-    using LA = DirectLoader<true, T::NW>;   // A row-major: K-contiguous
-    using LB = DirectLoader<false, T::NW>;  // B row-major: N-contiguous
+    constexpr bool A_KC = !AT;  // A row-major (M x K) is contiguous along K
+    constexpr bool B_KC = BT;   // B stored N x K is contiguous along K
+    using LA = DirectLoader<A_KC, T::NW>;
+    using LB = DirectLoader<B_KC, T::NW>;
     __shared__ __attribute__((aligned(16))) float sA0[LA::ELEMS];
     __shared__ __attribute__((aligned(16))) float sA1[LA::ELEMS];
     __shared__ __attribute__((aligned(16))) float sB0[LB::ELEMS];
@@ -151,14 +252,32 @@ __global__ void __launch_bounds__(T::NT)
     float fa[2][T::TM][4], fb[2][T::TN][4];
     // (every lambda here is force-inlined: a call would pass the accumulators
     // through scratch memory)
+    auto frags = [&](const float* As, const float* Bs, int kb) __attribute__((always_inline)) {
+        if constexpr (A_KC) {
+#pragma unroll
+            for (int i = 0; i < T::TM; ++i) LA::frag(As, wm * T::WM + i * 32, kb, lane, fa[kb & 1][i]);
+        } else {
+#pragma unroll
+            for (int u = 0; u < T::TM / 2; ++u)
+                LA::frag_pair(As, wm * T::WM + u * 64, kb, lane, fa[kb & 1] + 2 * u);
+        }
+        if constexpr (B_KC) {
+#pragma unroll
+            for (int j = 0; j < T::TN; ++j) LB::frag(Bs, wn * T::WN + j * 32, kb, lane, fb[kb & 1][j]);
+        } else {
+            LB::frag_pair(Bs, wn * T::WN, kb, lane, fb[kb & 1]);
+        }
+    };
+    // The next k-block's fragment reads are issued ahead of this k-block's
+    // MFMAs (scheduling barriers keep that order), so only the first read of
+    // a slice waits on LDS latency.
     auto compute = [&](const float* As, const float* Bs) __attribute__((always_inline)) {
+        frags(As, Bs, 0);
 #pragma unroll
         for (int kb = 0; kb < T::BK / 8; ++kb) {
             const int set = kb & 1;
-#pragma unroll
-            for (int i = 0; i < T::TM; ++i) LA::frag(As, wm * T::WM + i * 32, kb, lane, fa[set][i]);
-#pragma unroll
-            for (int j = 0; j < T::TN; ++j) LB::frag(Bs, wn * T::WN + j * 32, kb, lane, fb[set][j]);
+            if (kb + 1 < T::BK / 8) frags(As, Bs, kb + 1);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int s = 0; s < 4; ++s)
 #pragma unroll
@@ -167,6 +286,7 @@ __global__ void __launch_bounds__(T::NT)
                     for (int j = 0; j < T::TN; ++j)
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[set][j][s], fa[set][i][s],
                                                                          acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
         }
     };
 
@@ -196,13 +316,16 @@ __global__ void __launch_bounds__(T::NT)
             if (has_next) nw = decode_tile<T, kDense>(p, nt);
         }
         issue(nw, nit, nxtA, nxtB);
+        // keep the loads ahead of the MFMAs (the scheduler would sink them to
+        // the barrier, exposing their whole latency)
+        __builtin_amdgcn_sched_barrier(0);
         compute(curA, curB);
         __syncthreads();
         if (!last) {
             ++it;
             return false;
         }
-        store_tile<T, kDense, BIAS>(p, C, ldc, c_vec, cur, acc, false, wm, wn, lane);
+        store_tile_direct<T, !A_KC, !B_KC, BIAS>(p, C, ldc, c_vec, cur, acc, wm, wn, lane);
 #pragma unroll
         for (int i = 0; i < T::TM; ++i)
 #pragma unroll
@@ -221,20 +344,36 @@ __global__ void __launch_bounds__(T::NT)
     }
 }
 
-// N/N launches of the 256 tile on dense problems with every slice full,
-// 16-byte aligned operands and K >= 1024 take direct staging.
+// Launches of the 256 tile on dense problems with every slice full (K and
+// the split chunk multiples of 32) and 16-byte operands take direct staging
+// when each split is deep enough.  Measured against the register-staged
+// kernel (same process, interleaved, MI355X): direct wins on every layout
+// from K = 512 per split (8192^3: +3-6 %; 8192^2 x 512: +2-5 %); at K = 256
+// N/N still wins (65536 x 512 x 256: +3 %, 8192^2 x 256: +5 %) but the other
+// layouts lose up to 6 % (65536 x 512 x 256 T/T).
 inline bool direct_ok(const GemmLaunch& g) {
+    // byte offsets within a slice (256 rows of a K-contiguous operand, 32 rows
+    // of an MN-contiguous one) fit 32 bits
+    const int64_t lim_a = g.op_a == 0 ? (INT64_C(1) << 21) : (INT64_C(1) << 24);
+    const int64_t lim_b = g.op_b != 0 ? (INT64_C(1) << 21) : (INT64_C(1) << 24);
+    const int64_t min_chunk = (g.op_a == 0 && g.op_b == 0) ? 256 : 512;
     return g.cfg == kCfg256 && g.structure == kDense && g.vec == 4 && g.K % 32 == 0 &&
-           g.k_chunk % 32 == 0 && g.k_chunk >= 1024 && g.op_a == 0 && g.op_b == 0;
+           g.k_chunk % 32 == 0 && g.k_chunk >= min_chunk && g.lda <= lim_a && g.ldb <= lim_b;
 }
 
-inline hipError_t launch_direct_nn(const GemmLaunch& g, hipStream_t s) {
+template <bool AT, bool BT>
+inline hipError_t launch_direct(const GemmLaunch& g, hipStream_t s) {
     const GemmParams p = make_params(g);
     dim3 grid((unsigned)g.grid_x, (unsigned)g.split_k, (unsigned)g.batch);
-    if (g.bias != nullptr && g.split_k == 1)
-        hipLaunchKernelGGL((gemm_f32_direct_kernel<Tile256, true>), grid, dim3(Tile256::NT), 0, s, p);
-    else
-        hipLaunchKernelGGL((gemm_f32_direct_kernel<Tile256, false>), grid, dim3(Tile256::NT), 0, s, p);
+    if constexpr (!AT && !BT) {  // the row bias exists for N/N only
+        if (g.bias != nullptr && g.split_k == 1) {
+            hipLaunchKernelGGL((gemm_f32_direct_kernel<Tile256, false, false, true>), grid,
+                               dim3(Tile256::NT), 0, s, p);
+            return hipGetLastError();
+        }
+    }
+    hipLaunchKernelGGL((gemm_f32_direct_kernel<Tile256, AT, BT, false>), grid, dim3(Tile256::NT),
+                       0, s, p);
     return hipGetLastError();
 }
 

@@ -196,7 +196,9 @@ __host__ __device__ __forceinline__ bool tile_of(const GemmParams& p, int bid, i
 // One output tile's assignment, uniform across the workgroup.
 struct TileWork {
     int tm, tn, k_begin, k_end, nk;
-    bool compute;
+    // 0 or 1; an int so that the struct has no padding bytes (copies of a
+    // padded struct keep the padding in memory -- here, in LDS)
+    int compute;
 };
 
 template <class T, int MODE>

@@ -126,24 +126,61 @@ def test_split_k_partition_and_determinism(ck, orc, dev, split, cfg):
         np.testing.assert_array_equal(o, outs[0])
 
 
-@pytest.mark.parametrize("M,N,K,batch", [(300, 520, 1056, 1), (257, 255, 2048, 1), (513, 260, 1024, 3),
-                                         (256, 256, 4096, 1)])
-def test_direct_staging_nn(ck, orc, dev, M, N, K, batch):
-    """The 256-tile N/N path with global->LDS direct loads (K % 32 == 0,
-    K >= 1024): edge rows and columns are loaded from the last valid
-    row/column and must not leak into stored outputs; batched and biased."""
-    a = orc.uniform((batch, M, K), 131)
-    b = orc.uniform((batch, K, N), 132)
+@pytest.mark.parametrize("op_a,op_b", LAYOUTS)
+@pytest.mark.parametrize("M,N,K,batch,pad", [(300, 520, 1056, 1, 0), (260, 252, 2048, 1, 4),
+                                             (257, 255, 2048, 1, 0), (516, 260, 1024, 3, 0),
+                                             (256, 256, 4096, 1, 8), (264, 300, 512, 2, 4),
+                                             (300, 264, 256, 1, 0)])
+def test_direct_staging(ck, orc, dev, op_a, op_b, M, N, K, batch, pad):
+    """The 256-tile path with direct global->LDS loads (K % 32 == 0, K >= 256
+    per split for N/N and >= 512 otherwise, 16-byte operands -- other shapes
+    take the register-staged kernel, as do contiguous extents that are not
+    multiples of 4): edge rows and columns are
+    loaded from the last valid row / column and must not leak into stored
+    outputs; padded leading dimensions; batched; row bias (N/N only)."""
+    a_st = orc.uniform((batch,) + ((K, M) if op_a else (M, K)), 131)
+    b_st = orc.uniform((batch,) + ((N, K) if op_b else (K, N)), 132)
     bias = orc.uniform((M,), 133)
-    A, B, Bi = to_dev(a), to_dev(b), to_dev(bias)
-    for with_bias in (False, True):
-        C = torch.full((batch, M, N), float("nan"), device="cuda")
-        args = gemm_args(ck, A, B, C, M, N, K, batch=batch, sa=M * K, sb=K * N, sc=M * N, override=3)
+    lda = (M if op_a else K) + pad
+    ldb = (K if op_b else N) + pad
+    ldc = N + pad
+    # padded storage: the logical operands sit in the leading columns
+    a_pad = np.zeros((batch, a_st.shape[1], lda), np.float32)
+    a_pad[:, :, :a_st.shape[2]] = a_st
+    b_pad = np.zeros((batch, b_st.shape[1], ldb), np.float32)
+    b_pad[:, :, :b_st.shape[2]] = b_st
+    A, B, Bi = to_dev(a_pad), to_dev(b_pad), to_dev(bias)
+    la = np.swapaxes(a_st, 1, 2) if op_a else a_st
+    lb = np.swapaxes(b_st, 1, 2) if op_b else b_st
+    for with_bias in ((False, True) if (op_a, op_b) == (0, 0) else (False,)):
+        C = torch.full((batch, M, ldc), float("nan"), device="cuda")
+        args = gemm_args(ck, A, B, C, M, N, K, op_a, op_b, batch=batch, lda=lda, ldb=ldb, ldc=ldc,
+                         sa=a_pad[0].size, sb=b_pad[0].size, sc=M * ldc, override=3)
         if with_bias:
             args.bias_m = Bi.data_ptr()
         ck.abi.check(run_gemm(ck, args))
-        ref = orc.gemm(a, b) + (bias.astype(np.float64)[None, :, None] if with_bias else 0.0)
-        assert_close(orc, to_host(C), ref, K, what=f"direct {M}x{N}x{K}x{batch} bias={with_bias}")
+        ref = orc.gemm(la, lb) + (bias.astype(np.float64)[None, :, None] if with_bias else 0.0)
+        got = to_host(C)
+        assert_close(orc, got[:, :, :N], ref, K,
+                     what=f"direct {op_a}{op_b} {M}x{N}x{K}x{batch} pad={pad} bias={with_bias}")
+        if pad:
+            assert np.isnan(got[:, :, N:]).all(), "a store landed in the ldc padding"
+
+
+@pytest.mark.parametrize("op_a,op_b", LAYOUTS)
+def test_direct_staging_split_k(ck, orc, dev, op_a, op_b):
+    """Split-K over the direct path: two 1024-deep chunks per tile, partials
+    reduced in fixed order."""
+    M, N, K = 260, 264, 2048
+    a_st, b_st = _host_operands(orc, M, N, K, op_a, op_b, 141)
+    A, B = to_dev(a_st), to_dev(b_st)
+    C = torch.full((M, N), float("nan"), device="cuda")
+    args = gemm_args(ck, A, B, C, M, N, K, op_a, op_b, override=3 | (2 << 8))
+    ws = workspace(ck, args)
+    args = gemm_args(ck, A, B, C, M, N, K, op_a, op_b, override=3 | (2 << 8), ws=ws)
+    ck.abi.check(run_gemm(ck, args))
+    assert_close(orc, to_host(C), orc.gemm(_logical(a_st, op_a), _logical(b_st, op_b)), K,
+                 what=f"direct split {op_a}{op_b}")
 
 
 def test_split_k_without_workspace_is_rejected(ck, dev):
