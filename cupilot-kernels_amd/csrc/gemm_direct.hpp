@@ -69,12 +69,11 @@ struct DirectLoader {
     static_assert(INSTR % NW == 0, "instructions must split evenly over the waves");
     static constexpr int PER_WAVE = INSTR / NW;
 
-    // Issue this wave's loads of the slice at (mn0, k0) into `lds`.  Offsets
-    // are taken from the slice's origin and fit 32 bits (direct_ok bounds ld).
-    __device__ __forceinline__ static void load(const float* __restrict__ base, int64_t ld, int mn0,
-                                                int mn_ext, int k0, float* lds, int wave, int lane) {
-        const __amdgpu_buffer_rsrc_t rsrc =
-            raw_rsrc(KCONTIG ? base + (int64_t)mn0 * ld + k0 : base + (int64_t)k0 * ld + mn0);
+    // Byte offsets, from a slice's origin, of this wave's loads for the tile
+    // at mn0 (the same for every slice of the tile, so computed once per
+    // tile).  They fit 32 bits: direct_ok bounds ld.
+    __device__ __forceinline__ static void offsets(int64_t ld, int mn0, int mn_ext, int wave,
+                                                   int lane, uint32_t (&vo)[PER_WAVE]) {
         const uint32_t ld4 = (uint32_t)ld * 4u;
 #pragma unroll
         for (int i = 0; i < PER_WAVE; ++i) {
@@ -83,13 +82,26 @@ struct DirectLoader {
                 const int r = ins * 8 + (lane >> 3);          // tile row this lane fills
                 const int q = (lane & 7) ^ (r & 7);           // global chunk for its slot
                 const int rr = mn0 + r < mn_ext ? r : mn_ext - 1 - mn0;
-                load_lds16(rsrc, (uint32_t)rr * ld4 + (uint32_t)q * 16u, lds + ins * 8 * BK);
+                vo[i] = (uint32_t)rr * ld4 + (uint32_t)q * 16u;
             } else {
-                const int k = ins;
                 // (mn_ext - mn0 is a positive multiple of 4: vec4 operands)
                 const int c = mn0 + lane * 4 + 3 < mn_ext ? lane * 4 : mn_ext - 4 - mn0;
-                load_lds16(rsrc, (uint32_t)k * ld4 + (uint32_t)c * 4u, lds + row_of(k) * LD);
+                vo[i] = (uint32_t)ins * ld4 + (uint32_t)c * 4u;
             }
+        }
+    }
+
+    // Issue this wave's loads of the slice at (mn0, k0) into `lds`; per
+    // slice only the (scalar) descriptor base moves.
+    __device__ __forceinline__ static void load(const float* __restrict__ base, int64_t ld, int mn0,
+                                                int k0, const uint32_t (&vo)[PER_WAVE], float* lds,
+                                                int wave) {
+        const __amdgpu_buffer_rsrc_t rsrc =
+            raw_rsrc(KCONTIG ? base + (int64_t)mn0 * ld + k0 : base + (int64_t)k0 * ld + mn0);
+#pragma unroll
+        for (int i = 0; i < PER_WAVE; ++i) {
+            const int ins = wave * PER_WAVE + i;
+            load_lds16(rsrc, vo[i], lds + (KCONTIG ? ins * 8 * BK : row_of(ins) * LD));
         }
     }
 
@@ -217,7 +229,8 @@ __global__ void __launch_bounds__(T::NT)
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    // wave-uniform, made scalar so LDS destinations (M0) need no readfirstlane
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / T::WAVES_N;
     const int wn = wave % T::WAVES_N;
     const int batch = blockIdx.z;
@@ -243,10 +256,16 @@ __global__ void __launch_bounds__(T::NT)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
+    // load offsets of the tile whose slices are being issued
+    uint32_t voA[LA::PER_WAVE], voB[LB::PER_WAVE];
+    auto set_offsets = [&](const TileWork& w) __attribute__((always_inline)) {
+        LA::offsets(p.lda, w.tm * T::BM, p.M, wave, lane, voA);
+        LB::offsets(p.ldb, w.tn * T::BN, p.N, wave, lane, voB);
+    };
     auto issue = [&](const TileWork& w, int it, float* dA, float* dB) __attribute__((always_inline)) {
         const int k0 = w.k_begin + it * T::BK;
-        LA::load(A, p.lda, w.tm * T::BM, p.M, k0, dA, wave, lane);
-        LB::load(B, p.ldb, w.tn * T::BN, p.N, k0, dB, wave, lane);
+        LA::load(A, p.lda, w.tm * T::BM, k0, voA, dA, wave);
+        LB::load(B, p.ldb, w.tn * T::BN, k0, voB, dB, wave);
     };
     // fragments of one k-block, kept at kernel scope (two sets, by k-block parity)
     float fa[2][T::TM][4], fb[2][T::TN][4];
@@ -271,8 +290,12 @@ __global__ void __launch_bounds__(T::NT)
     // The next k-block's fragment reads are issued ahead of this k-block's
     // MFMAs (scheduling barriers keep that order), so only the first read of
     // a slice waits on LDS latency.
-    auto compute = [&](const float* As, const float* Bs) __attribute__((always_inline)) {
+    auto compute = [&](const float* As, const float* Bs, auto&& loads) __attribute__((always_inline)) {
         frags(As, Bs, 0);
+        // the next slice's loads go out while the first reads are in flight
+        __builtin_amdgcn_sched_barrier(0);
+        loads();
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int kb = 0; kb < T::BK / 8; ++kb) {
             const int set = kb & 1;
@@ -294,6 +317,7 @@ __global__ void __launch_bounds__(T::NT)
     if (t >= p.num_tiles) return;
     TileWork cur = decode_tile<T, kDense>(p, t);
     int it = 0;
+    set_offsets(cur);
     issue(cur, 0, sA0, sB0);
     __syncthreads();
 
@@ -313,13 +337,14 @@ __global__ void __launch_bounds__(T::NT)
             nt = t + gridDim.x;
             has_next = nt < p.num_tiles;
             nit = has_next ? 0 : it;
-            if (has_next) nw = decode_tile<T, kDense>(p, nt);
+            if (has_next) {
+                nw = decode_tile<T, kDense>(p, nt);
+                set_offsets(nw);
+            }
         }
-        issue(nw, nit, nxtA, nxtB);
-        // keep the loads ahead of the MFMAs (the scheduler would sink them to
-        // the barrier, exposing their whole latency)
-        __builtin_amdgcn_sched_barrier(0);
-        compute(curA, curB);
+        // (the scheduling barriers keep the loads ahead of the MFMAs: the
+        // scheduler would sink them to the barrier, exposing their latency)
+        compute(curA, curB, [&]() __attribute__((always_inline)) { issue(nw, nit, nxtA, nxtB); });
         __syncthreads();
         if (!last) {
             ++it;
