@@ -5,6 +5,7 @@
 // other than an immutable per-device CU count.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cstdint>
 
@@ -130,6 +131,17 @@ int mi_gemm_tile_of(const mi_gemm_args* args, int32_t num_cus, int64_t item, int
         *k_begin = 0;
         *k_end = g.K;
         return 1;
+    }
+    if (g.tri_cap > 0) {
+        // chunked triangular list: 2 marks a chunk whose partial sum is
+        // stored in the mirror tile (tile_n, tile_m) and added in afterwards
+        int u0, u1, mirror;
+        tri_item((int)item, g.tiles_m, g.tri_cap, g.structure == kLower, tm, tn, u0, u1, mirror);
+        *tile_m = tm;
+        *tile_n = tn;
+        *k_begin = (int64_t)u0 * 256;
+        *k_end = std::min<int64_t>(g.K, (int64_t)u1 * 256);
+        return mirror ? 2 : 1;
     }
     const int bid = (int)item, nb = g.num_tiles;
 #define MI_TILE_OF(BMN)                                                                        \

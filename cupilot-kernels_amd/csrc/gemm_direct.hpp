@@ -151,26 +151,38 @@ struct DirectLoader {
 //                column 2 i' + t of block t, so for each r / 4 a lane holds 8
 //                consecutive columns (two 16-byte stores); K-contiguous B puts
 //                it at 32 j + i' (4 consecutive columns per r / 4).
-template <class T, bool A_IL, bool B_IL, bool BIAS>
+//
+// Triangular modes write +0.0 on the wrong side of the diagonal, except for a
+// chunk whose partial sum goes to the mirror tile: it is stored unmasked at
+// (tn, tm) -- the same offsets within the tile -- for tri_finish to add in.
+template <class T, bool A_IL, bool B_IL, bool BIAS, int MODE>
 __device__ __forceinline__ void store_tile_direct(const GemmParams& p, float* C, int64_t ldc,
                                                   bool c_vec, const TileWork& w,
                                                   const f16v (&acc)[T::TM][T::TN], int wm, int wn,
                                                   int lane) {
     static_assert(!B_IL || T::TN == 2, "one interleaved pair of column blocks per wave");
     static_assert(!A_IL || T::TM % 2 == 0, "row blocks pair up");
+    const bool to_mirror = MODE != kDense && w.mirror;
+    const bool tri_mask = MODE != kDense && !w.mirror;
+    const int r0 = (to_mirror ? w.tn : w.tm) * T::BM;
+    const int c0 = (to_mirror ? w.tm : w.tn) * T::BN;
     const int l32 = lane & 31;
-    const int cw = w.tn * T::BN + wn * T::WN + (lane >> 5) * 4;
+    const int cw = c0 + wn * T::WN + (lane >> 5) * 4;
     const bool add_bias = BIAS && p.split_k == 1;
 #pragma unroll
     for (int i = 0; i < T::TM; ++i) {
-        const int row = w.tm * T::BM + wm * T::WM +
-                        (A_IL ? 64 * (i / 2) + 2 * l32 + (i & 1) : 32 * i + l32);
+        const int row = r0 + wm * T::WM + (A_IL ? 64 * (i / 2) + 2 * l32 + (i & 1) : 32 * i + l32);
         if (row >= p.M) continue;
         const float bv = add_bias ? p.bias[row] : 0.f;
         float* const crow = C + (int64_t)row * ldc;
         // one 16-byte group: columns col .. col + 3 get v
         auto put = [&](int col, f4 v) __attribute__((always_inline)) {
             if (add_bias) v += bv;
+            if (tri_mask) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (MODE == kLower ? col + e > row : col + e < row) v[e] = 0.f;
+            }
             if (c_vec && col + 3 < p.N) {
                 *reinterpret_cast<f4*>(crow + col) = v;
             } else {
@@ -213,11 +225,17 @@ __device__ __forceinline__ void store_tile_direct(const GemmParams& p, float* C,
 // a tile's last slice issue its stores.  The two LDS buffers of each operand
 // are separate __shared__ objects and the slice loop is unrolled by two, so
 // each access names its buffer at compile time.
-template <class T, bool AT, bool BT, bool BIAS>
+//
+// MODE kLower / kUpper: the chunked triangular work list (tri_item), one item
+// per workgroup (grid = items, dispatched longest first).  Operand entries on
+// the wrong side of the diagonal are zeroed in the fragments of the diagonal
+// K unit (tril(A) tril(B) / triu(A) triu(B) for any input).
+template <class T, bool AT, bool BT, bool BIAS, int MODE = kDense>
 __global__ void __launch_bounds__(T::NT)
     __attribute__((amdgpu_waves_per_eu(T::WAVES_PER_SIMD, T::WAVES_PER_SIMD)))
     gemm_f32_direct_kernel(const GemmParams p) {
     static_assert(T::BM == 256 && T::BN == 256 && T::BK == 32, "direct staging is built for Tile256");
+    static_assert(MODE == kDense || (!AT && !BT), "triangular products are N/N");
     constexpr bool A_KC = !AT;  // A row-major (M x K) is contiguous along K
     constexpr bool B_KC = BT;   // B stored N x K is contiguous along K
     using LA = DirectLoader<A_KC, T::NW>;
@@ -267,8 +285,27 @@ __global__ void __launch_bounds__(T::NT)
         LA::load(A, p.lda, w.tm * T::BM, k0, voA, dA, wave);
         LB::load(B, p.ldb, w.tn * T::BN, k0, voB, dB, wave);
     };
+    auto decode = [&](int item) __attribute__((always_inline)) -> TileWork {
+        if constexpr (MODE == kDense) {
+            return decode_tile<T, kDense>(p, item);
+        } else {
+            TileWork w;
+            int u0, u1;
+            tri_item(item, p.tiles_m, p.tri_cap, MODE == kLower, w.tm, w.tn, u0, u1, w.mirror);
+            // (the work list is planned only for N a multiple of 256)
+            w.k_begin = u0 * T::BM;
+            w.k_end = u1 * T::BM;
+            w.nk = (w.k_end - w.k_begin) / T::BK;
+            w.compute = 1;
+            return w;
+        }
+    };
     // fragments of one k-block, kept at kernel scope (two sets, by k-block parity)
     float fa[2][T::TM][4], fb[2][T::TN][4];
+    // Triangular modes: the slice lies in one K unit; in the unit of A's row
+    // tile (mask_a) / B's column tile (mask_b) entries past the diagonal read
+    // as zero.  kl0 = the slice's first k within that unit.
+    int mask_a = 0, mask_b = 0, kl0 = 0;
     // (every lambda here is force-inlined: a call would pass the accumulators
     // through scratch memory)
     auto frags = [&](const float* As, const float* Bs, int kb) __attribute__((always_inline)) {
@@ -285,6 +322,27 @@ __global__ void __launch_bounds__(T::NT)
             for (int j = 0; j < T::TN; ++j) LB::frag(Bs, wn * T::WN + j * 32, kb, lane, fb[kb & 1][j]);
         } else {
             LB::frag_pair(Bs, wn * T::WN, kb, lane, fb[kb & 1]);
+        }
+        if constexpr (MODE != kDense) {
+            const int klb = kl0 + 8 * kb + 4 * (lane >> 5);  // + s
+            if (mask_a) {  // A(m, k): lower keeps k <= m, upper k >= m
+#pragma unroll
+                for (int i = 0; i < T::TM; ++i) {
+                    const int ml = wm * T::WM + 32 * i + (lane & 31);
+#pragma unroll
+                    for (int s = 0; s < 4; ++s)
+                        if (MODE == kLower ? klb + s > ml : klb + s < ml) fa[kb & 1][i][s] = 0.f;
+                }
+            }
+            if (mask_b) {  // B(k, n): lower keeps n <= k, upper n >= k
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    const int nl = wn * T::WN + 2 * (lane & 31) + t;
+#pragma unroll
+                    for (int s = 0; s < 4; ++s)
+                        if (MODE == kLower ? nl > klb + s : nl < klb + s) fb[kb & 1][t][s] = 0.f;
+                }
+            }
         }
     };
     // The next k-block's fragment reads are issued ahead of this k-block's
@@ -315,7 +373,7 @@ __global__ void __launch_bounds__(T::NT)
 
     int t = blockIdx.x;
     if (t >= p.num_tiles) return;
-    TileWork cur = decode_tile<T, kDense>(p, t);
+    TileWork cur = decode(t);
     int it = 0;
     set_offsets(cur);
     issue(cur, 0, sA0, sB0);
@@ -338,9 +396,16 @@ __global__ void __launch_bounds__(T::NT)
             has_next = nt < p.num_tiles;
             nit = has_next ? 0 : it;
             if (has_next) {
-                nw = decode_tile<T, kDense>(p, nt);
+                nw = decode(nt);
                 set_offsets(nw);
             }
+        }
+        if constexpr (MODE != kDense) {
+            const int k0 = cur.k_begin + it * T::BK;
+            const int unit = k0 / T::BM;
+            mask_a = unit == cur.tm;
+            mask_b = unit == cur.tn;
+            kl0 = k0 - unit * T::BM;
         }
         // (the scheduling barriers keep the loads ahead of the MFMAs: the
         // scheduler would sink them to the barrier, exposing their latency)
@@ -350,7 +415,7 @@ __global__ void __launch_bounds__(T::NT)
             ++it;
             return false;
         }
-        store_tile_direct<T, !A_KC, !B_KC, BIAS>(p, C, ldc, c_vec, cur, acc, wm, wn, lane);
+        store_tile_direct<T, !A_KC, !B_KC, BIAS, MODE>(p, C, ldc, c_vec, cur, acc, wm, wn, lane);
 #pragma unroll
         for (int i = 0; i < T::TM; ++i)
 #pragma unroll
@@ -384,6 +449,24 @@ inline bool direct_ok(const GemmLaunch& g) {
     const int64_t min_chunk = (g.op_a == 0 && g.op_b == 0) ? 256 : 512;
     return g.cfg == kCfg256 && g.structure == kDense && g.vec == 4 && g.K % 32 == 0 &&
            g.k_chunk % 32 == 0 && g.k_chunk >= min_chunk && g.lda <= lim_a && g.ldb <= lim_b;
+}
+
+// Triangular N/N products on the chunked work list (the scheduler plans it
+// when N is a multiple of 256 and the direct path's operand conditions hold),
+// then the pass that folds the mirror partials in and zeroes the rest of the
+// zero triangle.
+inline hipError_t launch_direct_tri(const GemmLaunch& g, hipStream_t s) {
+    const GemmParams p = make_params(g);
+    dim3 grid((unsigned)g.num_tiles, 1, 1);
+    if (g.structure == kLower)
+        hipLaunchKernelGGL((gemm_f32_direct_kernel<Tile256, false, false, false, kLower>), grid,
+                           dim3(Tile256::NT), 0, s, p);
+    else
+        hipLaunchKernelGGL((gemm_f32_direct_kernel<Tile256, false, false, false, kUpper>), grid,
+                           dim3(Tile256::NT), 0, s, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return launch_tri_finish(g.C, g.ldc, g.tiles_m, g.tri_cap, g.structure == kLower, s);
 }
 
 template <bool AT, bool BT>

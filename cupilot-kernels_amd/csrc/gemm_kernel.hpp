@@ -196,9 +196,10 @@ __host__ __device__ __forceinline__ bool tile_of(const GemmParams& p, int bid, i
 // One output tile's assignment, uniform across the workgroup.
 struct TileWork {
     int tm, tn, k_begin, k_end, nk;
-    // 0 or 1; an int so that the struct has no padding bytes (copies of a
+    // 0 or 1 (ints, so that the struct has no padding bytes: copies of a
     // padded struct keep the padding in memory -- here, in LDS)
     int compute;
+    int mirror;  // chunked triangular list: partial sum goes to tile (tn, tm)
 };
 
 template <class T, int MODE>
@@ -207,6 +208,7 @@ __device__ __forceinline__ TileWork decode_tile(const GemmParams& p, int tile) {
     w.compute = tile_of<T::BM, T::BN, MODE>(p, tile, p.num_tiles, blockIdx.y, w.tm, w.tn,
                                             w.k_begin, w.k_end);
     w.nk = w.compute && w.k_end > w.k_begin ? (w.k_end - w.k_begin + T::BK - 1) / T::BK : 0;
+    w.mirror = 0;
     return w;
 }
 
@@ -428,6 +430,7 @@ inline GemmParams make_params(const GemmLaunch& g) {
     p.sc = g.sc;
     p.num_tiles = g.num_tiles;
     p.col_splits = g.col_splits;
+    p.tri_cap = g.tri_cap;
     p.ws_batch_stride = (int64_t)g.M * g.N;
     p.ws_split_stride = p.ws_batch_stride * g.batch;
     return p;

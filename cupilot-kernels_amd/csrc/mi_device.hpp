@@ -65,6 +65,69 @@ __host__ __device__ __forceinline__ bool tri_tile(int pid, int nt, bool lower, i
     return false;
 }
 
+// Chunked triangular work list (the 256-tile direct kernel).  Structure tile
+// (tm, tn) reduces L = |tm - tn| + 1 tile-widths ("units") of K starting at
+// unit min(tm, tn).  A tile longer than cap units is cut in two: its first
+// cap units, written to C, and the rest, written to the mirror tile (tn, tm)
+// -- which lies in the zero triangle, so C itself holds the partial sum until
+// the finishing pass adds it in and zeroes the mirror.  Items run longest
+// first, so workgroups dispatched in order as CUs free up balance the load:
+// for l = cap, cap - 1, ..., 1 come the whole tiles of length l (distance
+// l - 1 from the diagonal), then (l == cap only) the first chunks of every
+// long tile, longest tile first, then the second chunks of length l.
+// Requires 2 cap >= nt (every second chunk is at most cap long).
+__host__ __device__ __forceinline__ int tri_items(int nt, int cap) {
+    const int nl = nt > cap ? nt - cap : 0;
+    return nt * (nt + 1) / 2 + nl * (nl + 1) / 2;
+}
+
+// Item pid of that list: its tile, its K range [u0, u1) in units, and
+// whether it goes to the mirror tile.
+__host__ __device__ __forceinline__ void tri_item(int pid, int nt, int cap, bool lower, int& tm,
+                                                  int& tn, int& u0, int& u1, int& mirror) {
+    int rem = pid, d = 0, r = 0, first = 0, len = 0;
+    mirror = 0;
+    for (int l = cap; l >= 1; --l) {
+        if (rem < nt - (l - 1)) {  // whole tiles of length l
+            d = l - 1;
+            r = rem;
+            len = l;
+            break;
+        }
+        rem -= nt - (l - 1);
+        if (l == cap) {  // first chunks of the long tiles, L = nt down to cap + 1
+            bool found = false;
+            for (int L = nt; L > cap; --L) {
+                if (rem < nt - L + 1) {
+                    d = L - 1;
+                    r = rem;
+                    len = cap;
+                    found = true;
+                    break;
+                }
+                rem -= nt - L + 1;
+            }
+            if (found) break;
+        }
+        const int L = l + cap;  // second chunks of length l
+        if (L <= nt) {
+            if (rem < nt - L + 1) {
+                d = L - 1;
+                r = rem;
+                first = cap;
+                len = l;
+                mirror = 1;
+                break;
+            }
+            rem -= nt - L + 1;
+        }
+    }
+    tm = lower ? r + d : r;
+    tn = lower ? r : r + d;
+    u0 = r + first;
+    u1 = u0 + len;
+}
+
 __device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
     uint64_t z = x + 0x9E3779B97F4A7C15ULL;
     z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;

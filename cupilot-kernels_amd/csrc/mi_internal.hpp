@@ -61,6 +61,7 @@ struct GemmLaunch {
     int num_tiles;        // output tiles per (split, batch): tiles_m*tiles_n, or tiles_m^2 (triangular)
     int grid_x;           // workgroups per (split, batch), <= num_tiles; each walks its tiles
     int col_splits;       // panel configs: column runs per A row panel
+    int tri_cap;          // > 0: chunked triangular work list (tri_item) of the direct kernel
 };
 
 // Kernel-side parameter block (passed by value).
@@ -74,6 +75,7 @@ struct GemmParams {
     int tiles_m, tiles_n, group_m;
     int num_tiles;
     int col_splits;
+    int tri_cap;
     int k_chunk, split_k;
     int64_t lda, ldb, ldc;
     int64_t sa, sb, sc;
@@ -88,6 +90,11 @@ hipError_t launch_gemm_tt(const GemmLaunch& g, hipStream_t s);
 
 hipError_t launch_splitk_reduce(const float* ws, float* C, int M, int N, int batch, int split_k,
                                 int64_t ldc, int64_t sc, const float* bias, hipStream_t s);
+// After the chunked triangular direct kernel: for every tile of the zero
+// triangle, add it into its mirror compute tile when that tile was cut in two
+// (it holds the second chunk's partial sum), then write it with +0.0.  C is
+// nt*256 square.
+hipError_t launch_tri_finish(float* C, int64_t ldc, int nt, int cap, bool lower, hipStream_t s);
 // C[b][r][c] = bias ? bias[r] : 0 (a contraction with K = 0)
 hipError_t launch_fill_zero_2d(float* C, int64_t rows, int64_t cols, int64_t ld, int64_t batch,
                                int64_t batch_stride, hipStream_t s, const float* bias = nullptr);

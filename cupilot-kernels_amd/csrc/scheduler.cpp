@@ -19,6 +19,7 @@
 #include <cstdint>
 
 #include "../../include/mi355_gemm.h"
+#include "mi_device.hpp"
 #include "mi_internal.hpp"
 
 namespace mi {
@@ -117,9 +118,30 @@ int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
         !((override_cfg == kCfg128K32 || override_cfg == kCfg128K64 || is_panel_cfg(override_cfg)) &&
           a.K > cfg_info(override_cfg).bk) &&
         !(is_panel_cfg(override_cfg) && a.structure != MI_DENSE);
+    // Triangular products with N a multiple of 256 and operands the direct
+    // kernel can stage run on the 256-tile direct kernel over the chunked
+    // longest-first work list (tri_item) when the structure has a tile for
+    // every CU (or the 256 config is asked for).  Tiles longer than a CU's
+    // share of the work are cut in two (cap = ceil(nt / 2) units), so the
+    // longest item no longer sets the finishing time; an override split
+    // (>= ceil(nt / 2)) sets the cap instead.
+    int tri_cap = 0;
+    if (a.structure != MI_DENSE && a.N % 256 == 0 && choose_vec(a) == 4 &&
+        a.lda <= (INT64_C(1) << 21) && a.ldb <= (INT64_C(1) << 24)) {
+        const int64_t nt = a.N / 256;
+        const bool wanted =
+            override_ok ? override_cfg == kCfg256 : nt * (nt + 1) / 2 >= (int64_t)num_cus;
+        if (wanted) {
+            const double units_per_cu = (double)nt * (nt + 1) * (nt + 2) / 6.0 / num_cus;
+            tri_cap = (int)(units_per_cu < (double)nt ? (nt + 1) / 2 : nt);
+            if (override_ok && override_split > 0)
+                tri_cap = (int)std::min<int64_t>(nt, std::max<int64_t>((nt + 1) / 2, override_split));
+        }
+    }
     if (a.structure != MI_DENSE) {
         best_cfg = a.N > 2048 ? kCfg128 : kCfg64;
         if (override_ok) best_cfg = override_cfg;
+        if (tri_cap > 0) best_cfg = kCfg256;
     } else if (override_ok) {
         best_cfg = override_cfg;
         best_split = is_panel_cfg(override_cfg) ? 1 : std::max(1, override_split);
@@ -173,7 +195,9 @@ int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
     // an override split larger than K allows collapses to what K can feed
     best_split = (int)std::min<int64_t>(best_split, cdiv(std::max<int64_t>(a.K, 1), k_chunk));
     if (best_split > 65535) return MI_ERR_BAD_SIZE;
-    const int64_t num_tiles = a.structure != MI_DENSE ? tiles_m * tiles_m : tiles_m * tiles_n;
+    const int64_t num_tiles = tri_cap > 0              ? tri_items((int)tiles_m, tri_cap)
+                              : a.structure != MI_DENSE ? tiles_m * tiles_m
+                                                        : tiles_m * tiles_n;
     if (num_tiles > INT32_MAX) return MI_ERR_BAD_SIZE;
     // Persistent grid: as many workgroups as the CUs hold at once (a multiple
     // of the 8 XCDs so every workgroup keeps to one XCD), each walking the
@@ -240,6 +264,7 @@ int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
         g.num_tiles = (int)num_tiles;
         g.col_splits = (int)col_splits;
         g.grid_x = (int)grid;
+        g.tri_cap = tri_cap;
     }
     return MI_OK;
 }

@@ -368,6 +368,47 @@ hipError_t launch_fill_zero_2d(float* C, int64_t rows, int64_t cols, int64_t ld,
     return hipGetLastError();
 }
 
+// One workgroup per (zero-triangle tile, quarter of its 256 rows).  Zero
+// tile (a, b) is the mirror of compute tile (b, a); when that tile was longer
+// than cap K units its second chunk's partial sum sits here and is added to
+// the first chunk's result (one fixed-order fp32 add).
+template <bool VEC>
+__global__ void __launch_bounds__(256)
+    tri_finish_kernel(float* __restrict__ C, int64_t ldc, int nt, int cap, int lower) {
+    int a, b;
+    tri_tile(nt * (nt + 1) / 2 + (int)blockIdx.x, nt, lower != 0, a, b);
+    const bool add = (a > b ? a - b : b - a) + 1 > cap;
+    const int64_t row0 = (int64_t)blockIdx.y * 64;
+    float* const z0 = C + ((int64_t)a * 256 + row0) * ldc + (int64_t)b * 256;
+    float* const d0 = C + ((int64_t)b * 256 + row0) * ldc + (int64_t)a * 256;
+    for (int e = threadIdx.x; e < 64 * 64; e += 256) {
+        const int r = e >> 6, c = (e & 63) * 4;
+        float* const z = z0 + (int64_t)r * ldc + c;
+        float* const d = d0 + (int64_t)r * ldc + c;
+        if (VEC) {
+            if (add) *reinterpret_cast<f4*>(d) += *reinterpret_cast<const f4*>(z);
+            *reinterpret_cast<f4*>(z) = f4{0.f, 0.f, 0.f, 0.f};
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                if (add) d[q] += z[q];
+                z[q] = 0.f;
+            }
+        }
+    }
+}
+
+hipError_t launch_tri_finish(float* C, int64_t ldc, int nt, int cap, bool lower, hipStream_t s) {
+    const int zero_tiles = nt * (nt - 1) / 2;
+    if (zero_tiles == 0) return hipSuccess;
+    const dim3 grid((unsigned)zero_tiles, 4);
+    if (ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(C) & 15u) == 0)
+        hipLaunchKernelGGL(tri_finish_kernel<true>, grid, dim3(256), 0, s, C, ldc, nt, cap, (int)lower);
+    else
+        hipLaunchKernelGGL(tri_finish_kernel<false>, grid, dim3(256), 0, s, C, ldc, nt, cap, (int)lower);
+    return hipGetLastError();
+}
+
 __global__ void fill_uniform_kernel(float* __restrict__ out, int64_t n, uint64_t base) {
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * blockDim.x)

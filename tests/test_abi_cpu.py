@@ -125,7 +125,7 @@ def _cover(ck, args, num_cus=256):
     for s in range(p.split_k):
         for wg in range(p.num_tiles):
             rc, tm, tn, kb, ke = ck.abi.tile_of(args, wg, s, num_cus)
-            assert rc in (0, 1)
+            assert rc in (0, 1, 2)
             seen.setdefault((tm, tn), []).append((rc, kb, ke))
     return p, seen
 
@@ -147,7 +147,7 @@ def test_dense_tiles_cover_output_once_and_partition_k(ck, M, N, K):
 
 
 @pytest.mark.parametrize("structure", [1, 2])
-@pytest.mark.parametrize("n,cfg", [(640, 0), (8192, 0), (1000, 1), (300, 3), (64, 2)])
+@pytest.mark.parametrize("n,cfg", [(640, 0), (8000, 0), (1000, 1), (300, 3), (64, 2), (2048, 2)])
 def test_triangular_enumeration(ck, structure, n, cfg):
     args = ck.abi.make_args(n, n, n, structure=structure, plan_override=cfg)
     p, seen = _cover(ck, args)
@@ -169,6 +169,51 @@ def test_triangular_enumeration(ck, structure, n, cfg):
         lengths.append(ke - kb)
     assert all(x >= y for x, y in zip(lengths[:-T], lengths[T:])) or T == 1
     assert lengths[0] == max(lengths)
+
+
+@pytest.mark.parametrize("structure", [1, 2])
+@pytest.mark.parametrize("n,override,cap", [(8192, 0, 16), (1024, 3, 2), (2048, 3 | (5 << 8), 5),
+                                            (2048, 3 | (8 << 8), 8), (1536, 3 | (1 << 8), 3),
+                                            (16384, 0, 64), (6144, 0, 12)])
+def test_triangular_chunked_work_list(ck, structure, n, override, cap):
+    """N % 256 == 0 triangular products on the 256-tile direct kernel: every
+    structure tile's K range [min(tm,tn), max(tm,tn)+1) x 256 is covered by
+    one item, or -- tiles longer than cap units -- by a first chunk of cap
+    units (rc 1, to C) and the rest (rc 2, to the mirror tile); items run
+    longest first; zero-triangle tiles are not items (a finishing pass writes
+    them)."""
+    args = ck.abi.make_args(n, n, n, structure=structure, plan_override=override)
+    p, seen = _cover(ck, args)
+    T = n // 256
+    assert p.plan_id == 3 and p.tiles_m == T and p.split_k == 1
+    n_long = max(0, T - cap) * (max(0, T - cap) + 1) // 2
+    assert p.num_tiles == T * (T + 1) // 2 + n_long and p.grid == p.num_tiles
+    want = {(i, j) for i in range(T) for j in range(T) if (i >= j if structure == 1 else i <= j)}
+    assert set(seen) == want
+    for (tm, tn), parts in seen.items():
+        lo, hi = min(tm, tn), max(tm, tn)
+        L = hi - lo + 1
+        parts = sorted(parts, key=lambda x: x[1])
+        if L > cap:
+            assert [x[0] for x in parts] == [1, 2]
+            assert parts[0][1:] == (lo * 256, (lo + cap) * 256)
+            assert parts[1][1:] == ((lo + cap) * 256, (hi + 1) * 256)
+        else:
+            assert parts == [(1, lo * 256, (hi + 1) * 256)]
+    lengths = []
+    for wg in range(p.num_tiles):
+        rc, tm, tn, kb, ke = ck.abi.tile_of(args, wg)
+        lengths.append(ke - kb)
+    assert all(x >= y for x, y in zip(lengths, lengths[1:])), "items must run longest first"
+
+
+def test_triangular_chunked_plan_needs_direct_operands(ck):
+    # N not a multiple of 256, or a leading dimension the direct loads cannot
+    # address, keeps the classic enumeration (one tile per item, zero tiles
+    # included)
+    for n, kw in [(8000, {}), (8192, dict(lda=8194))]:
+        rc, p = ck.abi.plan(n, n, n, structure=1, **kw)
+        assert rc == 0 and p.num_tiles == p.tiles_m ** 2 and p.plan_id != 3
 
 
 def test_xcd_remap_groups_neighbouring_tiles(ck):

@@ -248,6 +248,40 @@ def test_triangular_products(ck, orc, dev, structure, n, cfg):
 
 
 @pytest.mark.parametrize("structure", [1, 2])
+@pytest.mark.parametrize("n,override", [(1024, 3), (1536, 3 | (1 << 8)), (2048, 3 | (5 << 8)),
+                                        (2048, 3 | (8 << 8)), (768, 3)])
+@pytest.mark.parametrize("triangular_inputs", [True, False])
+def test_triangular_chunked_direct(ck, orc, dev, structure, n, override, triangular_inputs):
+    """The 256-tile direct kernel on the chunked longest-first work list: long
+    tiles are cut in two, the second chunk's partial parked in the mirror tile
+    of the zero triangle and added by the finishing pass.  Checks parity,
+    +0.0 structural zeros (the parked partials must be gone), the masking of
+    non-triangular inputs, the ldc padding, and run-to-run bitwise equality."""
+    tri = np.tril if structure == 1 else np.triu
+    a, b = orc.uniform((n, n), 75), orc.uniform((n, n), 76)
+    if triangular_inputs:
+        a, b = tri(a), tri(b)
+    ldc = n + 4
+    A, B = to_dev(a), to_dev(b)
+    outs = []
+    for _ in range(2):
+        C = torch.full((n, ldc), float("nan"), device="cuda")
+        args = gemm_args(ck, A, B, C, n, n, n, ldc=ldc, structure=structure, override=override)
+        rc, p = ck.abi.plan(n, n, n, structure=structure, plan_override=override, ldc=ldc)
+        assert p.plan_id == 3 and p.num_tiles != p.tiles_m ** 2, "expected the chunked work list"
+        ck.abi.check(run_gemm(ck, args))
+        outs.append(to_host(C))
+    got = outs[0]
+    assert np.isnan(got[:, n:]).all(), "a store landed in the ldc padding"
+    got = got[:, :n]
+    assert_close(orc, got, orc.gemm(a, b, structure), n, what=f"tri-direct {structure} n={n}")
+    zero = np.triu(np.ones((n, n), bool), 1) if structure == 1 else np.tril(np.ones((n, n), bool), -1)
+    z = got[zero]
+    assert np.all(z == 0.0) and not np.any(np.signbit(z)), "structural zeros must be +0.0"
+    np.testing.assert_array_equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("structure", [1, 2])
 def test_triangular_masks_non_triangular_input(ck, orc, dev, structure):
     # The operator is tril(tril(A) tril(B)) / triu(triu(A) triu(B)): entries of
     # the inputs outside the triangle must not leak into the result.
