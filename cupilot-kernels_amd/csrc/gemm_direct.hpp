@@ -14,10 +14,13 @@
 //     the wave's own loads first) publishes the whole next slice.
 // A wave's 64 lanes fill 1 KiB of contiguous LDS, which fixes the layouts:
 //   K-contiguous operand: [mn][32] with the 16-byte chunks of row mn stored
-//     at chunk (q ^ (mn % 8)); a lane chooses which global chunk it loads so
-//     that its fixed LDS slot holds the right one.  The fragment read of 32
-//     consecutive rows at one chunk then touches 8 different bank groups per
-//     8 lanes (no conflicts) without padding.
+//     at chunk (q ^ ((mn / 2) % 8)); a lane chooses which global chunk it
+//     loads so that its fixed LDS slot holds the right one.  A fragment read
+//     (32 consecutive rows at one chunk) then puts any 16 consecutive rows --
+//     2 rows per 256 bytes of banks -- in 16 different 16-byte bank groups:
+//     no conflicts, no padding.  (Swizzling by mn % 8 instead left rows r and
+//     r + 8 in one bank group: rocprof counted LDS bank-conflict stalls on
+//     40-50 % of the LDS-active cycles of the N/N and N/T kernels.)
 //   MN-contiguous operand: [32][256 + 4], one k-row per wave instruction
 //     (the +4 padding sits between rows, where each instruction's base is
 //     free).  k-row k = 4 g + s sits at LDS row 8 s + g.
@@ -80,7 +83,7 @@ struct DirectLoader {
             const int ins = wave * PER_WAVE + i;
             if (KCONTIG) {
                 const int r = ins * 8 + (lane >> 3);          // tile row this lane fills
-                const int q = (lane & 7) ^ (r & 7);           // global chunk for its slot
+                const int q = (lane & 7) ^ ((r >> 1) & 7);    // global chunk for its slot
                 const int rr = mn0 + r < mn_ext ? r : mn_ext - 1 - mn0;
                 vo[i] = (uint32_t)rr * ld4 + (uint32_t)q * 16u;
             } else {
@@ -117,7 +120,7 @@ struct DirectLoader {
         const int half = lane >> 5;
         const int l32 = lane & 31;
         const int row = r0 + l32;
-        const int q = (2 * kb + half) ^ (l32 & 7);  // r0 % 8 == 0, so row % 8 == l32 % 8
+        const int q = (2 * kb + half) ^ ((l32 >> 1) & 7);  // r0 % 16 == 0: row / 2 % 8 = l32 / 2 % 8
         const f4 t = *reinterpret_cast<const f4*>(lds + row * BK + q * 4);
         out[0] = t[0];
         out[1] = t[1];
