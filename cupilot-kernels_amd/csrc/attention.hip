@@ -26,6 +26,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
+#include "gemm_direct.hpp"
 #include "mi_device.hpp"
 #include "mi_internal.hpp"
 
@@ -171,6 +174,204 @@ __global__ void __launch_bounds__(kHgThreads) __attribute__((amdgpu_waves_per_eu
 }
 
 // ---------------------------------------------------------------------------
+// The same NT contraction on 256 x 256 tiles with direct LDS staging, for
+// the full-size shapes: 8 waves (2 x 4) of 128 x 64 (4 x 2 blocks), K in
+// 64-half (128-byte) slices.  A 64-half row is 32 floats, so the fp32 direct
+// loader stages both operands byte for byte (buffer_load_dwordx4 ... lds,
+// [row][32 floats] with its chunk swizzle), and its fragment read -- 16 bytes
+// of row r0 + lane % 32 at chunk 2 ks + lane / 32 -- is exactly the fp16
+// MFMA's operand (8 halves: k = 16 ks + 8 (lane / 32) .. + 7).  Persistent
+// over (batch, tile), XCD-remapped so the tiles of one batch entry share an
+// L2; per slice: first fragment reads, the next slice's loads, then the
+// MFMAs with the following k-step's reads issued ahead (as the fp32 kernel).
+// With 64 x 64 wave tiles (hgemm_nt_kernel) every MFMA needed 2 KiB of
+// fragment reads and the LDS read rate set the pace (~20 % of the MFMA peak).
+// ---------------------------------------------------------------------------
+template <bool OUT_HALF>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+    hgemm_direct_kernel(const HgemmParams p, int batch) {
+    constexpr int BM = 256, BN = 256, WM = 128, WN = 64, TM = 4, TN = 2, BKH = 64;
+    using L = DirectLoader<true, 8>;
+    __shared__ __attribute__((aligned(16))) float sA0[L::ELEMS];
+    __shared__ __attribute__((aligned(16))) float sA1[L::ELEMS];
+    __shared__ __attribute__((aligned(16))) float sB0[L::ELEMS];
+    __shared__ __attribute__((aligned(16))) float sB1[L::ELEMS];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 2, wn = wave & 3;
+    const int tiles_m = (p.M + BM - 1) / BM;
+    const int per_b = tiles_m * p.tiles_n;
+    const int total = per_b * batch;
+    const int nk = p.K / BKH;
+    const int64_t lda = p.lda / 2, ldb = p.ldb / 2;  // in floats
+
+    struct Work {
+        int b, tm, tn;
+    };
+    auto decode = [&](int t) {
+        const int id = xcd_remap(t, total);
+        Work w;
+        w.b = id / per_b;
+        const int r = id - w.b * per_b;
+        w.tm = r / p.tiles_n;
+        w.tn = r - w.tm * p.tiles_n;
+        return w;
+    };
+
+    uint32_t voA[L::PER_WAVE], voB[L::PER_WAVE];
+    auto set_offsets = [&](const Work& w) __attribute__((always_inline)) {
+        L::offsets(lda, w.tm * BM, p.M, wave, lane, voA);
+        L::offsets(ldb, w.tn * BN, p.N, wave, lane, voB);
+    };
+    auto issue = [&](const Work& w, int it, float* dA, float* dB) __attribute__((always_inline)) {
+        const int k0 = it * BKH;
+        const int kb = (p.b_kwrap > 0 && k0 >= p.b_kwrap) ? k0 - p.b_kwrap : k0;
+        const float* A = reinterpret_cast<const float*>(p.A + (int64_t)w.b * p.sa);
+        const float* B = reinterpret_cast<const float*>(p.B + (int64_t)w.b * p.sb);
+        L::load(A, lda, w.tm * BM, k0 / 2, voA, dA, wave);
+        L::load(B, ldb, w.tn * BN, kb / 2, voB, dB, wave);
+    };
+
+    f16v acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+    h8 fa[2][TM], fb[2][TN];
+    auto frags = [&](const float* As, const float* Bs, int ks) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            float t[4];
+            L::frag(As, wm * WM + i * 32, ks, lane, t);
+            fa[ks & 1][i] = __builtin_bit_cast(h8, f4{t[0], t[1], t[2], t[3]});
+        }
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            float t[4];
+            L::frag(Bs, wn * WN + j * 32, ks, lane, t);
+            fb[ks & 1][j] = __builtin_bit_cast(h8, f4{t[0], t[1], t[2], t[3]});
+        }
+    };
+    auto compute = [&](const float* As, const float* Bs, auto&& loads) __attribute__((always_inline)) {
+        frags(As, Bs, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        loads();
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int ks = 0; ks < BKH / 16; ++ks) {
+            if (ks + 1 < BKH / 16) frags(As, Bs, ks + 1);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    // B fragment as the row operand: the block holds C^T
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[ks & 1][j], fa[ks & 1][i],
+                                                                       acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    auto store = [&](const Work& w) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            const int row = w.tm * BM + wm * WM + i * 32 + (lane & 31);
+            if (row >= p.M) continue;
+            const int64_t roff = (int64_t)w.b * p.sc + (int64_t)row * p.ldc;
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int col = w.tn * BN + wn * WN + j * 32 + g * 8 + (lane >> 5) * 4;
+                    f4 v;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * g + e] * p.alpha;
+                    if (OUT_HALF) {
+                        _Float16* dst = static_cast<_Float16*>(p.C) + roff + col;
+                        if (col + 3 < p.N) {
+                            *reinterpret_cast<h4*>(dst) =
+                                h4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+                        } else {
+#pragma unroll
+                            for (int e = 0; e < 4; ++e)
+                                if (col + e < p.N) dst[e] = (_Float16)v[e];
+                        }
+                    } else {
+                        float* dst = static_cast<float*>(p.C) + roff + col;
+                        if (col + 3 < p.N) {
+                            *reinterpret_cast<f4*>(dst) = v;
+                        } else {
+#pragma unroll
+                            for (int e = 0; e < 4; ++e)
+                                if (col + e < p.N) dst[e] = v[e];
+                        }
+                    }
+                }
+        }
+    };
+
+    int t = blockIdx.x;
+    if (t >= total) return;
+    Work cur = decode(t);
+    int it = 0;
+    set_offsets(cur);
+    issue(cur, 0, sA0, sB0);
+    __syncthreads();
+    auto slice = [&](auto cb_tag) __attribute__((always_inline)) -> bool {
+        constexpr int CB = decltype(cb_tag)::value;
+        const float* const curA = CB == 0 ? sA0 : sA1;
+        const float* const curB = CB == 0 ? sB0 : sB1;
+        float* const nxtA = CB == 0 ? sA1 : sA0;
+        float* const nxtB = CB == 0 ? sB1 : sB0;
+        const bool last = it + 1 >= nk;
+        int nt = t;
+        bool has_next = true;
+        Work nw = cur;
+        int nit = it + 1;
+        if (last) {
+            nt = t + gridDim.x;
+            has_next = nt < total;
+            nit = has_next ? 0 : it;
+            if (has_next) {
+                nw = decode(nt);
+                set_offsets(nw);
+            }
+        }
+        if (it == p.k_switch) {
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) acc[i][j] *= p.switch_mul;
+        }
+        compute(curA, curB, [&]() __attribute__((always_inline)) { issue(nw, nit, nxtA, nxtB); });
+        __syncthreads();
+        if (!last) {
+            ++it;
+            return false;
+        }
+        store(cur);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+        if (!has_next) return true;
+        t = nt;
+        cur = nw;
+        it = 0;
+        return false;
+    };
+    for (;;) {
+        if (slice(std::integral_constant<int, 0>{})) break;
+        if (slice(std::integral_constant<int, 1>{})) break;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Row softmax with the two-term fp16 split.  One wave per row of S (n values,
 // row stride lds floats); writes the P' row (2 * sp halves) [H | 0 pad | L | 0 pad]
 // with 2^14 p = H + 2^-11 L.  Rows up to 64 * VPL values stay in registers
@@ -231,25 +432,40 @@ __global__ void __launch_bounds__(256)
 }
 
 // ---------------------------------------------------------------------------
-// Vt[b] (E x sp) = V[b]^T, zero for keys >= n.  64 x 64 tiles through LDS
-// so both the read (along E) and the write (along keys) coalesce.
+// Vt[b] (E x sp) = V[b]^T, zero for keys >= n.  64 x 64 tiles through LDS:
+// 16-byte loads (8 halves along E) and 16-byte stores (8 halves along the
+// keys), so both sides move whole 128-byte lines per 8 lanes; E % 8 == 0 and
+// sp % 64 == 0 (16-byte aligned rows).  (Element-wise loads and stores ran at
+// 2.5 TB/s.)
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(256)
     transpose_kernel(const _Float16* __restrict__ V, _Float16* __restrict__ Vt, int n, int E, int sp) {
-    __shared__ _Float16 tile[64][65];
+    constexpr int LDH = 64 + 8;  // halves per LDS row (16-byte aligned rows)
+    __shared__ __attribute__((aligned(16))) _Float16 tile[64 * LDH];
     const int b = blockIdx.z;
     const int k0 = blockIdx.y * 64, e0 = blockIdx.x * 64;
     const _Float16* v = V + (int64_t)b * n * E;
     _Float16* vt = Vt + (int64_t)b * E * (int64_t)sp;
-    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-    for (int r = ty; r < 64; r += 4) {
-        const int k = k0 + r, e = e0 + tx;
-        tile[r][tx] = (k < n && e < E) ? v[(int64_t)k * E + e] : (_Float16)0.f;
+    const int t = threadIdx.x;
+    const int c = (t & 7) * 8;  // 8-half chunk within a 64-wide row
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+        const int r = pass * 32 + (t >> 3);  // key row of the tile
+        const int k = k0 + r, e = e0 + c;
+        h8 x = h8{};
+        if (k < n && e < E) x = *reinterpret_cast<const h8*>(v + (int64_t)k * E + e);
+        *reinterpret_cast<h8*>(&tile[r * LDH + c]) = x;
     }
     __syncthreads();
-    for (int r = ty; r < 64; r += 4) {
-        const int e = e0 + r, k = k0 + tx;
-        if (e < E && k < sp) vt[(int64_t)e * sp + k] = tile[tx][r];
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+        const int r = pass * 32 + (t >> 3);  // E row of the output tile
+        const int e = e0 + r, k = k0 + c;
+        if (e >= E) continue;
+        h8 y;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) y[j] = tile[(c + j) * LDH + r];
+        *reinterpret_cast<h8*>(vt + (int64_t)e * sp + k) = y;
     }
 }
 
@@ -268,6 +484,27 @@ hipError_t launch_hgemm(const HgemmParams& p, int batch, hipStream_t s) {
     const int tiles_m = (p.M + kHgBM - 1) / kHgBM;
     dim3 grid((unsigned)(tiles_m * p.tiles_n), 1u, (unsigned)batch);
     hipLaunchKernelGGL((hgemm_nt_kernel<OUT_HALF>), grid, dim3(kHgThreads), 0, s, p);
+    return hipGetLastError();
+}
+
+// The 256-tile direct kernel, persistent over (batch, tile): one workgroup per
+// CU (its LDS holds two 64-deep slices of both 256-row operands).  p.tiles_n
+// counts 256-wide tiles.  Byte offsets within a slice (256 rows) fit 32 bits
+// for lda, ldb < 2^22 halves.
+template <bool OUT_HALF>
+hipError_t launch_hgemm_direct(HgemmParams p, int batch, hipStream_t s) {
+    if (p.lda >= (INT64_C(1) << 22) || p.ldb >= (INT64_C(1) << 22))
+        return launch_hgemm<OUT_HALF>(p, batch, s);
+    p.tiles_n = (p.N + 255) / 256;
+    const int total = ((p.M + 255) / 256) * p.tiles_n * batch;
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) == hipSuccess) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+            cus = v;
+    }
+    const int grid = total < cus ? total : cus;
+    hipLaunchKernelGGL((hgemm_direct_kernel<OUT_HALF>), dim3((unsigned)grid), dim3(512), 0, s, p, batch);
     return hipGetLastError();
 }
 
@@ -315,7 +552,7 @@ hipError_t launch_sdpa(const _Float16* Q, const _Float16* K, const _Float16* V, 
         q.k_switch = -1;
         q.switch_mul = 1.0f;
         q.b_kwrap = 0;
-        hipError_t e = launch_hgemm<false>(q, hc, s);
+        hipError_t e = launch_hgemm_direct<false>(q, hc, s);
         if (e != hipSuccess) return e;
         // 2. P' = split softmax rows
         const int64_t rows = (int64_t)hc * seq;
@@ -355,7 +592,7 @@ hipError_t launch_sdpa(const _Float16* Q, const _Float16* K, const _Float16* V, 
         o.k_switch = sp / kHgBK;       // first slice of the L half
         o.switch_mul = 2048.0f;        // 2^11: H.V -> 2^11 H.V, then + L.V
         o.alpha = 1.0f / (16384.0f * 2048.0f);  // 2^-25
-        if ((e = launch_hgemm<true>(o, hc, s)) != hipSuccess) return e;
+        if ((e = launch_hgemm_direct<true>(o, hc, s)) != hipSuccess) return e;
     }
     return hipSuccess;
 }

@@ -35,7 +35,8 @@ def _check(orc, got, q, k, v, what):
 
 
 @pytest.mark.parametrize("shape", [(1, 1, 512, 1024), (2, 3, 100, 1024), (1, 2, 1, 1024),
-                                   (1, 1, 33, 1024)])
+                                   (1, 1, 33, 1024), (1, 96, 512, 1024), (1, 130, 64, 1024),
+                                   (2, 5, 300, 1024)])
 def test_fused_attention_operator(ck, orc, dev, shape):
     q, k, v = _inputs(orc, shape, 40)
     Q, K, V = to_dev(q), to_dev(k), to_dev(v)
