@@ -39,6 +39,12 @@ __global__ void __launch_bounds__(T::NT) gemm_f32_panel_kernel(const GemmParams 
     using LB = TileLoader<T::BN, T::KMAX, T::NT, B_KC, VEC>;
     __shared__ __attribute__((aligned(16))) float sA[LA::ELEMS];
     __shared__ __attribute__((aligned(16))) float sB[2][LB::ELEMS];
+    // 32-deep panels (small K, store-bound): each wave turns its finished
+    // 32 x 32 blocks into whole-row stores through a [32][36] staging block
+    // (the 64-deep panel's LDS has no room for it)
+    constexpr bool STAGE_C = T::KMAX == 32;
+    constexpr int SCLD = 36;
+    __shared__ __attribute__((aligned(16))) float sC[STAGE_C ? T::NW * 32 * SCLD : 4];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -96,27 +102,59 @@ __global__ void __launch_bounds__(T::NT) gemm_f32_panel_kernel(const GemmParams 
         }
         __syncthreads();
 
-        // Fast path: the item's tiles are all interior, K fills every k-block
-        // and rows are 16-byte aligned, so every store is unconditional.  Two
+        // Fast path: the item's tiles are all interior and rows are 16-byte
+        // aligned, so every store is unconditional; K may leave trailing
+        // k-blocks of a 32-deep panel empty.  Two
         // accumulator sets: while tile s is computed, tile s-1 is stored, a
         // few 16-byte stores after each k-block of MFMAs, so stores and MFMAs
         // overlap inside each wave instead of alternating.
-        const bool fast = c_vec && nkb == T::KMAX / 8 && m0 + T::BM <= p.M &&
-                          (int64_t)tn_end * T::BN <= p.N && run >= 2;
+        // (the 64-deep panel takes it only when K fills all its k-blocks: there
+        // a per-k-block skip test cost 6 % on the MFMA-bound tall-skinny shape)
+        constexpr bool SKIP_KB = T::KMAX == 32;
+        const bool fast = c_vec && m0 + T::BM <= p.M && (int64_t)tn_end * T::BN <= p.N && run >= 2 &&
+                          (SKIP_KB || nkb == T::KMAX / 8);
         if (fast) {
             constexpr int KBLK = T::KMAX / 8;
-            constexpr int NST = T::TM * T::TN * 4;   // 16-byte stores per wave per tile
+            // store units per wave per tile: 16-byte stores, or whole blocks
+            // when staged through LDS
+            constexpr int NST = STAGE_C ? T::TM * T::TN : T::TM * T::TN * 4;
             constexpr int SPK = (NST + KBLK - 1) / KBLK;
             f16v acc0[T::TM][T::TN], acc1[T::TM][T::TN];
 
             auto store_one = [&](const f16v (&acc)[T::TM][T::TN], int q, int tn) {
-                const int i = q / (T::TN * 4), j = (q / 4) % T::TN, g = q % 4;
-                const int row = m0 + wm * T::WM + i * 32 + (lane & 31);
-                const int col = tn * T::BN + wn * T::WN + j * 32 + g * 8 + half * 4;
-                f4 v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
-                        acc[i][j][4 * g + 3]};
-                if (add_bias) v += bias_r[i];
-                *reinterpret_cast<f4*>(C + (int64_t)row * p.ldc + col) = v;
+                if constexpr (STAGE_C) {
+                    // block (i, j): write it in its C^T register layout (lane l:
+                    // row l % 32, columns 8 g + 4 h .. +3), read it back as rows
+                    // (lane L: row 8 r + L / 8, columns 4 (L % 8) .. +3), so each
+                    // 16-byte store has 8 lanes covering one whole 128-byte row
+                    // segment.  One wave's LDS operations run in order, so the
+                    // reads see the writes and the next block's writes follow them.
+                    const int i = q / T::TN, j = q % T::TN;
+                    float* const buf = sC + wave * (32 * SCLD);
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        f4 v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                                acc[i][j][4 * g + 3]};
+                        if (add_bias) v += bias_r[i];
+                        *reinterpret_cast<f4*>(buf + (lane & 31) * SCLD + g * 8 + half * 4) = v;
+                    }
+                    const int r0 = m0 + wm * T::WM + i * 32;
+                    const int c0 = tn * T::BN + wn * T::WN + j * 32 + (lane & 7) * 4;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int rr = r * 8 + (lane >> 3);
+                        const f4 v = *reinterpret_cast<const f4*>(buf + rr * SCLD + (lane & 7) * 4);
+                        *reinterpret_cast<f4*>(C + (int64_t)(r0 + rr) * p.ldc + c0) = v;
+                    }
+                } else {
+                    const int i = q / (T::TN * 4), j = (q / 4) % T::TN, g = q % 4;
+                    const int row = m0 + wm * T::WM + i * 32 + (lane & 31);
+                    const int col = tn * T::BN + wn * T::WN + j * 32 + g * 8 + half * 4;
+                    f4 v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                            acc[i][j][4 * g + 3]};
+                    if (add_bias) v += bias_r[i];
+                    *reinterpret_cast<f4*>(C + (int64_t)row * p.ldc + col) = v;
+                }
             };
             // MFMAs of one tile from LDS buffer `buf` into acc_c; with
             // STORE, the previous tile's stores ride along, SPK per k-block.
@@ -130,19 +168,23 @@ __global__ void __launch_bounds__(T::NT) gemm_f32_panel_kernel(const GemmParams 
                         for (int r = 0; r < 16; ++r) acc_c[i][j][r] = 0.f;
 #pragma unroll
                 for (int kb = 0; kb < KBLK; ++kb) {
-                    float a[T::TM][4], b[T::TN][4];
+                    // k-blocks past K hold only zero fill: their MFMAs are
+                    // skipped, the stores riding along with them are not
+                    if (!SKIP_KB || kb < nkb) {
+                        float a[T::TM][4], b[T::TN][4];
 #pragma unroll
-                    for (int i = 0; i < T::TM; ++i) LA::frag(sA, wm * T::WM + i * 32, kb, lane, a[i]);
+                        for (int i = 0; i < T::TM; ++i) LA::frag(sA, wm * T::WM + i * 32, kb, lane, a[i]);
 #pragma unroll
-                    for (int j = 0; j < T::TN; ++j) LB::frag(Bs, wn * T::WN + j * 32, kb, lane, b[j]);
+                        for (int j = 0; j < T::TN; ++j) LB::frag(Bs, wn * T::WN + j * 32, kb, lane, b[j]);
 #pragma unroll
-                    for (int s = 0; s < 4; ++s)
+                        for (int s = 0; s < 4; ++s)
 #pragma unroll
-                        for (int i = 0; i < T::TM; ++i)
+                            for (int i = 0; i < T::TM; ++i)
 #pragma unroll
-                            for (int j = 0; j < T::TN; ++j)
-                                acc_c[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(b[j][s], a[i][s],
-                                                                                   acc_c[i][j], 0, 0, 0);
+                                for (int j = 0; j < T::TN; ++j)
+                                    acc_c[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(b[j][s], a[i][s],
+                                                                                       acc_c[i][j], 0, 0, 0);
+                    }
                     if (store) {
 #pragma unroll
                         for (int qq = 0; qq < SPK; ++qq)

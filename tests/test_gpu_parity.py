@@ -183,6 +183,28 @@ def test_direct_staging_split_k(ck, orc, dev, op_a, op_b):
                  what=f"direct split {op_a}{op_b}")
 
 
+@pytest.mark.parametrize("op_a,op_b", LAYOUTS)
+@pytest.mark.parametrize("K,cfg", [(32, 6), (64, 7), (30, 6), (24, 6), (5, 6), (40, 7)])
+def test_panel_fast_path(ck, orc, dev, op_a, op_b, K, cfg):
+    """The A-panel kernel's fast path (interior tiles, runs of >= 2 column
+    tiles: 4096 x 4096 gives 16 row panels x 16 runs of 2): stores of one tile
+    overlap the next tile's MFMAs; 32-deep panels stage each 32 x 32 block
+    through LDS to store whole rows.  With and without the row bias (N/N)."""
+    M = N = 4096
+    a_st, b_st = _host_operands(orc, M, N, K, op_a, op_b, 151)
+    bias = orc.uniform((M,), 153)
+    A, B, Bi = to_dev(a_st), to_dev(b_st), to_dev(bias)
+    ref = orc.gemm(_logical(a_st, op_a), _logical(b_st, op_b))
+    for with_bias in ((False, True) if (op_a, op_b) == (0, 0) else (False,)):
+        C = torch.full((M, N), float("nan"), device="cuda")
+        args = gemm_args(ck, A, B, C, M, N, K, op_a, op_b, override=cfg)
+        if with_bias:
+            args.bias_m = Bi.data_ptr()
+        ck.abi.check(run_gemm(ck, args))
+        want = ref + (bias.astype(np.float64)[:, None] if with_bias else 0.0)
+        assert_close(orc, to_host(C), want, K, what=f"panel {op_a}{op_b} K={K} bias={with_bias}")
+
+
 def test_split_k_without_workspace_is_rejected(ck, dev):
     M, N, K = 64, 64, 8192
     A = torch.zeros((M, K), device="cuda")
