@@ -112,7 +112,11 @@ MI_API int mi_gemm_plan(const mi_gemm_args* args, int32_t num_cus, mi_plan* out)
  * `item` (0 <= item < mi_plan.num_tiles; workgroup w runs items w, w + grid,
  * ...) of split `split` under the plan mi_gemm_f32 would use on a device with
  * num_cus compute units.  Returns 1 for a compute tile, 0 for a
- * structural-zero tile (triangular products), a negative mi_status on error. */
+ * structural-zero tile (triangular products), 2 for a K chunk of a long
+ * triangular tile whose partial sum is parked in the mirror tile
+ * (tile_n, tile_m) of the zero triangle and added in by a finishing pass
+ * (the chunked work list of triangular products with N % 256 == 0), a
+ * negative mi_status on error. */
 MI_API int mi_gemm_tile_of(const mi_gemm_args* args, int32_t num_cus, int64_t item, int32_t split,
                            int32_t* tile_m, int32_t* tile_n, int64_t* k_begin, int64_t* k_end);
 
