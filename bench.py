@@ -72,6 +72,7 @@ PLAN_KERNELS = {
     5: "gemm_f32_kernel<Tile<128,128,64,64,64,2,1>>",
     6: "gemm_f32_panel_kernel<PanelTile<256,128,32>>",
     7: "gemm_f32_panel_kernel<PanelTile<256,128,64>>",
+    8: "gemm_f32_panel_kernel<PanelTile<128,128,64,64,32>>",
 }
 
 

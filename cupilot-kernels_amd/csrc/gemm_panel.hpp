@@ -19,10 +19,10 @@
 
 namespace mi {
 
-template <int BM_, int BN_, int KMAX_>
+template <int BM_, int BN_, int KMAX_, int WM_ = 64, int WN_ = 64>
 struct PanelTile {
     static constexpr int BM = BM_, BN = BN_, KMAX = KMAX_;
-    static constexpr int WM = 64, WN = 64;  // wave tile: 2 x 2 MFMA blocks
+    static constexpr int WM = WM_, WN = WN_;  // wave tile
     static constexpr int WAVES_M = BM / WM, WAVES_N = BN / WN;
     static constexpr int NW = WAVES_M * WAVES_N, NT = NW * 64;
     static constexpr int TM = WM / 32, TN = WN / 32;
@@ -30,6 +30,9 @@ struct PanelTile {
 
 using Panel32 = PanelTile<256, 128, 32>;
 using Panel64 = PanelTile<256, 128, 64>;
+// 128-row panels (M = 128 .. 2047 not a multiple of 256: a 256-row panel
+// would spend MFMAs on padding rows), 8 waves of 64 x 32
+using Panel128x64 = PanelTile<128, 128, 64, 64, 32>;
 
 template <class T, bool AT, bool BT, int VEC, bool BIAS>
 __global__ void __launch_bounds__(T::NT) gemm_f32_panel_kernel(const GemmParams p) {
@@ -39,10 +42,11 @@ __global__ void __launch_bounds__(T::NT) gemm_f32_panel_kernel(const GemmParams 
     using LB = TileLoader<T::BN, T::KMAX, T::NT, B_KC, VEC>;
     __shared__ __attribute__((aligned(16))) float sA[LA::ELEMS];
     __shared__ __attribute__((aligned(16))) float sB[2][LB::ELEMS];
-    // 32-deep panels (small K, store-bound): each wave turns its finished
-    // 32 x 32 blocks into whole-row stores through a [32][36] staging block
-    // (the 64-deep panel's LDS has no room for it)
-    constexpr bool STAGE_C = T::KMAX == 32;
+    // Where LDS has room (the 32-deep and the 128-row panels, not the 256-row
+    // 64-deep one), each wave turns its finished 32 x 32 blocks into
+    // whole-row stores through a [32][36] staging block.
+    constexpr bool STAGE_C =
+        (LA::ELEMS + 2 * LB::ELEMS + T::NW * 32 * 36) * 4 <= 160 * 1024;
     constexpr int SCLD = 36;
     __shared__ __attribute__((aligned(16))) float sC[STAGE_C ? T::NW * 32 * SCLD : 4];
 
@@ -108,9 +112,10 @@ __global__ void __launch_bounds__(T::NT) gemm_f32_panel_kernel(const GemmParams 
         // accumulator sets: while tile s is computed, tile s-1 is stored, a
         // few 16-byte stores after each k-block of MFMAs, so stores and MFMAs
         // overlap inside each wave instead of alternating.
-        // (the 64-deep panel takes it only when K fills all its k-blocks: there
-        // a per-k-block skip test cost 6 % on the MFMA-bound tall-skinny shape)
-        constexpr bool SKIP_KB = T::KMAX == 32;
+        // (the 256-row 64-deep panel takes it only when K fills all its
+        // k-blocks: there a per-k-block skip test cost 6 % on the MFMA-bound
+        // tall-skinny shape)
+        constexpr bool SKIP_KB = T::KMAX == 32 || T::BM == 128;
         const bool fast = c_vec && m0 + T::BM <= p.M && (int64_t)tn_end * T::BN <= p.N && run >= 2 &&
                           (SKIP_KB || nkb == T::KMAX / 8);
         if (fast) {
@@ -307,6 +312,9 @@ hipError_t launch_panel(const GemmLaunch& g, hipStream_t s) {
             if (g.cfg == kCfgPanel32)
                 return g.vec == 4 ? launch_panel_one<Panel32, AT, BT, 4, true>(g, s)
                                   : launch_panel_one<Panel32, AT, BT, 1, true>(g, s);
+            if (g.cfg == kCfgPanel128x64)
+                return g.vec == 4 ? launch_panel_one<Panel128x64, AT, BT, 4, true>(g, s)
+                                  : launch_panel_one<Panel128x64, AT, BT, 1, true>(g, s);
             return g.vec == 4 ? launch_panel_one<Panel64, AT, BT, 4, true>(g, s)
                               : launch_panel_one<Panel64, AT, BT, 1, true>(g, s);
         }
@@ -314,6 +322,9 @@ hipError_t launch_panel(const GemmLaunch& g, hipStream_t s) {
     if (g.cfg == kCfgPanel32)
         return g.vec == 4 ? launch_panel_one<Panel32, AT, BT, 4>(g, s)
                           : launch_panel_one<Panel32, AT, BT, 1>(g, s);
+    if (g.cfg == kCfgPanel128x64)
+        return g.vec == 4 ? launch_panel_one<Panel128x64, AT, BT, 4>(g, s)
+                          : launch_panel_one<Panel128x64, AT, BT, 1>(g, s);
     return g.vec == 4 ? launch_panel_one<Panel64, AT, BT, 4>(g, s)
                       : launch_panel_one<Panel64, AT, BT, 1>(g, s);
 }

@@ -20,9 +20,11 @@ namespace mi {
 //   7   256 x 128 panel  8      64 x 64     A panel resident, K <= 64 (~137 KiB)
 enum TileCfgId {
     kCfg64 = 1, kCfg128 = 2, kCfg256 = 3, kCfg128K32 = 4, kCfg128K64 = 5,
-    kCfgPanel32 = 6, kCfgPanel64 = 7, kNumCfg = 8
+    kCfgPanel32 = 6, kCfgPanel64 = 7, kCfgPanel128x64 = 8, kNumCfg = 9
 };
-inline bool is_panel_cfg(int id) { return id == kCfgPanel32 || id == kCfgPanel64; }
+inline bool is_panel_cfg(int id) {
+    return id == kCfgPanel32 || id == kCfgPanel64 || id == kCfgPanel128x64;
+}
 
 struct CfgInfo {
     int bm, bn, bk, threads;
@@ -36,6 +38,7 @@ inline CfgInfo cfg_info(int id) {
         case kCfg128K64: return {128, 128, 64, 256};
         case kCfgPanel32: return {256, 128, 32, 512};
         case kCfgPanel64: return {256, 128, 64, 512};
+        case kCfgPanel128x64: return {128, 128, 64, 512};
         default: return {0, 0, 0, 0};
     }
 }

@@ -59,6 +59,7 @@ int resident_wgs(int cfg) {
         case kCfg128K64: return 2;
         case kCfgPanel32: return 1;
         case kCfgPanel64: return 1;
+        case kCfgPanel128x64: return 1;
         default: return 8;
     }
 }
@@ -145,6 +146,12 @@ int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
     } else if (override_ok) {
         best_cfg = override_cfg;
         best_split = is_panel_cfg(override_cfg) ? 1 : std::max(1, override_split);
+    } else if (a.K <= 64 && a.M % 128 == 0 && a.M % 256 != 0 && a.M < 2048 &&
+               cdiv(a.M, 128) * cdiv(a.N, 128) * std::max<int64_t>(1, a.batch) >=
+                   2 * (int64_t)num_cus) {
+        // The same for M an odd multiple of 128 (the 1x1 convolution's
+        // output channels): 128-row panels, none of them padding.
+        best_cfg = kCfgPanel128x64;
     } else if (a.K <= 64 && (a.M % 256 == 0 || a.M >= 2048) &&
                cdiv(a.M, 256) * cdiv(a.N, 128) * std::max<int64_t>(1, a.batch) >=
                    2 * (int64_t)num_cus) {

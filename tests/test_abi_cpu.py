@@ -83,7 +83,7 @@ def test_invalid_arguments_rejected_before_launch(ck):
 PLAN_CASES = [
     (8192, 8192, 8192, 1), (1024, 1024, 1024, 1), (1023, 517, 2049, 1), (1, 1, 1, 1),
     (512, 768, 1024, 128), (16384, 768, 2048, 1), (65536, 512, 256, 1), (16384, 16384, 32, 1),
-    (256, 256, 1 << 20, 1), (65536, 65536, 64, 1), (7, 300, 5, 3),
+    (256, 256, 1 << 20, 1), (65536, 65536, 64, 1), (7, 300, 5, 3), (128, 65536, 64, 16), (384, 65536, 40, 1),
 ]
 
 
@@ -92,14 +92,14 @@ def test_plan_is_sane(ck, M, N, K, batch):
     rc, p = ck.abi.plan(M, N, K, batch=batch, workspace_bytes=1 << 40)
     assert rc == 0
     assert p.block_m in (64, 128, 256) and p.block_k in (16, 32, 64)
-    assert p.block_m == p.block_n or p.plan_id in (6, 7)
+    assert p.block_m == p.block_n or p.plan_id in (6, 7, 8)
     assert p.tiles_m * p.block_m >= M > (p.tiles_m - 1) * p.block_m
     assert p.tiles_n * p.block_n >= N > (p.tiles_n - 1) * p.block_n
     assert p.num_tiles == p.tiles_m * p.tiles_n
     # persistent grid: no more workgroups than tiles, a multiple of the 8 XCDs
     # unless the tiles run out first
     assert 1 <= p.grid <= p.num_tiles
-    if p.plan_id not in (6, 7):  # panel plans size the grid by row panels x column runs
+    if p.plan_id not in (6, 7, 8):  # panel plans size the grid by row panels x column runs
         assert p.grid % 8 == 0 or p.grid == p.num_tiles
     assert p.k_chunk % p.block_k == 0
     assert p.k_chunk * p.split_k >= K > p.k_chunk * (p.split_k - 1)

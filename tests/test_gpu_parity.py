@@ -184,12 +184,14 @@ def test_direct_staging_split_k(ck, orc, dev, op_a, op_b):
 
 
 @pytest.mark.parametrize("op_a,op_b", LAYOUTS)
-@pytest.mark.parametrize("K,cfg", [(32, 6), (64, 7), (30, 6), (24, 6), (5, 6), (40, 7)])
+@pytest.mark.parametrize("K,cfg", [(32, 6), (64, 7), (30, 6), (24, 6), (5, 6), (40, 7), (64, 8), (40, 8),
+                                   (16, 8)])
 def test_panel_fast_path(ck, orc, dev, op_a, op_b, K, cfg):
     """The A-panel kernel's fast path (interior tiles, runs of >= 2 column
-    tiles: 4096 x 4096 gives 16 row panels x 16 runs of 2): stores of one tile
-    overlap the next tile's MFMAs; 32-deep panels stage each 32 x 32 block
-    through LDS to store whole rows.  With and without the row bias (N/N)."""
+    tiles: 4096 x 4096 gives 16 (32) row panels x 16 (8) runs of 2 (4)):
+    stores of one tile overlap the next tile's MFMAs; the 32-deep and the
+    128-row panels stage each 32 x 32 block through LDS to store whole rows.
+    With and without the row bias (N/N)."""
     M = N = 4096
     a_st, b_st = _host_operands(orc, M, N, K, op_a, op_b, 151)
     bias = orc.uniform((M,), 153)
@@ -203,6 +205,30 @@ def test_panel_fast_path(ck, orc, dev, op_a, op_b, K, cfg):
         ck.abi.check(run_gemm(ck, args))
         want = ref + (bias.astype(np.float64)[:, None] if with_bias else 0.0)
         assert_close(orc, to_host(C), want, K, what=f"panel {op_a}{op_b} K={K} bias={with_bias}")
+
+
+@pytest.mark.parametrize("M,batch", [(128, 2), (384, 1)])
+def test_panel_128_rows_auto(ck, orc, dev, M, batch):
+    """M an odd multiple of 128 with a large output and K <= 64 (the 1x1
+    convolution's shape) is planned on 128-row panels; the weight is
+    broadcast over the batch (stride_a = 0) and the row bias added."""
+    N, K = 65536, 64
+    rc, p = ck.abi.plan(M, N, K, batch=batch)
+    assert p.plan_id == 8
+    w = orc.uniform((M, K), 161)
+    x = orc.uniform((batch, K, N), 162)
+    bias = orc.uniform((M,), 163)
+    W, X, Bi = to_dev(w), to_dev(x), to_dev(bias)
+    C = torch.full((batch, M, N), float("nan"), device="cuda")
+    args = gemm_args(ck, W, X, C, M, N, K, batch=batch, sa=0, sb=K * N, sc=M * N)
+    args.bias_m = Bi.data_ptr()
+    ck.abi.check(run_gemm(ck, args))
+    got = to_host(C)
+    cols = np.r_[0:300, N - 300:N]  # sampled columns keep the fp64 oracle cheap
+    for b in range(batch):
+        ref = orc.gemm(w, np.ascontiguousarray(x[b][:, cols])) + bias.astype(np.float64)[:, None]
+        assert_close(orc, got[b][:, cols], ref, K, what=f"panel128 b={b}")
+    assert not np.isnan(got).any()
 
 
 def test_split_k_without_workspace_is_rejected(ck, dev):
