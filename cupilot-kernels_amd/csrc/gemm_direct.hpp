@@ -1,11 +1,16 @@
-// gemm_direct.hpp -- the 256 x 256 contraction (all four operand layouts)
-// with global -> LDS direct loads (gfx950 buffer_load_dwordx4 ... lds), for
-// dense problems whose slices are all full (K a multiple of 32, 16-byte
-// aligned operands) and deep enough (direct_ok).
+// gemm_direct.hpp -- the 256 x 256 and 128 x 128 contractions (all four
+// operand layouts) with global -> LDS direct loads (gfx950
+// buffer_load_dwordx4 ... lds), for dense problems whose slices are all full
+// (K a multiple of the slice depth, 16-byte aligned operands) and deep enough
+// (direct_ok).
 //
-// Same tile, waves and MFMA order as gemm_f32_kernel<Tile256> (so the same
-// results, bit for bit); what changes is the staging and, with it, the order
-// of rows / columns within a wave's MN-contiguous blocks.  Each lane's
+// Same tiles, waves and MFMA order as gemm_f32_kernel<Tile256> /
+// <Tile128> (so the same results, bit for bit); what changes is the staging
+// and, with it, the order of rows / columns within a wave's MN-contiguous
+// blocks.  The layouts below are given for the 256 tile's 32-deep slices; the
+// 128 tile's 16-deep ones follow the same rules (4 chunks per K-contiguous
+// row, swizzled by (mn / 4) % 4; two 128-float k-rows per MN-contiguous
+// instruction).  Each lane's
 // 16-byte global load lands in LDS at (wave's LDS base + 16 * lane) without
 // passing through VGPRs, so
 //   * no VGPRs hold the next slice (32 per lane in the register-staged kernel),
@@ -60,17 +65,31 @@ __device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, uint32_t vo
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_ptr)(lds), 16, (int)voff, 0, 0, 0);
 }
 
-// One operand of a 256 x 32 slice, staged directly into LDS by NW waves.
-template <bool KCONTIG, int NW>
+// One operand of a ROWS x BK slice (256 x 32 or 128 x 16), staged directly
+// into LDS by NW waves.
+template <bool KCONTIG, int NW, int ROWS = 256, int BK = 32>
 struct DirectLoader {
-    static constexpr int ROWS = 256, BK = 32;
-    static constexpr int LD = KCONTIG ? BK : ROWS + 4;
-    static constexpr int ELEMS = KCONTIG ? ROWS * BK : BK * LD;
-    // wave instructions per slice: 8 rows of 128 B (K-contiguous) or one
-    // k-row of 1 KiB (MN-contiguous) each
-    static constexpr int INSTR = KCONTIG ? ROWS / 8 : BK;
+    static_assert((ROWS == 256 && BK == 32) || (ROWS == 128 && BK == 16), "slice shapes built");
+    // K-contiguous: a row is CH 16-byte chunks; one wave instruction fills
+    // RPI rows; RPW rows share one 256-byte window of the 64 banks.
+    static constexpr int CH = BK / 4, RPI = 64 / CH, RPW = 64 / BK;
+    // MN-contiguous: one wave instruction fills KPI whole k-rows (1 KiB),
+    // followed by 4 floats of padding.
+    static constexpr int KPI = 256 / ROWS, IPITCH = KPI * ROWS + 4;
+    static constexpr int INSTR = KCONTIG ? ROWS / RPI : BK / KPI;
+    static constexpr int ELEMS = KCONTIG ? ROWS * BK : INSTR * IPITCH;
     static_assert(INSTR % NW == 0, "instructions must split evenly over the waves");
     static constexpr int PER_WAVE = INSTR / NW;
+
+    // MN-contiguous layout: LDS row rho holds k-row k_of(rho), where k =
+    // 4 g + s sits at rho = (BK / 4) s + g, so the four reads of one fragment
+    // (s = 0..3) are >= 2080 bytes apart.
+    __device__ __forceinline__ static constexpr int k_of(int rho) {
+        return 4 * (rho % (BK / 4)) + rho / (BK / 4);
+    }
+    __device__ __forceinline__ static constexpr int row_base(int rho) {
+        return (rho / KPI) * IPITCH + (rho % KPI) * ROWS;
+    }
 
     // Byte offsets, from a slice's origin, of this wave's loads for the tile
     // at mn0 (the same for every slice of the tile, so computed once per
@@ -82,14 +101,17 @@ struct DirectLoader {
         for (int i = 0; i < PER_WAVE; ++i) {
             const int ins = wave * PER_WAVE + i;
             if (KCONTIG) {
-                const int r = ins * 8 + (lane >> 3);          // tile row this lane fills
-                const int q = (lane & 7) ^ ((r >> 1) & 7);    // global chunk for its slot
+                const int r = ins * RPI + lane / CH;                 // tile row this lane fills
+                const int q = (lane % CH) ^ ((r / RPW) % CH);        // global chunk for its slot
                 const int rr = mn0 + r < mn_ext ? r : mn_ext - 1 - mn0;
                 vo[i] = (uint32_t)rr * ld4 + (uint32_t)q * 16u;
             } else {
+                constexpr int LPR = ROWS / 4;  // lanes per k-row
+                const int k = k_of(ins * KPI + lane / LPR);
                 // (mn_ext - mn0 is a positive multiple of 4: vec4 operands)
-                const int c = mn0 + lane * 4 + 3 < mn_ext ? lane * 4 : mn_ext - 4 - mn0;
-                vo[i] = (uint32_t)ins * ld4 + (uint32_t)c * 4u;
+                const int c0 = (lane % LPR) * 4;
+                const int c = mn0 + c0 + 3 < mn_ext ? c0 : mn_ext - 4 - mn0;
+                vo[i] = (uint32_t)k * ld4 + (uint32_t)c * 4u;
             }
         }
     }
@@ -104,12 +126,9 @@ struct DirectLoader {
 #pragma unroll
         for (int i = 0; i < PER_WAVE; ++i) {
             const int ins = wave * PER_WAVE + i;
-            load_lds16(rsrc, vo[i], lds + (KCONTIG ? ins * 8 * BK : row_of(ins) * LD));
+            load_lds16(rsrc, vo[i], lds + (KCONTIG ? ins * RPI * BK : ins * IPITCH));
         }
     }
-
-    // LDS row of k-row k (MN-contiguous layout)
-    __device__ __forceinline__ static constexpr int row_of(int k) { return (k & 3) * 8 + (k >> 2); }
 
     // K-contiguous operand: values for the 4 MFMA steps of k-block kb,
     // 32-row group at r0 (same k permutation as TileLoader::frag:
@@ -120,7 +139,8 @@ struct DirectLoader {
         const int half = lane >> 5;
         const int l32 = lane & 31;
         const int row = r0 + l32;
-        const int q = (2 * kb + half) ^ ((l32 >> 1) & 7);  // r0 % 16 == 0: row / 2 % 8 = l32 / 2 % 8
+        // r0 % 16 == 0, so (row / RPW) % CH = (l32 / RPW) % CH
+        const int q = (2 * kb + half) ^ ((l32 / RPW) % CH);
         const f4 t = *reinterpret_cast<const f4*>(lds + row * BK + q * 4);
         out[0] = t[0];
         out[1] = t[1];
@@ -135,10 +155,10 @@ struct DirectLoader {
                                                      float out[2][4]) {
         static_assert(!KCONTIG, "K-contiguous fragments are read one block at a time");
         const int g = 2 * kb + (lane >> 5);  // k = 4 g + s
-        const float* p = lds + g * LD + c0 + 2 * (lane & 31);
+        const int col = c0 + 2 * (lane & 31);
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-            const f2 t = *reinterpret_cast<const f2*>(p + s * 8 * LD);
+            const f2 t = *reinterpret_cast<const f2*>(lds + row_base(s * (BK / 4) + g) + col);
             out[0][s] = t[0];
             out[1][s] = t[1];
         }
@@ -237,12 +257,13 @@ template <class T, bool AT, bool BT, bool BIAS, int MODE = kDense>
 __global__ void __launch_bounds__(T::NT)
     __attribute__((amdgpu_waves_per_eu(T::WAVES_PER_SIMD, T::WAVES_PER_SIMD)))
     gemm_f32_direct_kernel(const GemmParams p) {
-    static_assert(T::BM == 256 && T::BN == 256 && T::BK == 32, "direct staging is built for Tile256");
-    static_assert(MODE == kDense || (!AT && !BT), "triangular products are N/N");
+    static_assert(T::STAGES == 2 && T::BM == T::BN, "double-buffered square tiles");
+    static_assert(MODE == kDense || (!AT && !BT && T::BM == 256),
+                  "triangular products are N/N on the 256 tile");
     constexpr bool A_KC = !AT;  // A row-major (M x K) is contiguous along K
     constexpr bool B_KC = BT;   // B stored N x K is contiguous along K
-    using LA = DirectLoader<A_KC, T::NW>;
-    using LB = DirectLoader<B_KC, T::NW>;
+    using LA = DirectLoader<A_KC, T::NW, T::BM, T::BK>;
+    using LB = DirectLoader<B_KC, T::NW, T::BN, T::BK>;
     __shared__ __attribute__((aligned(16))) float sA0[LA::ELEMS];
     __shared__ __attribute__((aligned(16))) float sA1[LA::ELEMS];
     __shared__ __attribute__((aligned(16))) float sB0[LB::ELEMS];
@@ -443,15 +464,29 @@ __global__ void __launch_bounds__(T::NT)
 // kernel (same process, interleaved, MI355X): direct wins on every layout
 // from K = 512 per split (8192^3: +3-6 %; 8192^2 x 512: +2-5 %); at K = 256
 // N/N still wins (65536 x 512 x 256: +3 %, 8192^2 x 256: +5 %) but the other
-// layouts lose up to 6 % (65536 x 512 x 256 T/T).
+// layouts lose up to 6 % (65536 x 512 x 256 T/T).  The 128 tile (16-deep
+// slices) likewise with K and the chunk multiples of 16.
+constexpr int64_t kDirect128MinChunk = 256;
+
 inline bool direct_ok(const GemmLaunch& g) {
-    // byte offsets within a slice (256 rows of a K-contiguous operand, 32 rows
-    // of an MN-contiguous one) fit 32 bits
-    const int64_t lim_a = g.op_a == 0 ? (INT64_C(1) << 21) : (INT64_C(1) << 24);
-    const int64_t lim_b = g.op_b != 0 ? (INT64_C(1) << 21) : (INT64_C(1) << 24);
-    const int64_t min_chunk = (g.op_a == 0 && g.op_b == 0) ? 256 : 512;
-    return g.cfg == kCfg256 && g.structure == kDense && g.vec == 4 && g.K % 32 == 0 &&
-           g.k_chunk % 32 == 0 && g.k_chunk >= min_chunk && g.lda <= lim_a && g.ldb <= lim_b;
+    if (g.structure != kDense || g.vec != 4) return false;
+    if (g.cfg == kCfg256) {
+        // byte offsets within a slice (256 rows of a K-contiguous operand, 32
+        // rows of an MN-contiguous one) fit 32 bits
+        const int64_t lim_a = g.op_a == 0 ? (INT64_C(1) << 21) : (INT64_C(1) << 24);
+        const int64_t lim_b = g.op_b != 0 ? (INT64_C(1) << 21) : (INT64_C(1) << 24);
+        const int64_t min_chunk = (g.op_a == 0 && g.op_b == 0) ? 256 : 512;
+        return g.K % 32 == 0 && g.k_chunk % 32 == 0 && g.k_chunk >= min_chunk &&
+               g.lda <= lim_a && g.ldb <= lim_b;
+    }
+    if (g.cfg == kCfg128) {
+        // 128 rows of a K-contiguous operand, 16 rows of an MN-contiguous one
+        const int64_t lim_a = g.op_a == 0 ? (INT64_C(1) << 22) : (INT64_C(1) << 25);
+        const int64_t lim_b = g.op_b != 0 ? (INT64_C(1) << 22) : (INT64_C(1) << 25);
+        return g.K % 16 == 0 && g.k_chunk % 16 == 0 && g.k_chunk >= kDirect128MinChunk &&
+               g.lda <= lim_a && g.ldb <= lim_b;
+    }
+    return false;
 }
 
 // Triangular N/N products on the chunked work list (the scheduler plans it
@@ -472,20 +507,25 @@ inline hipError_t launch_direct_tri(const GemmLaunch& g, hipStream_t s) {
     return launch_tri_finish(g.C, g.ldc, g.tiles_m, g.tri_cap, g.structure == kLower, s);
 }
 
-template <bool AT, bool BT>
-inline hipError_t launch_direct(const GemmLaunch& g, hipStream_t s) {
+template <class T, bool AT, bool BT>
+inline hipError_t launch_direct_tile(const GemmLaunch& g, hipStream_t s) {
     const GemmParams p = make_params(g);
     dim3 grid((unsigned)g.grid_x, (unsigned)g.split_k, (unsigned)g.batch);
     if constexpr (!AT && !BT) {  // the row bias exists for N/N only
         if (g.bias != nullptr && g.split_k == 1) {
-            hipLaunchKernelGGL((gemm_f32_direct_kernel<Tile256, false, false, true>), grid,
-                               dim3(Tile256::NT), 0, s, p);
+            hipLaunchKernelGGL((gemm_f32_direct_kernel<T, false, false, true>), grid, dim3(T::NT),
+                               0, s, p);
             return hipGetLastError();
         }
     }
-    hipLaunchKernelGGL((gemm_f32_direct_kernel<Tile256, AT, BT, false>), grid, dim3(Tile256::NT),
-                       0, s, p);
+    hipLaunchKernelGGL((gemm_f32_direct_kernel<T, AT, BT, false>), grid, dim3(T::NT), 0, s, p);
     return hipGetLastError();
+}
+
+template <bool AT, bool BT>
+inline hipError_t launch_direct(const GemmLaunch& g, hipStream_t s) {
+    return g.cfg == kCfg128 ? launch_direct_tile<Tile128, AT, BT>(g, s)
+                            : launch_direct_tile<Tile256, AT, BT>(g, s);
 }
 
 }  // namespace mi

@@ -126,18 +126,20 @@ def test_split_k_partition_and_determinism(ck, orc, dev, split, cfg):
         np.testing.assert_array_equal(o, outs[0])
 
 
+@pytest.mark.parametrize("cfg", [3, 2])
 @pytest.mark.parametrize("op_a,op_b", LAYOUTS)
 @pytest.mark.parametrize("M,N,K,batch,pad", [(300, 520, 1056, 1, 0), (260, 252, 2048, 1, 4),
                                              (257, 255, 2048, 1, 0), (516, 260, 1024, 3, 0),
                                              (256, 256, 4096, 1, 8), (264, 300, 512, 2, 4),
-                                             (300, 264, 256, 1, 0)])
-def test_direct_staging(ck, orc, dev, op_a, op_b, M, N, K, batch, pad):
-    """The 256-tile path with direct global->LDS loads (K % 32 == 0, K >= 256
-    per split for N/N and >= 512 otherwise, 16-byte operands -- other shapes
-    take the register-staged kernel, as do contiguous extents that are not
-    multiples of 4): edge rows and columns are
-    loaded from the last valid row / column and must not leak into stored
-    outputs; padded leading dimensions; batched; row bias (N/N only)."""
+                                             (300, 264, 256, 1, 0), (130, 132, 272, 1, 0)])
+def test_direct_staging(ck, orc, dev, cfg, op_a, op_b, M, N, K, batch, pad):
+    """The 256- and 128-tile paths with direct global->LDS loads (K a multiple
+    of the slice depth, 32 / 16; K >= 256 per split, and >= 512 for the 256
+    tile's layouts other than N/N; 16-byte operands -- other shapes take the
+    register-staged kernel, as do contiguous extents that are not multiples
+    of 4): edge rows and columns are loaded from the last valid row / column
+    and must not leak into stored outputs; padded leading dimensions; batched;
+    row bias (N/N only)."""
     a_st = orc.uniform((batch,) + ((K, M) if op_a else (M, K)), 131)
     b_st = orc.uniform((batch,) + ((N, K) if op_b else (K, N)), 132)
     bias = orc.uniform((M,), 133)
@@ -155,32 +157,33 @@ def test_direct_staging(ck, orc, dev, op_a, op_b, M, N, K, batch, pad):
     for with_bias in ((False, True) if (op_a, op_b) == (0, 0) else (False,)):
         C = torch.full((batch, M, ldc), float("nan"), device="cuda")
         args = gemm_args(ck, A, B, C, M, N, K, op_a, op_b, batch=batch, lda=lda, ldb=ldb, ldc=ldc,
-                         sa=a_pad[0].size, sb=b_pad[0].size, sc=M * ldc, override=3)
+                         sa=a_pad[0].size, sb=b_pad[0].size, sc=M * ldc, override=cfg)
         if with_bias:
             args.bias_m = Bi.data_ptr()
         ck.abi.check(run_gemm(ck, args))
         ref = orc.gemm(la, lb) + (bias.astype(np.float64)[None, :, None] if with_bias else 0.0)
         got = to_host(C)
         assert_close(orc, got[:, :, :N], ref, K,
-                     what=f"direct {op_a}{op_b} {M}x{N}x{K}x{batch} pad={pad} bias={with_bias}")
+                     what=f"direct cfg {cfg} {op_a}{op_b} {M}x{N}x{K}x{batch} pad={pad} bias={with_bias}")
         if pad:
             assert np.isnan(got[:, :, N:]).all(), "a store landed in the ldc padding"
 
 
+@pytest.mark.parametrize("cfg", [3, 2])
 @pytest.mark.parametrize("op_a,op_b", LAYOUTS)
-def test_direct_staging_split_k(ck, orc, dev, op_a, op_b):
+def test_direct_staging_split_k(ck, orc, dev, cfg, op_a, op_b):
     """Split-K over the direct path: two 1024-deep chunks per tile, partials
     reduced in fixed order."""
     M, N, K = 260, 264, 2048
     a_st, b_st = _host_operands(orc, M, N, K, op_a, op_b, 141)
     A, B = to_dev(a_st), to_dev(b_st)
     C = torch.full((M, N), float("nan"), device="cuda")
-    args = gemm_args(ck, A, B, C, M, N, K, op_a, op_b, override=3 | (2 << 8))
+    args = gemm_args(ck, A, B, C, M, N, K, op_a, op_b, override=cfg | (2 << 8))
     ws = workspace(ck, args)
-    args = gemm_args(ck, A, B, C, M, N, K, op_a, op_b, override=3 | (2 << 8), ws=ws)
+    args = gemm_args(ck, A, B, C, M, N, K, op_a, op_b, override=cfg | (2 << 8), ws=ws)
     ck.abi.check(run_gemm(ck, args))
     assert_close(orc, to_host(C), orc.gemm(_logical(a_st, op_a), _logical(b_st, op_b)), K,
-                 what=f"direct split {op_a}{op_b}")
+                 what=f"direct split cfg {cfg} {op_a}{op_b}")
 
 
 @pytest.mark.parametrize("op_a,op_b", LAYOUTS)
