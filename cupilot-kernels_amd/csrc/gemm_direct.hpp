@@ -465,8 +465,8 @@ __global__ void __launch_bounds__(T::NT)
 // from K = 512 per split (8192^3: +3-6 %; 8192^2 x 512: +2-5 %); at K = 256
 // N/N still wins (65536 x 512 x 256: +3 %, 8192^2 x 256: +5 %) but the other
 // layouts lose up to 6 % (65536 x 512 x 256 T/T).  The 128 tile (16-deep
-// slices) likewise with K and the chunk multiples of 16.
-constexpr int64_t kDirect128MinChunk = 256;
+// slices) takes it at any depth with K and the chunk multiples of 16 (it won
+// on every shape measured, K = 96 ... 3072).
 
 inline bool direct_ok(const GemmLaunch& g) {
     if (g.structure != kDense || g.vec != 4) return false;
@@ -483,8 +483,7 @@ inline bool direct_ok(const GemmLaunch& g) {
         // 128 rows of a K-contiguous operand, 16 rows of an MN-contiguous one
         const int64_t lim_a = g.op_a == 0 ? (INT64_C(1) << 22) : (INT64_C(1) << 25);
         const int64_t lim_b = g.op_b != 0 ? (INT64_C(1) << 22) : (INT64_C(1) << 25);
-        return g.K % 16 == 0 && g.k_chunk % 16 == 0 && g.k_chunk >= kDirect128MinChunk &&
-               g.lda <= lim_a && g.ldb <= lim_b;
+        return g.K % 16 == 0 && g.k_chunk % 16 == 0 && g.lda <= lim_a && g.ldb <= lim_b;
     }
     return false;
 }

@@ -131,11 +131,12 @@ def test_split_k_partition_and_determinism(ck, orc, dev, split, cfg):
 @pytest.mark.parametrize("M,N,K,batch,pad", [(300, 520, 1056, 1, 0), (260, 252, 2048, 1, 4),
                                              (257, 255, 2048, 1, 0), (516, 260, 1024, 3, 0),
                                              (256, 256, 4096, 1, 8), (264, 300, 512, 2, 4),
-                                             (300, 264, 256, 1, 0), (130, 132, 272, 1, 0)])
+                                             (300, 264, 256, 1, 0), (130, 132, 272, 1, 0),
+                                             (200, 196, 80, 2, 4)])
 def test_direct_staging(ck, orc, dev, cfg, op_a, op_b, M, N, K, batch, pad):
     """The 256- and 128-tile paths with direct global->LDS loads (K a multiple
-    of the slice depth, 32 / 16; K >= 256 per split, and >= 512 for the 256
-    tile's layouts other than N/N; 16-byte operands -- other shapes take the
+    of the slice depth, 32 / 16; for the 256 tile K >= 256 per split, and >=
+    512 in the layouts other than N/N; 16-byte operands -- other shapes take the
     register-staged kernel, as do contiguous extents that are not multiples
     of 4): edge rows and columns are loaded from the last valid row / column
     and must not leak into stored outputs; padded leading dimensions; batched;
