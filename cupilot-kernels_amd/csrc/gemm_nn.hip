@@ -7,7 +7,7 @@ namespace mi {
 hipError_t launch_gemm_nn(const GemmLaunch& g, hipStream_t s) {
     if (is_panel_cfg(g.cfg)) return launch_panel<false, false>(g, s);
     if (g.tri_cap > 0) return launch_direct_tri(g, s);
-    if (direct_ok(g)) return launch_direct<false, false>(g, s);
+    if (direct_ok(g) || direct4_ok(g)) return launch_direct<false, false>(g, s);
     return launch_layout<false, false>(g, s);
 }
 }  // namespace mi

@@ -6,7 +6,7 @@
 namespace mi {
 hipError_t launch_gemm_nt(const GemmLaunch& g, hipStream_t s) {
     if (is_panel_cfg(g.cfg)) return launch_panel<false, true>(g, s);
-    if (direct_ok(g)) return launch_direct<false, true>(g, s);
+    if (direct_ok(g) || direct4_ok(g)) return launch_direct<false, true>(g, s);
     return launch_layout<false, true>(g, s);
 }
 }  // namespace mi

@@ -6,7 +6,7 @@
 namespace mi {
 hipError_t launch_gemm_tt(const GemmLaunch& g, hipStream_t s) {
     if (is_panel_cfg(g.cfg)) return launch_panel<true, true>(g, s);
-    if (direct_ok(g)) return launch_direct<true, true>(g, s);
+    if (direct_ok(g) || direct4_ok(g)) return launch_direct<true, true>(g, s);
     return launch_layout<true, true>(g, s);
 }
 }  // namespace mi

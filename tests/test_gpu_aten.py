@@ -177,10 +177,11 @@ def test_pointwise_conv_empty_and_checks(ck, dev):
 
 @pytest.mark.parametrize("M,K,N,ta,tb", [(1030, 517, 1027, False, False), (513, 1031, 770, True, False),
                                          (600, 401, 999, False, True), (515, 1029, 515, True, True)])
-def test_unaligned_rows_take_padded_copies(ck, orc, dev, M, K, N, ta, tb):
+def test_unaligned_rows_in_place(ck, orc, dev, M, K, N, ta, tb):
     """Large products whose rows are not 16-byte aligned (kernels/8_... style
-    irregular extents) run on zero-padded aligned copies; results and the
-    output shape are those of the plain product."""
+    irregular extents) run on the operands in place (4-byte direct staging,
+    partial last K slice); results and the output shape are those of the
+    plain product."""
     a_st = _u(orc, (K, M) if ta else (M, K), 70)
     b_st = _u(orc, (N, K) if tb else (K, N), 71)
     A = to_dev(a_st).t() if ta else to_dev(a_st)
@@ -188,7 +189,7 @@ def test_unaligned_rows_take_padded_copies(ck, orc, dev, M, K, N, ta, tb):
     C = ck.p08.matmul_cuda(A, B)
     assert tuple(C.shape) == (M, N) and C.is_contiguous()
     ref = orc.gemm(a_st.T if ta else a_st, b_st.T if tb else b_st)
-    assert_close(orc, to_host(C), ref, K, what=f"padded {M}x{K}x{N} {ta}{tb}")
+    assert_close(orc, to_host(C), ref, K, what=f"unaligned {M}x{K}x{N} {ta}{tb}")
 
 
 def test_torch_ops_dispatch_to_the_kernels(ck, orc, dev):

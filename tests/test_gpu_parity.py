@@ -170,6 +170,52 @@ def test_direct_staging(ck, orc, dev, cfg, op_a, op_b, M, N, K, batch, pad):
             assert np.isnan(got[:, :, N:]).all(), "a store landed in the ldc padding"
 
 
+@pytest.mark.parametrize("op_a,op_b", LAYOUTS)
+@pytest.mark.parametrize("M,N,K,batch,pad,split", [(301, 299, 517, 1, 0, 1), (130, 129, 37, 2, 1, 1),
+                                                   (257, 263, 1000, 1, 0, 1), (260, 264, 48, 1, 3, 1),
+                                                   (129, 250, 2001, 1, 0, 2), (5, 7, 19, 1, 0, 1)])
+def test_direct_staging_unaligned(ck, orc, dev, op_a, op_b, M, N, K, batch, pad, split):
+    """The 128-tile path with 4-byte direct loads: operands that are not
+    16-byte aligned or K not a multiple of 16.  The last slice of each K
+    range is partial: its loads are clamped into the operand and its
+    fragments past the range zeroed; with split-K only the last chunk has
+    one.  Edge rows / columns, padded leading dimensions, batched, row bias."""
+    a_st = orc.uniform((batch,) + ((K, M) if op_a else (M, K)), 171)
+    b_st = orc.uniform((batch,) + ((N, K) if op_b else (K, N)), 172)
+    bias = orc.uniform((M,), 173)
+    lda = (M if op_a else K) + pad
+    ldb = (K if op_b else N) + pad
+    ldc = N + pad
+    a_pad = np.zeros((batch, a_st.shape[1], lda), np.float32)
+    a_pad[:, :, :a_st.shape[2]] = a_st
+    b_pad = np.zeros((batch, b_st.shape[1], ldb), np.float32)
+    b_pad[:, :, :b_st.shape[2]] = b_st
+    # a NaN in the padding would poison any product that read past the K range
+    if pad:
+        a_pad[:, :, a_st.shape[2]:] = np.nan
+        b_pad[:, :, b_st.shape[2]:] = np.nan
+    A, B, Bi = to_dev(a_pad), to_dev(b_pad), to_dev(bias)
+    la = np.swapaxes(a_st, 1, 2) if op_a else a_st
+    lb = np.swapaxes(b_st, 1, 2) if op_b else b_st
+    ov = 2 | (split << 8)
+    for with_bias in ((False, True) if (op_a, op_b) == (0, 0) and split == 1 else (False,)):
+        C = torch.full((batch, M, ldc), float("nan"), device="cuda")
+        kw = dict(batch=batch, lda=lda, ldb=ldb, ldc=ldc, sa=a_pad[0].size, sb=b_pad[0].size,
+                  sc=M * ldc, override=ov)
+        args = gemm_args(ck, A, B, C, M, N, K, op_a, op_b, **kw)
+        if split > 1:
+            args = gemm_args(ck, A, B, C, M, N, K, op_a, op_b, ws=workspace(ck, args), **kw)
+        if with_bias:
+            args.bias_m = Bi.data_ptr()
+        ck.abi.check(run_gemm(ck, args))
+        ref = orc.gemm(la, lb) + (bias.astype(np.float64)[None, :, None] if with_bias else 0.0)
+        got = to_host(C)
+        assert_close(orc, got[:, :, :N], ref, K,
+                     what=f"direct4 {op_a}{op_b} {M}x{N}x{K}x{batch} pad={pad} split={split} bias={with_bias}")
+        if pad:
+            assert np.isnan(got[:, :, N:]).all(), "a store landed in the ldc padding"
+
+
 @pytest.mark.parametrize("cfg", [3, 2])
 @pytest.mark.parametrize("op_a,op_b", LAYOUTS)
 def test_direct_staging_split_k(ck, orc, dev, cfg, op_a, op_b):
