@@ -116,6 +116,22 @@ def test_plan_choices_for_baseline_configs(ck):
     assert p.split_k >= 64, "large-K must split K to fill 256 CUs"
 
 
+@pytest.mark.parametrize("M,N,K,ops,want", [
+    (8192, 8192, 8192, (0, 0), 3),    # 16-byte operands, K % 32 == 0: the 256 tile stages directly
+    (8191, 8191, 8191, (0, 0), 2),    # odd extents: only the 128 tile stages directly (4-byte loads)
+    (2048, 8190, 4096, (0, 0), 2),    # N % 4 != 0
+    (8192, 8192, 8176, (0, 0), 2),    # K % 32 != 0 (16-byte operands, K % 16 == 0)
+    (8205, 5921, 2949, (1, 1), 2),    # kernels/8_... style extents, transposed
+    (16384, 770, 2050, (0, 0), 2),
+])
+def test_plan_steers_unaligned_shapes_to_the_direct_128_tile(ck, M, N, K, ops, want):
+    """The 256 tile loads element-wise through registers unless its operands
+    are 16-byte rows with K a multiple of 32; the cost model discounts it then,
+    so such shapes take the 128 tile (4-byte direct staging)."""
+    rc, p = ck.abi.plan(M, N, K, op_a=ops[0], op_b=ops[1])
+    assert rc == 0 and p.plan_id == want, (M, N, K, p.plan_id)
+
+
 def _cover(ck, args, num_cus=256):
     rc, p = ck.abi.plan(args.M, args.N, args.K, num_cus=num_cus, batch=args.batch,
                         op_a=args.op_a, op_b=args.op_b, structure=args.structure,
