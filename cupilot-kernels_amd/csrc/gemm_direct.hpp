@@ -463,6 +463,42 @@ __global__ void __launch_bounds__(T::NT)
         }
     };
 
+    // Dense 16-byte staging: the last k-block's s = 2, 3 MFMAs are held back
+    // until after the slice barrier, where they cover the latency of the next
+    // slice's first fragment reads (issued right after the barrier).
+    constexpr bool SPLIT = MODE == kDense && VB == 16;
+    constexpr int NKB = T::BK / 8;
+    auto compute_split = [&](const float* As, const float* Bs, auto&& loads) __attribute__((always_inline)) {
+        loads();
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) {
+            const int set = kb & 1;
+            if (kb + 1 < NKB) frags(As, Bs, kb + 1);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int s = 0; s < (kb + 1 < NKB ? 4 : 2); ++s)
+#pragma unroll
+                for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < T::TN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[set][j][s], fa[set][i][s],
+                                                                         acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    auto tail = [&]() __attribute__((always_inline)) {
+        constexpr int set = (NKB - 1) & 1;
+#pragma unroll
+        for (int s = 2; s < 4; ++s)
+#pragma unroll
+            for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+                for (int j = 0; j < T::TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[set][j][s], fa[set][i][s],
+                                                                     acc[i][j], 0, 0, 0);
+    };
+
     int t = blockIdx.x;
     if (t >= p.num_tiles) return;
     TileWork cur = decode(t);
@@ -470,6 +506,7 @@ __global__ void __launch_bounds__(T::NT)
     set_offsets(cur);
     issue(cur, 0, sA0, sB0);
     __syncthreads();
+    if constexpr (SPLIT) frags(sA0, sB0, 0);
 
     // One slice from buffer CB; returns true after the workgroup's last tile.
     auto slice = [&](auto cb_tag) __attribute__((always_inline)) -> bool {
@@ -505,8 +542,19 @@ __global__ void __launch_bounds__(T::NT)
         }
         // (the scheduling barriers keep the loads ahead of the MFMAs: the
         // scheduler would sink them to the barrier, exposing their latency)
-        compute(curA, curB, [&]() __attribute__((always_inline)) { issue(nw, nit, nxtA, nxtB); });
-        __syncthreads();
+        if constexpr (SPLIT) {
+            compute_split(curA, curB, [&]() __attribute__((always_inline)) { issue(nw, nit, nxtA, nxtB); });
+            __syncthreads();
+            // the next slice's first k-block (fragment set 0; the held-back
+            // MFMAs use set (NKB - 1) & 1 = 1)
+            if (has_next) frags(nxtA, nxtB, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            tail();
+            __builtin_amdgcn_sched_barrier(0);
+        } else {
+            compute(curA, curB, [&]() __attribute__((always_inline)) { issue(nw, nit, nxtA, nxtB); });
+            __syncthreads();
+        }
         if (!last) {
             ++it;
             return false;
