@@ -437,38 +437,15 @@ __global__ void __launch_bounds__(T::NT)
             }
         }
     };
-    // The next k-block's fragment reads are issued ahead of this k-block's
-    // MFMAs (scheduling barriers keep that order), so only the first read of
-    // a slice waits on LDS latency.
-    auto compute = [&](const float* As, const float* Bs, auto&& loads) __attribute__((always_inline)) {
-        frags(As, Bs, 0);
-        // the next slice's loads go out while the first reads are in flight
-        __builtin_amdgcn_sched_barrier(0);
-        loads();
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int kb = 0; kb < T::BK / 8; ++kb) {
-            const int set = kb & 1;
-            if (kb + 1 < T::BK / 8) frags(As, Bs, kb + 1);
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int s = 0; s < 4; ++s)
-#pragma unroll
-                for (int i = 0; i < T::TM; ++i)
-#pragma unroll
-                    for (int j = 0; j < T::TN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[set][j][s], fa[set][i][s],
-                                                                         acc[i][j], 0, 0, 0);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    };
-
-    // Dense 16-byte staging: the last k-block's s = 2, 3 MFMAs are held back
-    // until after the slice barrier, where they cover the latency of the next
-    // slice's first fragment reads (issued right after the barrier).
-    constexpr bool SPLIT = MODE == kDense && VB == 16;
+    // Per slice: the next slice's loads, then for each k-block the next
+    // k-block's fragment reads ahead of this k-block's MFMAs (scheduling
+    // barriers keep that order).  The last k-block's s = 2, 3 MFMAs are held
+    // back until after the slice barrier (tail), where they cover the latency
+    // of the next slice's first fragment reads, issued right after the
+    // barrier; so the slice's first k-block fragments are already in
+    // registers (set 0) when compute starts.
     constexpr int NKB = T::BK / 8;
-    auto compute_split = [&](const float* As, const float* Bs, auto&& loads) __attribute__((always_inline)) {
+    auto compute = [&](const float* As, const float* Bs, auto&& loads) __attribute__((always_inline)) {
         loads();
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -499,6 +476,21 @@ __global__ void __launch_bounds__(T::NT)
                                                                      acc[i][j], 0, 0, 0);
     };
 
+    // per-slice fragment masks of slice i of tile w (read by frags)
+    auto slice_state = [&](const TileWork& w, int i) __attribute__((always_inline)) {
+        if constexpr (VB == 4) {
+            const int left = w.k_end - (w.k_begin + i * T::BK);
+            kv = left < T::BK ? left : T::BK;
+        }
+        if constexpr (MODE != kDense) {
+            const int k0 = w.k_begin + i * T::BK;
+            const int unit = k0 / T::BM;
+            mask_a = unit == w.tm;
+            mask_b = unit == w.tn;
+            kl0 = k0 - unit * T::BM;
+        }
+    };
+
     int t = blockIdx.x;
     if (t >= p.num_tiles) return;
     TileWork cur = decode(t);
@@ -506,7 +498,8 @@ __global__ void __launch_bounds__(T::NT)
     set_offsets(cur);
     issue(cur, 0, sA0, sB0);
     __syncthreads();
-    if constexpr (SPLIT) frags(sA0, sB0, 0);
+    slice_state(cur, 0);
+    frags(sA0, sB0, 0);
 
     // One slice from buffer CB; returns true after the workgroup's last tile.
     auto slice = [&](auto cb_tag) __attribute__((always_inline)) -> bool {
@@ -529,32 +522,19 @@ __global__ void __launch_bounds__(T::NT)
                 set_offsets(nw);
             }
         }
-        if constexpr (VB == 4) {
-            const int left = cur.k_end - (cur.k_begin + it * T::BK);
-            kv = left < T::BK ? left : T::BK;
-        }
-        if constexpr (MODE != kDense) {
-            const int k0 = cur.k_begin + it * T::BK;
-            const int unit = k0 / T::BM;
-            mask_a = unit == cur.tm;
-            mask_b = unit == cur.tn;
-            kl0 = k0 - unit * T::BM;
-        }
         // (the scheduling barriers keep the loads ahead of the MFMAs: the
         // scheduler would sink them to the barrier, exposing their latency)
-        if constexpr (SPLIT) {
-            compute_split(curA, curB, [&]() __attribute__((always_inline)) { issue(nw, nit, nxtA, nxtB); });
-            __syncthreads();
-            // the next slice's first k-block (fragment set 0; the held-back
-            // MFMAs use set (NKB - 1) & 1 = 1)
-            if (has_next) frags(nxtA, nxtB, 0);
-            __builtin_amdgcn_sched_barrier(0);
-            tail();
-            __builtin_amdgcn_sched_barrier(0);
-        } else {
-            compute(curA, curB, [&]() __attribute__((always_inline)) { issue(nw, nit, nxtA, nxtB); });
-            __syncthreads();
+        compute(curA, curB, [&]() __attribute__((always_inline)) { issue(nw, nit, nxtA, nxtB); });
+        __syncthreads();
+        // the next slice's first k-block (fragment set 0; the held-back MFMAs
+        // use set (NKB - 1) & 1 = 1), with that slice's masks
+        if (has_next) {
+            slice_state(nw, nit);
+            frags(nxtA, nxtB, 0);
         }
+        __builtin_amdgcn_sched_barrier(0);
+        tail();
+        __builtin_amdgcn_sched_barrier(0);
         if (!last) {
             ++it;
             return false;
