@@ -9,20 +9,20 @@
 //                                        fp32 accumulation and output
 //   2. P = softmax_rows(S)               fp32, written as two scaled fp16 terms
 //                                        2^14 P = H + 2^-11 L, side by side
-//   3. Vt = V^T                          E x Sp (zero padded to Sp keys)
-//   4. O = 2^-14 (H.V + 2^-11 L.V)       fp16 MFMA over [H | L] . [Vt | Vt]^T
-//                                        (the B operand wraps around Vt),
-//                                        fp32 accumulation, fp16 out
-// Step 4 is one contraction of depth 2*Sp whose accumulator is multiplied by
+//   3. O = 2^-14 (H.V + 2^-11 L.V)       fp16 MFMA over [H | L] . [V ; V]
+//                                        (the B operand's key index wraps),
+//                                        V read in place with LDS transpose
+//                                        loads, fp32 accumulation, fp16 out
+// Step 3 is one contraction of depth 2*Sp whose accumulator is multiplied by
 // 2^11 where the H half ends, so the attention weights keep ~22 bits
 // (fp32-like) although the MFMA takes fp16.  The 2^14 and 2^11 scalings keep
 // H and L in binary16's normal range: the MFMA treats subnormal fp16 inputs
 // as zero, which unscaled would drop most of L and every weight below 2^-14.
 // Products of fp16 values are exact in fp32, so every step except the final
 // rounding to fp16 carries fp32-level error, as the reference's fp32 math does.
-// Both contractions are "NT" (both operands contiguous along the reduction),
-// so every operand fetch is a 16-byte row chunk: one ds_read_b128 feeds one
-// MFMA operand (8 halves per lane).
+// QK is "NT" (both operands contiguous along the reduction): one ds_read_b128
+// feeds one MFMA operand (8 halves per lane); in PV the key-major V operand
+// takes two ds_read_b64_tr_b16 per MFMA operand.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -38,16 +38,11 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------------------
-// fp16 NT contraction: C[b] (M x N) = alpha * A[b] (M x K) . B[b]^T, with A
-// row-major (lda) and B stored N x K row-major (ldb); K % 64 == 0 and 16-byte
-// aligned rows (lda, ldb multiples of 8).  Output fp32 (OUT_HALF = false) or
-// fp16.  128 x 128 tiles, 4 waves of 64 x 64 (2 x 2 blocks of 32 x 32), K in
-// 64-deep slices through two LDS buffers (one barrier per slice, next slice's
-// loads in flight during the MFMAs, as in the fp32 engine).
+// fp16 contraction: C[b] (M x N) = alpha * A[b] (M x K) . B[b]^T, with A
+// row-major (lda) and B stored N x K row-major (ldb), or key-major K x N;
+// K % 64 == 0 and 16-byte aligned rows (lda, ldb multiples of 8).  Output
+// fp32 (OUT_HALF = false) or fp16.
 // ---------------------------------------------------------------------------
-constexpr int kHgBM = 128, kHgBN = 128, kHgBK = 64, kHgThreads = 256;
-constexpr int kHgLD = kHgBK + 8;  // halves per LDS row (+16 B: conflict-free b128 reads)
-
 struct HgemmParams {
     const _Float16* A;
     const _Float16* B;
@@ -58,120 +53,84 @@ struct HgemmParams {
     int k_switch;         // slice index at which the accumulator is multiplied by switch_mul
     float switch_mul;
     int b_kwrap;          // > 0: B holds K / 2 columns, read twice (k -> k - b_kwrap past it)
+    int b_rows;           // key-major B (hgemm_direct_kernel<*, true>): valid key rows
     int64_t lda, ldb, ldc;
     int64_t sa, sb, sc;   // batch strides (elements)
     float alpha;
 };
 
-template <bool OUT_HALF>
-__global__ void __launch_bounds__(kHgThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
-    hgemm_nt_kernel(const HgemmParams p) {
-    __shared__ __attribute__((aligned(16))) _Float16 sA[2][kHgBM * kHgLD];
-    __shared__ __attribute__((aligned(16))) _Float16 sB[2][kHgBN * kHgLD];
+// ---------------------------------------------------------------------------
+// Key-major fp16 operand (V of the PV contraction: keys x E, E contiguous),
+// staged directly and read with the gfx950 LDS transpose load.  A slice is
+// 64 key rows of 256 columns; wave instruction m (1 KiB) holds keys m (lanes
+// 0-31) and m + 32 (lanes 32-63) in an LDS slot of 1088 bytes, so key k sits
+// at slot k % 32, half k / 32.  ds_read_b64_tr_b16 works on groups of 16
+// lanes: if lane j of a group points at the 4 halves x[j][0..3], lane i
+// receives x[4 e + i / 4][i % 4] for e = 0..3 (measured on MI355X with an
+// in-bounds probe).  So when lane j points at key kb + j / 4, column n0 +
+// 4 (j % 4), lane i gets keys kb..kb+3 of column n0 + i -- a quarter of the
+// MFMA operand the key-contiguous layout gives with one 16-byte read; two
+// such reads make the 8 halves k = 16 ks + 8 (lane / 32) .. + 7 of column
+// c0 + lane % 32.  The four key rows of one read sit in consecutive slots,
+// 1088 = 4 * 256 + 64 bytes apart, i.e. in four different 64-byte windows
+// of the 256-byte bank space: conflict-free.
+// ---------------------------------------------------------------------------
+typedef short s4v __attribute__((ext_vector_type(4)));
 
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int half = lane >> 5, l32 = lane & 31;
-    const int tm = blockIdx.x / p.tiles_n, tn = blockIdx.x % p.tiles_n;
-    const int m0 = tm * kHgBM, n0 = tn * kHgBN;
-    const _Float16* A = p.A + (int64_t)blockIdx.z * p.sa;
-    const _Float16* B = p.B + (int64_t)blockIdx.z * p.sb;
+struct KeyLoader {
+    static constexpr int ROWS = 256, BKH = 64, NW = 8;
+    static constexpr int SLOT = 272;  // floats per instruction slot (1088 bytes)
+    static constexpr int INSTR = BKH / 2, PER_WAVE = INSTR / NW;
+    static constexpr int ELEMS = INSTR * SLOT;
 
-    // 16-byte chunks: a tile is 128 rows x 8 chunks; 4 chunks per thread
-    constexpr int NS = kHgBM * (kHgBK / 8) / kHgThreads;
-    h8 ra[NS], rb[NS];
-    auto load = [&](int k0) {
-        const int kb0 = (p.b_kwrap > 0 && k0 >= p.b_kwrap) ? k0 - p.b_kwrap : k0;
-#pragma unroll
-        for (int s = 0; s < NS; ++s) {
-            const int c = tid + s * kHgThreads;
-            const int row = c >> 3, kc = (c & 7) * 8;
-            const int am = m0 + row, bn = n0 + row;
-            ra[s] = am < p.M ? *reinterpret_cast<const h8*>(A + (int64_t)am * p.lda + k0 + kc) : h8{};
-            rb[s] = bn < p.N ? *reinterpret_cast<const h8*>(B + (int64_t)bn * p.ldb + kb0 + kc) : h8{};
-        }
-    };
-    auto store = [&](int buf) {
-#pragma unroll
-        for (int s = 0; s < NS; ++s) {
-            const int c = tid + s * kHgThreads;
-            const int row = c >> 3, kc = (c & 7) * 8;
-            *reinterpret_cast<h8*>(&sA[buf][row * kHgLD + kc]) = ra[s];
-            *reinterpret_cast<h8*>(&sB[buf][row * kHgLD + kc]) = rb[s];
-        }
-    };
-
-    f16v acc[2][2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-
-    const int nk = p.K / kHgBK;
-    load(0);
-    store(0);
-    __syncthreads();
-    for (int it = 0; it < nk; ++it) {
-        const int cb = it & 1;
-        if (it == p.k_switch) {
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j) acc[i][j] *= p.switch_mul;
-        }
-        // next slice's loads (the last iteration re-reads its own slice, unused)
-        load((it + 1 < nk ? it + 1 : it) * kHgBK);
-#pragma unroll
-        for (int ks = 0; ks < kHgBK / 16; ++ks) {
-            h8 fa[2], fb[2];
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-                fa[i] = *reinterpret_cast<const h8*>(
-                    &sA[cb][(wm * 64 + i * 32 + l32) * kHgLD + ks * 16 + half * 8]);
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-                fb[j] = *reinterpret_cast<const h8*>(
-                    &sB[cb][(wn * 64 + j * 32 + l32) * kHgLD + ks * 16 + half * 8]);
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    // B fragment as the row operand: the block holds C^T, so
-                    // lane l owns row l % 32 and 4 consecutive columns per
-                    // register group
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[j], fa[i], acc[i][j], 0, 0, 0);
-        }
-        store(cb ^ 1);
-        __syncthreads();
+    __device__ __forceinline__ static constexpr int byte_of(int key, int col) {
+        return (key % 32) * (SLOT * 4) + (key / 32) * 512 + col * 2;
     }
-
+    // Byte offsets (from the slice origin) of this wave's loads for the tile
+    // at column n0; keys at or past krows (a slice that runs past the last
+    // key) read key krows - 1 instead, whose weights are zero.
+    __device__ __forceinline__ static void offsets(int64_t ld, int n0, int n_ext, int wave, int lane,
+                                                   uint32_t (&vo)[PER_WAVE], int krows = BKH) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < PER_WAVE; ++i) {
+            const int ins = wave * PER_WAVE + i;
+            int key = ins + 32 * (lane >> 5);
+            key = key < krows ? key : krows - 1;
+            // (n_ext - n0 is a positive multiple of 8: E % 64 == 0)
+            const int c0 = (lane & 31) * 8;
+            const int c = n0 + c0 + 7 < n_ext ? c0 : n_ext - 8 - n0;
+            vo[i] = ((uint32_t)key * (uint32_t)ld + (uint32_t)c) * 2u;
+        }
+    }
+    __device__ __forceinline__ static void load(const _Float16* base, int64_t ld, int n0, int k0,
+                                                const uint32_t (&vo)[PER_WAVE], float* lds,
+                                                int wave) {
+        const __amdgpu_buffer_rsrc_t rsrc =
+            raw_rsrc(reinterpret_cast<const float*>(base + (int64_t)k0 * ld + n0));
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int i = 0; i < PER_WAVE; ++i) {
+            const int ins = wave * PER_WAVE + i;
+            load_lds16(rsrc, vo[i], lds + ins * SLOT);
+        }
+    }
+    // MFMA operand of k-step ks for the 32 columns at c0
+    __device__ __forceinline__ static h8 frag(const float* lds, int c0, int ks, int lane) {
+        const int g = lane >> 4, i = lane & 15;
+        const char* base = reinterpret_cast<const char*>(lds);
+        h8 out;
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int row = m0 + wm * 64 + i * 32 + l32;
-                const int col = n0 + wn * 64 + j * 32 + g * 8 + half * 4;
-                if (row >= p.M || col + 3 >= p.n_store) continue;
-                const int64_t off = (int64_t)blockIdx.z * p.sc + (int64_t)row * p.ldc + col;
-                if (OUT_HALF) {
-                    h4 v;
+        for (int hh = 0; hh < 2; ++hh) {
+            const int key = 16 * ks + 8 * (g >> 1) + 4 * hh + (i >> 2);
+            const int col = c0 + 16 * (g & 1) + 4 * (i & 3);
+            const s4v v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) s4v*)(base + byte_of(key, col)));
+            const h4 hv = __builtin_bit_cast(h4, v);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) v[e] = (_Float16)(acc[i][j][4 * g + e] * p.alpha);
-                    *reinterpret_cast<h4*>(static_cast<_Float16*>(p.C) + off) = v;
-                } else {
-                    f4 v;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * g + e] * p.alpha;
-                    *reinterpret_cast<f4*>(static_cast<float*>(p.C) + off) = v;
-                }
-            }
-}
+            for (int e = 0; e < 4; ++e) out[4 * hh + e] = hv[e];
+        }
+        return out;
+    }
+};
 
 // ---------------------------------------------------------------------------
 // The same NT contraction on 256 x 256 tiles with direct LDS staging, for
@@ -184,18 +143,21 @@ __global__ void __launch_bounds__(kHgThreads) __attribute__((amdgpu_waves_per_eu
 // over (batch, tile), XCD-remapped so the tiles of one batch entry share an
 // L2; per slice: first fragment reads, the next slice's loads, then the
 // MFMAs with the following k-step's reads issued ahead (as the fp32 kernel).
-// With 64 x 64 wave tiles (hgemm_nt_kernel) every MFMA needed 2 KiB of
-// fragment reads and the LDS read rate set the pace (~20 % of the MFMA peak).
+// (An earlier 128 x 128 tile with 64 x 64 wave tiles needed 2 KiB of fragment
+// reads per MFMA; the LDS read rate set its pace, ~20 % of the MFMA peak.)
 // ---------------------------------------------------------------------------
-template <bool OUT_HALF>
+template <bool OUT_HALF, bool B_KEYS>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
     hgemm_direct_kernel(const HgemmParams p, int batch) {
     constexpr int BM = 256, BN = 256, WM = 128, WN = 64, TM = 4, TN = 2, BKH = 64;
     using L = DirectLoader<true, 8>;
+    // B_KEYS: B is key-major (K x N, N contiguous; ldb per key row), staged by
+    // KeyLoader and read with transpose loads
+    using LB = std::conditional_t<B_KEYS, KeyLoader, L>;
     __shared__ __attribute__((aligned(16))) float sA0[L::ELEMS];
     __shared__ __attribute__((aligned(16))) float sA1[L::ELEMS];
-    __shared__ __attribute__((aligned(16))) float sB0[L::ELEMS];
-    __shared__ __attribute__((aligned(16))) float sB1[L::ELEMS];
+    __shared__ __attribute__((aligned(16))) float sB0[LB::ELEMS];
+    __shared__ __attribute__((aligned(16))) float sB1[LB::ELEMS];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -220,18 +182,32 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
         return w;
     };
 
-    uint32_t voA[L::PER_WAVE], voB[L::PER_WAVE];
+    uint32_t voA[L::PER_WAVE], voB[LB::PER_WAVE];
     auto set_offsets = [&](const Work& w) __attribute__((always_inline)) {
         L::offsets(lda, w.tm * BM, p.M, wave, lane, voA);
-        L::offsets(ldb, w.tn * BN, p.N, wave, lane, voB);
+        if constexpr (B_KEYS)
+            KeyLoader::offsets(p.ldb, w.tn * BN, p.N, wave, lane, voB);
+        else
+            L::offsets(ldb, w.tn * BN, p.N, wave, lane, voB);
     };
     auto issue = [&](const Work& w, int it, float* dA, float* dB) __attribute__((always_inline)) {
         const int k0 = it * BKH;
         const int kb = (p.b_kwrap > 0 && k0 >= p.b_kwrap) ? k0 - p.b_kwrap : k0;
         const float* A = reinterpret_cast<const float*>(p.A + (int64_t)w.b * p.sa);
-        const float* B = reinterpret_cast<const float*>(p.B + (int64_t)w.b * p.sb);
         L::load(A, lda, w.tm * BM, k0 / 2, voA, dA, wave);
-        L::load(B, ldb, w.tn * BN, kb / 2, voB, dB, wave);
+        if constexpr (B_KEYS) {
+            const _Float16* B = p.B + (int64_t)w.b * p.sb;
+            if (kb + BKH > p.b_rows) {  // slice runs past the last key: clamped offsets
+                uint32_t tB[KeyLoader::PER_WAVE];
+                KeyLoader::offsets(p.ldb, w.tn * BN, p.N, wave, lane, tB, p.b_rows - kb);
+                KeyLoader::load(B, p.ldb, w.tn * BN, kb, tB, dB, wave);
+            } else {
+                KeyLoader::load(B, p.ldb, w.tn * BN, kb, voB, dB, wave);
+            }
+        } else {
+            const float* B = reinterpret_cast<const float*>(p.B + (int64_t)w.b * p.sb);
+            L::load(B, ldb, w.tn * BN, kb / 2, voB, dB, wave);
+        }
     };
 
     f16v acc[TM][TN];
@@ -251,9 +227,13 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
         }
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-            float t[4];
-            L::frag(Bs, wn * WN + j * 32, ks, lane, t);
-            fb[ks & 1][j] = __builtin_bit_cast(h8, f4{t[0], t[1], t[2], t[3]});
+            if constexpr (B_KEYS) {
+                fb[ks & 1][j] = KeyLoader::frag(Bs, wn * WN + j * 32, ks, lane);
+            } else {
+                float t[4];
+                L::frag(Bs, wn * WN + j * 32, ks, lane, t);
+                fb[ks & 1][j] = __builtin_bit_cast(h8, f4{t[0], t[1], t[2], t[3]});
+            }
         }
     };
     auto compute = [&](const float* As, const float* Bs, auto&& loads) __attribute__((always_inline)) {
@@ -432,69 +412,22 @@ __global__ void __launch_bounds__(256)
 }
 
 // ---------------------------------------------------------------------------
-// Vt[b] (E x sp) = V[b]^T, zero for keys >= n.  64 x 64 tiles through LDS:
-// 16-byte loads (8 halves along E) and 16-byte stores (8 halves along the
-// keys), so both sides move whole 128-byte lines per 8 lanes; E % 8 == 0 and
-// sp % 64 == 0 (16-byte aligned rows).  (Element-wise loads and stores ran at
-// 2.5 TB/s.)
-// ---------------------------------------------------------------------------
-__global__ void __launch_bounds__(256)
-    transpose_kernel(const _Float16* __restrict__ V, _Float16* __restrict__ Vt, int n, int E, int sp) {
-    constexpr int LDH = 64 + 8;  // halves per LDS row (16-byte aligned rows)
-    __shared__ __attribute__((aligned(16))) _Float16 tile[64 * LDH];
-    const int b = blockIdx.z;
-    const int k0 = blockIdx.y * 64, e0 = blockIdx.x * 64;
-    const _Float16* v = V + (int64_t)b * n * E;
-    _Float16* vt = Vt + (int64_t)b * E * (int64_t)sp;
-    const int t = threadIdx.x;
-    const int c = (t & 7) * 8;  // 8-half chunk within a 64-wide row
-#pragma unroll
-    for (int pass = 0; pass < 2; ++pass) {
-        const int r = pass * 32 + (t >> 3);  // key row of the tile
-        const int k = k0 + r, e = e0 + c;
-        h8 x = h8{};
-        if (k < n && e < E) x = *reinterpret_cast<const h8*>(v + (int64_t)k * E + e);
-        *reinterpret_cast<h8*>(&tile[r * LDH + c]) = x;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int pass = 0; pass < 2; ++pass) {
-        const int r = pass * 32 + (t >> 3);  // E row of the output tile
-        const int e = e0 + r, k = k0 + c;
-        if (e >= E) continue;
-        h8 y;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) y[j] = tile[(c + j) * LDH + r];
-        *reinterpret_cast<h8*>(vt + (int64_t)e * sp + k) = y;
-    }
-}
-
-// ---------------------------------------------------------------------------
 // Host side: one chunk of heads at a time through the caller's workspace.
 // ---------------------------------------------------------------------------
 namespace {
 
 int round_up(int x, int m) { return (x + m - 1) / m * m; }
-// keys per half of a P' row (and per Vt row): whole 64-deep slices, so the switch from
+// keys per half of a P' row: whole 64-deep slices, so the switch from
 // the H half to the L half falls between slices
 constexpr int kSdpaKeyPad = 64;
 
-template <bool OUT_HALF>
-hipError_t launch_hgemm(const HgemmParams& p, int batch, hipStream_t s) {
-    const int tiles_m = (p.M + kHgBM - 1) / kHgBM;
-    dim3 grid((unsigned)(tiles_m * p.tiles_n), 1u, (unsigned)batch);
-    hipLaunchKernelGGL((hgemm_nt_kernel<OUT_HALF>), grid, dim3(kHgThreads), 0, s, p);
-    return hipGetLastError();
-}
-
 // The 256-tile direct kernel, persistent over (batch, tile): one workgroup per
-// CU (its LDS holds two 64-deep slices of both 256-row operands).  p.tiles_n
-// counts 256-wide tiles.  Byte offsets within a slice (256 rows) fit 32 bits
-// for lda, ldb < 2^22 halves.
-template <bool OUT_HALF>
+// CU (its LDS holds two 64-deep slices of both operands).  Byte offsets within
+// a slice fit 32 bits for lda, ldb < 2^22 halves; the C entry point's limits
+// (seq <= 32768, embed <= 65536) keep every leading dimension far below.
+template <bool OUT_HALF, bool B_KEYS = false>
 hipError_t launch_hgemm_direct(HgemmParams p, int batch, hipStream_t s) {
-    if (p.lda >= (INT64_C(1) << 22) || p.ldb >= (INT64_C(1) << 22))
-        return launch_hgemm<OUT_HALF>(p, batch, s);
+    if (p.lda >= (INT64_C(1) << 22) || p.ldb >= (INT64_C(1) << 22)) return hipErrorInvalidValue;
     p.tiles_n = (p.N + 255) / 256;
     const int total = ((p.M + 255) / 256) * p.tiles_n * batch;
     int dev = 0, cus = 256;
@@ -504,7 +437,8 @@ hipError_t launch_hgemm_direct(HgemmParams p, int batch, hipStream_t s) {
             cus = v;
     }
     const int grid = total < cus ? total : cus;
-    hipLaunchKernelGGL((hgemm_direct_kernel<OUT_HALF>), dim3((unsigned)grid), dim3(512), 0, s, p, batch);
+    hipLaunchKernelGGL((hgemm_direct_kernel<OUT_HALF, B_KEYS>), dim3((unsigned)grid), dim3(512), 0, s,
+                       p, batch);
     return hipGetLastError();
 }
 
@@ -516,9 +450,9 @@ size_t sdpa_workspace_bytes(int64_t heads, int seq, int embed) {
     if (heads <= 0 || seq <= 0 || embed <= 0) return 0;
     const int64_t hc = sdpa_chunk_heads(heads);
     const int64_t sp = round_up(seq, kSdpaKeyPad);
-    return (size_t)hc * (seq * sp * 4       // S (fp32)
-                         + seq * 2 * sp * 2  // P' (fp16)
-                         + embed * sp * 2);     // Vt (fp16)
+    (void)embed;  // V is read in place
+    return (size_t)hc * (seq * sp * 4         // S (fp32)
+                         + seq * 2 * sp * 2);  // P' (fp16)
 }
 
 hipError_t launch_sdpa(const _Float16* Q, const _Float16* K, const _Float16* V, _Float16* O,
@@ -527,7 +461,6 @@ hipError_t launch_sdpa(const _Float16* Q, const _Float16* K, const _Float16* V, 
     const int64_t hc_max = sdpa_chunk_heads(heads);
     float* S = static_cast<float*>(ws);
     _Float16* P = reinterpret_cast<_Float16*>(S + hc_max * seq * sp);
-    _Float16* Vt = P + hc_max * seq * 2 * sp;
     const int64_t head_elems = (int64_t)seq * embed;
     const float scale = 1.0f / sqrtf((float)embed);
     for (int64_t h0 = 0; h0 < heads; h0 += hc_max) {
@@ -541,7 +474,6 @@ hipError_t launch_sdpa(const _Float16* Q, const _Float16* K, const _Float16* V, 
         q.N = seq;
         q.K = embed;
         q.n_store = sp;
-        q.tiles_n = (seq + kHgBN - 1) / kHgBN;
         q.lda = embed;
         q.ldb = embed;
         q.ldc = sp;
@@ -567,32 +499,29 @@ hipError_t launch_sdpa(const _Float16* Q, const _Float16* K, const _Float16* V, 
             hipLaunchKernelGGL((softmax_split_kernel<0>), sm_grid, dim3(256), 0, s, S, P, rows, seq, sp,
                                (int64_t)sp);
         if ((e = hipGetLastError()) != hipSuccess) return e;
-        // 3. Vt = V^T
-        hipLaunchKernelGGL(transpose_kernel,
-                           dim3((unsigned)((embed + 63) / 64), (unsigned)((sp + 63) / 64), (unsigned)hc),
-                           dim3(256), 0, s, V + h0 * head_elems, Vt, seq, embed, sp);
-        if ((e = hipGetLastError()) != hipSuccess) return e;
-        // 4. O = P' . [Vt | Vt]^T (seq x E, fp16): B wraps around Vt's sp columns
+        // 3. O = P' . [V ; V] (seq x E, fp16): the B operand's key index wraps
+        // at sp (keys sp .. 2 sp - 1 read keys 0 .. sp - 1 again); keys past
+        // seq carry zero weights
         HgemmParams o{};
         o.A = P;
-        o.B = Vt;
         o.C = O + h0 * head_elems;
         o.M = seq;
         o.N = embed;
         o.K = 2 * sp;
         o.n_store = embed;
-        o.tiles_n = (embed + kHgBN - 1) / kHgBN;
         o.lda = 2 * sp;
-        o.ldb = sp;
         o.b_kwrap = sp;
         o.ldc = embed;
         o.sa = (int64_t)seq * 2 * sp;
-        o.sb = (int64_t)embed * sp;
         o.sc = head_elems;
-        o.k_switch = sp / kHgBK;       // first slice of the L half
+        o.B = V + h0 * head_elems;  // key-major V itself
+        o.ldb = embed;
+        o.sb = head_elems;
+        o.b_rows = seq;
+        o.k_switch = sp / 64;          // first 64-deep slice of the L half
         o.switch_mul = 2048.0f;        // 2^11: H.V -> 2^11 H.V, then + L.V
         o.alpha = 1.0f / (16384.0f * 2048.0f);  // 2^-25
-        if ((e = launch_hgemm_direct<true>(o, hc, s)) != hipSuccess) return e;
+        if ((e = launch_hgemm_direct<true, true>(o, hc, s)) != hipSuccess) return e;
     }
     return hipSuccess;
 }

@@ -257,6 +257,13 @@ def test_workspace_queries(ck):
     assert L.mi_matmul_large_k_workspace_bytes(8192, 8192, 8192) == 0
     assert L.mi_gemv_workspace_bytes(32768, 65536) == 0
     assert L.mi_gemv_workspace_bytes(64, 1 << 20) > 0
+    # attention: scores (fp32, seq x sp) and split weights (fp16, seq x 2 sp)
+    # per head of a 128-head chunk; V is read in place (no transposed copy)
+    L.mi_sdpa_workspace_bytes.restype = ctypes.c_size_t
+    L.mi_sdpa_workspace_bytes.argtypes = [ctypes.c_int64] * 3
+    assert L.mi_sdpa_workspace_bytes(1024, 512, 1024) == 128 * (512 * 512 * 4 + 512 * 1024 * 2)
+    assert L.mi_sdpa_workspace_bytes(2, 300, 1024) == 2 * (300 * 320 * 4 + 300 * 640 * 2)
+    assert L.mi_sdpa_workspace_bytes(1, 3, 1 << 17) == 0  # embed beyond the entry point's limit
 
 
 def test_header_is_plain_c(tmp_path):
