@@ -115,6 +115,52 @@ def test_runs_on_current_stream(ck, orc, dev):
     assert_close(orc, C.cpu().numpy(), orc.gemm(a, b), 256, what="side stream")
 
 
+def test_operators_replay_in_a_hip_graph(ck, dev):
+    """The operators only launch kernels on the current stream (no host
+    synchronisation, no memset; workspaces from the caching allocator), so a
+    sequence of them can be captured in a HIP graph: captured once, replayed
+    three times with eager work and synchronisations between the replays,
+    every replay bitwise equal to the eager results.  Covers the direct-staged
+    256 and 128 tiles, split-K with its reduction (workspace), the chunked
+    triangular list with its finishing pass, GEMV, diag, pointwise conv and
+    attention."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(97)
+    u = lambda *shape: torch.rand(*shape, device="cuda", generator=g) * 2 - 1
+    a4, b4 = u(4096, 4096), u(4096, 4096)
+    a2, b2 = u(2048, 768), u(768, 1536)
+    lka, lkb = u(256, 1 << 17), u(1 << 17, 256)
+    ta, tb = u(6144, 6144).tril_(), u(6144, 6144).tril_()
+    ga, gx = u(4096, 8192), u(8192, 1)
+    dv, dm = u(2048), u(2048, 2048)
+    cx, cw, cb = u(2, 64, 64, 64), u(128, 64), u(128)
+    q, k, v = (u(1, 2, 128, 1024).half() for _ in range(3))
+
+    def ops():
+        return [ck.p01.matmul_cuda(a4, b4), ck.p02.matmul_cuda(a2, b2), ck.p06.matmul_cuda(lka, lkb),
+                ck.p15.lower_tri_mul_cuda(ta, tb), ck.p04.gemv_cuda(ga, gx), ck.p12.diag_mult_cuda(dv, dm),
+                ck.p87.pointwise_conv_cuda(cx, cw, cb), ck.p97.fused_attention_cuda(q, k, v)]
+
+    eager = [x.clone() for x in ops()]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm-up on the capture stream
+        ops()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = ops()
+    for rep in range(3):
+        for o in outs:  # eager work between replays
+            o.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for i, (o, e) in enumerate(zip(outs, eager)):
+            assert torch.equal(o, e), f"replay {rep}: operator {i} differs from its eager result"
+
+
 def test_matrix_scalar_operator(ck, orc, dev):
     """PID 5 matrix_scalar_mult_cuda(A, float s) (kernels/5_...:47-71): the
     output is empty_like(A) (any shape), bitwise the fp32 product, an empty A
