@@ -161,6 +161,47 @@ def test_operators_replay_in_a_hip_graph(ck, dev):
             assert torch.equal(o, e), f"replay {rep}: operator {i} differs from its eager result"
 
 
+def test_operators_reentrant_across_threads_and_streams(ck, dev):
+    """No global mutable state: four host threads, each on its own stream,
+    run different operators concurrently (split-K workspaces from the caching
+    allocator, the triangular list's finishing pass, attention's workspace);
+    every result bitwise equals the same call made alone."""
+    import threading
+
+    g = torch.Generator(device="cuda")
+    g.manual_seed(7)
+    u = lambda *shape: torch.rand(*shape, device="cuda", generator=g) * 2 - 1
+    jobs = [
+        (lambda x, y: ck.p06.matmul_cuda(x, y), (u(256, 1 << 16), u(1 << 16, 256))),
+        (lambda x, y: ck.p14.upper_tri_matmul_cuda(x, y), (u(6144, 6144).triu_(), u(6144, 6144).triu_())),
+        (lambda x, y: ck.p16.matmul_transposed_cuda(x, y), (u(1024, 2048), u(1024, 3000))),
+        (lambda x, y: ck.p97.fused_attention_cuda(x, y, y), (u(1, 4, 256, 1024).half(), u(1, 4, 256, 1024).half())),
+    ]
+    alone = [fn(*args).clone() for fn, args in jobs]
+    torch.cuda.synchronize()
+    results, errors = [None] * len(jobs), []
+
+    def run(i):
+        try:
+            s = torch.cuda.Stream()
+            with torch.cuda.stream(s):
+                outs = [jobs[i][0](*jobs[i][1]) for _ in range(3)]
+            s.synchronize()
+            results[i] = outs
+        except Exception as e:  # surfaced below
+            errors.append(e)
+
+    threads = [threading.Thread(target=run, args=(i,)) for i in range(len(jobs))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+    for i, outs in enumerate(results):
+        for o in outs:
+            assert torch.equal(o, alone[i]), f"job {i} differs when run concurrently"
+
+
 def test_matrix_scalar_operator(ck, orc, dev):
     """PID 5 matrix_scalar_mult_cuda(A, float s) (kernels/5_...:47-71): the
     output is empty_like(A) (any shape), bitwise the fp32 product, an empty A
