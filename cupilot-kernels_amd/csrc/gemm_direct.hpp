@@ -314,8 +314,11 @@ __global__ void __launch_bounds__(T::NT)
     const int lane = tid & 63;
     // wave-uniform, made scalar so LDS destinations (M0) need no readfirstlane
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // Triangular modes: the two waves on a SIMD (waves w and w + 4) own
+    // different column blocks, so when the diagonal masks leave whole waves
+    // without work (idle) both halves of the machine shed work together.
     const int wm = wave / T::WAVES_N;
-    const int wn = wave % T::WAVES_N;
+    const int wn = MODE == kDense ? wave % T::WAVES_N : (wave + 2 * wm) % T::WAVES_N;
     const int batch = blockIdx.z;
 
     const float* __restrict__ A = p.A + (int64_t)batch * p.sa;
@@ -381,6 +384,9 @@ __global__ void __launch_bounds__(T::NT)
     // tile (mask_a) / B's column tile (mask_b) entries past the diagonal read
     // as zero.  kl0 = the slice's first k within that unit.
     int mask_a = 0, mask_b = 0, kl0 = 0;
+    // the wave's fragments of the slice are all zero (masked): its MFMAs are
+    // skipped (they would add exact zeros)
+    int idle = 0;
     // VB == 4: k of the slice being computed that are in range (< BK only in
     // a partial last slice, whose fragments past it are zeroed)
     int kv = T::BK;
@@ -453,19 +459,22 @@ __global__ void __launch_bounds__(T::NT)
             const int set = kb & 1;
             if (kb + 1 < NKB) frags(As, Bs, kb + 1);
             __builtin_amdgcn_sched_barrier(0);
+            if (MODE == kDense || !idle) {
 #pragma unroll
-            for (int s = 0; s < (kb + 1 < NKB ? 4 : 2); ++s)
+                for (int s = 0; s < (kb + 1 < NKB ? 4 : 2); ++s)
 #pragma unroll
-                for (int i = 0; i < T::TM; ++i)
+                    for (int i = 0; i < T::TM; ++i)
 #pragma unroll
-                    for (int j = 0; j < T::TN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[set][j][s], fa[set][i][s],
-                                                                         acc[i][j], 0, 0, 0);
+                        for (int j = 0; j < T::TN; ++j)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                                fb[set][j][s], fa[set][i][s], acc[i][j], 0, 0, 0);
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
     };
-    auto tail = [&]() __attribute__((always_inline)) {
+    auto tail = [&](int skip) __attribute__((always_inline)) {
         constexpr int set = (NKB - 1) & 1;
+        if (MODE != kDense && skip) return;
 #pragma unroll
         for (int s = 2; s < 4; ++s)
 #pragma unroll
@@ -488,6 +497,13 @@ __global__ void __launch_bounds__(T::NT)
             mask_a = unit == w.tm;
             mask_b = unit == w.tn;
             kl0 = k0 - unit * T::BM;
+            // slice k range [kl0, kl0 + BK) against the wave's rows (A masked:
+            // lower keeps k <= m, upper k >= m) and columns (B masked: lower
+            // keeps n <= k, upper n >= k)
+            const int r0 = wm * T::WM, c0 = wn * T::WN;
+            const bool a_idle = MODE == kLower ? kl0 > r0 + T::WM - 1 : kl0 + T::BK - 1 < r0;
+            const bool b_idle = MODE == kLower ? c0 > kl0 + T::BK - 1 : c0 + T::WN - 1 < kl0;
+            idle = (mask_a && a_idle) || (mask_b && b_idle);
         }
     };
 
@@ -528,12 +544,13 @@ __global__ void __launch_bounds__(T::NT)
         __syncthreads();
         // the next slice's first k-block (fragment set 0; the held-back MFMAs
         // use set (NKB - 1) & 1 = 1), with that slice's masks
+        const int tail_idle = idle;  // (slice_state below moves on to the next slice)
         if (has_next) {
             slice_state(nw, nit);
             frags(nxtA, nxtB, 0);
         }
         __builtin_amdgcn_sched_barrier(0);
-        tail();
+        tail(tail_idle);
         __builtin_amdgcn_sched_barrier(0);
         if (!last) {
             ++it;
