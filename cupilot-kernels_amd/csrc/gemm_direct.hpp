@@ -507,7 +507,26 @@ __global__ void __launch_bounds__(T::NT)
         }
     };
 
+    // Triangular work list, dynamic order: persistent workgroups take the
+    // next item of the longest-first list from a counter as they finish one,
+    // so XCDs that run faster take more items.  The counter is the first word
+    // of zero-triangle tile (0, 1) (lower; (1, 0) upper): with cap >= 2 it is
+    // never a mirror tile, the launcher zeroes the word first and the
+    // finishing pass zeroes the tile.  One thread claims the next item at the
+    // current item's second-to-last slice (as late as the one-slice load
+    // lookahead allows: a claim made earlier would reserve the item for a
+    // workgroup still busy), through LDS: written after every wave has read
+    // the previous value (items have >= 8 slices), read at the last slice.
+    const bool dyn = MODE != kDense && p.tri_cap >= 2;
+    __shared__ int s_item;
+    int* const ctr = MODE == kLower ? reinterpret_cast<int*>(p.C + 256)
+                                    : reinterpret_cast<int*>(p.C + 256 * p.ldc);
     int t = blockIdx.x;
+    if (dyn) {
+        if (tid == 0) s_item = atomicAdd(ctr, 1);
+        __syncthreads();
+        t = s_item;
+    }
     if (t >= p.num_tiles) return;
     TileWork cur = decode(t);
     int it = 0;
@@ -529,8 +548,11 @@ __global__ void __launch_bounds__(T::NT)
         bool has_next = true;
         TileWork nw = cur;
         int nit = it + 1;
+        if constexpr (MODE != kDense) {
+            if (dyn && it == cur.nk - 2 && tid == 0) s_item = atomicAdd(ctr, 1);
+        }
         if (last) {
-            nt = t + gridDim.x;
+            nt = dyn ? s_item : t + gridDim.x;
             has_next = nt < p.num_tiles;
             nit = has_next ? 0 : it;
             if (has_next) {
@@ -623,7 +645,21 @@ inline bool direct4_ok(const GemmLaunch& g) {
 // zero triangle.
 inline hipError_t launch_direct_tri(const GemmLaunch& g, hipStream_t s) {
     const GemmParams p = make_params(g);
-    dim3 grid((unsigned)g.num_tiles, 1, 1);
+    unsigned n_wg = (unsigned)g.num_tiles;
+    if (g.tri_cap >= 2) {  // dynamic order (see the kernel): one persistent workgroup per CU
+        float* const ctr = g.structure == kLower ? g.C + 256 : g.C + 256 * g.ldc;
+        hipError_t e = launch_zero_word(ctr, s);
+        if (e != hipSuccess) return e;
+        int dev = 0, cus = 256;
+        if (hipGetDevice(&dev) == hipSuccess) {
+            int v = 0;
+            if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+                v > 0)
+                cus = v;
+        }
+        if ((unsigned)cus < n_wg) n_wg = (unsigned)cus;
+    }
+    dim3 grid(n_wg, 1, 1);
     if (g.structure == kLower)
         hipLaunchKernelGGL((gemm_f32_direct_kernel<Tile256, false, false, false, kLower>), grid,
                            dim3(Tile256::NT), 0, s, p);

@@ -98,6 +98,8 @@ hipError_t launch_splitk_reduce(const float* ws, float* C, int M, int N, int bat
 // (it holds the second chunk's partial sum), then write it with +0.0.  C is
 // nt*256 square.
 hipError_t launch_tri_finish(float* C, int64_t ldc, int nt, int cap, bool lower, hipStream_t s);
+// Writes integer 0 to one 4-byte word (a kernel, so it can be graph-captured).
+hipError_t launch_zero_word(void* w, hipStream_t s);
 // C[b][r][c] = bias ? bias[r] : 0 (a contraction with K = 0)
 hipError_t launch_fill_zero_2d(float* C, int64_t rows, int64_t cols, int64_t ld, int64_t batch,
                                int64_t batch_stride, hipStream_t s, const float* bias = nullptr);

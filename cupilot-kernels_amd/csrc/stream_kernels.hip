@@ -409,6 +409,15 @@ hipError_t launch_tri_finish(float* C, int64_t ldc, int nt, int cap, bool lower,
     return hipGetLastError();
 }
 
+__global__ void zero_word_kernel(int* w) {
+    if (threadIdx.x == 0) *w = 0;
+}
+
+hipError_t launch_zero_word(void* w, hipStream_t s) {
+    hipLaunchKernelGGL(zero_word_kernel, dim3(1), dim3(64), 0, s, static_cast<int*>(w));
+    return hipGetLastError();
+}
+
 __global__ void fill_uniform_kernel(float* __restrict__ out, int64_t n, uint64_t base) {
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * blockDim.x)
