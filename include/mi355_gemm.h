@@ -115,7 +115,9 @@ MI_API int mi_gemm_plan(const mi_gemm_args* args, int32_t num_cus, mi_plan* out)
  * structural-zero tile (triangular products), 2 for a K chunk of a long
  * triangular tile whose partial sum is parked in the mirror tile
  * (tile_n, tile_m) of the zero triangle and added in by a finishing pass
- * (the chunked work list of triangular products with N % 256 == 0), a
+ * (the chunked work list of triangular products with N % 256 == 0; its items
+ * run longest first, claimed in list order by persistent workgroups as they
+ * free up, so which workgroup runs an item is decided at run time), a
  * negative mi_status on error. */
 MI_API int mi_gemm_tile_of(const mi_gemm_args* args, int32_t num_cus, int64_t item, int32_t split,
                            int32_t* tile_m, int32_t* tile_n, int64_t* k_begin, int64_t* k_end);
