@@ -66,8 +66,8 @@ def read_traffic():
 # the kernel symbols rocprofv3 reports
 PLAN_KERNELS = {
     1: "gemm_f32_kernel<Tile<64,64,32,32,16,8,2>>",
-    2: "gemm_f32_kernel<Tile<128,128,64,64,16,3,2>>",
-    3: "gemm_f32_kernel<Tile<256,256,128,64,32,2,2>>",
+    2: "gemm_f32_direct_kernel<Tile<128,128,64,64,16,3,2>> (gemm_f32_kernel where direct staging does not apply)",
+    3: "gemm_f32_direct_kernel<Tile<256,256,128,64,32,2,2>> (gemm_f32_kernel where direct staging does not apply)",
     4: "gemm_f32_kernel<Tile<128,128,64,64,32,3,1>>",
     5: "gemm_f32_kernel<Tile<128,128,64,64,64,2,1>>",
     6: "gemm_f32_panel_kernel<PanelTile<256,128,32>>",
@@ -77,14 +77,15 @@ PLAN_KERNELS = {
 
 
 def nn_kernel_name(ck) -> str:
-    """Kernel the scheduler picks for the NN 8192^3 launch (N/N launches of the
-    256 tile with K % 32 == 0 and K >= 256 per split take the direct-staging
-    kernel)."""
+    """Kernel the scheduler picks for the NN 8192^3 launch, spelled as rocprof
+    prints it (N/N launches of the 256 tile with 16-byte operands, K % 32 == 0
+    and K >= 256 per split take the direct-staging kernel; template arguments
+    <tile, A transposed, B transposed, row bias, structure, bytes per load>)."""
     rc, plan = ck.abi.plan(N, N, N)
     ck.abi.check(rc, "mi_gemm_plan")
     if plan.plan_id == 3 and N % 32 == 0 and plan.k_chunk >= 256:
-        return ("mi::gemm_f32_direct_kernel<Tile<256,256,128,64,32,2,2>, false, false, false> "
-                f"(split_k {plan.split_k})")
+        return ("mi::gemm_f32_direct_kernel<mi::Tile<256, 256, 128, 64, 32, 2, 2>, false, false, false, 0, 16>"
+                f" (split_k {plan.split_k})")
     return f"mi::{PLAN_KERNELS.get(plan.plan_id, plan.plan_id)}, NN, vec4, dense (split_k {plan.split_k})"
 
 
