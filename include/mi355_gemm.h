@@ -55,7 +55,10 @@ typedef enum { MI_OP_N = 0, MI_OP_T = 1 } mi_op;
 typedef enum {
     MI_DENSE = 0,
     MI_LOWER = 1,   /* C = tril(tril(A) . tril(B)), exact zeros above the diagonal */
-    MI_UPPER = 2,   /* C = triu(triu(A) . triu(B)), exact zeros below the diagonal */
+    MI_UPPER = 2,   /* C = triu(triu(A) . triu(B)), exact zeros below the diagonal
+                       (both: while the call runs, C's zero triangle may hold
+                       partial sums and a work counter; it is +0.0 when the
+                       stream reaches the next operation) */
     MI_SYMMETRIC = 3 /* C = A . B with A = A^T and B = B^T (square, per batch): the
                         operands are read in the fastest orientation (A as stored,
                         B as its transpose), which the symmetry makes identical */
