@@ -149,7 +149,14 @@ __global__ void __launch_bounds__(T::NT) gemm_f32_panel_kernel(const GemmParams 
                     for (int r = 0; r < 4; ++r) {
                         const int rr = r * 8 + (lane >> 3);
                         const f4 v = *reinterpret_cast<const f4*>(buf + rr * SCLD + (lane & 7) * 4);
-                        *reinterpret_cast<f4*>(C + (int64_t)(r0 + rr) * p.ldc + c0) = v;
+                        f4* const dst = reinterpret_cast<f4*>(C + (int64_t)(r0 + rr) * p.ldc + c0);
+                        // non-temporal for the 128-row panel: measured 190 vs 208 us on
+                        // the 1x1 convolution shape; equal or slower (up to 4 %) for
+                        // the 256-row panels
+                        if constexpr (T::BM == 128)
+                            __builtin_nontemporal_store(v, dst);
+                        else
+                            *dst = v;
                     }
                 } else {
                     const int i = q / (T::TN * 4), j = (q / 4) % T::TN, g = q % 4;
