@@ -49,6 +49,9 @@ constexpr double kWriteBytesPerNs = 5500.0;        // sustained write-only bandw
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Smallest K per split the cost model may choose.
+constexpr int64_t kMinSplitK = 256;
+
 // Workgroups of each config held on one CU at once; the kernels are built to
 // exactly this occupancy (amdgpu_waves_per_eu): 64-tile 8, 128-tile 3, 256-tile 1.
 int resident_wgs(int cfg) {
@@ -179,9 +182,9 @@ int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
             const int64_t tiles = cdiv(a.M, ci.bm) * cdiv(a.N, ci.bn) * batch;
             for (int s = 1; s <= 1024; s *= 2) {
                 if (s > 1) {
-                    // split only to fill the machine, with >= 1024 K per split
+                    // split only to fill the machine, with >= kMinSplitK of K per split
                     if (tiles * (s / 2) >= (int64_t)num_cus) break;
-                    if (a.K / s < 1024) break;
+                    if (a.K / s < kMinSplitK) break;
                     const size_t need = (size_t)s * batch * a.M * a.N * sizeof(float);
                     if (a.workspace_bytes < need) break;
                 }
