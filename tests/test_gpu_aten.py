@@ -115,6 +115,22 @@ def test_runs_on_current_stream(ck, orc, dev):
     assert_close(orc, C.cpu().numpy(), orc.gemm(a, b), 256, what="side stream")
 
 
+@pytest.mark.parametrize("M,K,N", [(300, 5000, 300), (512, 2048, 512), (1024, 1024, 1024), (256, 4096, 256),
+                                   (768, 3072, 768)])
+def test_small_deep_products_split_by_default(ck, orc, dev, M, K, N):
+    """Problems whose tiles leave most CUs idle are split along K by default
+    (down to 256 of K per split) with the workspace from the caching
+    allocator; the fixed-order reduction keeps repeated calls bitwise equal."""
+    rc, p = ck.abi.plan(M, N, K, workspace_bytes=1 << 40)
+    assert rc == 0 and p.split_k > 1, (M, N, K, p.split_k)
+    a, b = _u(orc, (M, K), 91), _u(orc, (K, N), 92)
+    A, B = to_dev(a), to_dev(b)
+    C1 = ck.p02.matmul_cuda(A, B)
+    C2 = ck.p02.matmul_cuda(A, B)
+    assert torch.equal(C1, C2)
+    assert_close(orc, to_host(C1), orc.gemm(a, b), K, what=f"split by default {M}x{K}x{N}")
+
+
 def test_operators_replay_in_a_hip_graph(ck, dev):
     """The operators only launch kernels on the current stream (no host
     synchronisation, no memset; workspaces from the caching allocator), so a
