@@ -13,6 +13,8 @@
 //                                        (the B operand's key index wraps),
 //                                        V read in place with LDS transpose
 //                                        loads, fp32 accumulation, fp16 out
+// For seq <= 512 steps 1 and 2 are one kernel (qk_softmax_kernel): a tile of
+// 128 queries holds whole score rows, so S never leaves the accumulators.
 // Step 3 is one contraction of depth 2*Sp whose accumulator is multiplied by
 // 2^11 where the H half ends, so the attention weights keep ~22 bits
 // (fp32-like) although the MFMA takes fp16.  The 2^14 and 2^11 scalings keep
@@ -352,6 +354,234 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
 }
 
 // ---------------------------------------------------------------------------
+// QK with the row softmax fused in, for sp <= 512: one tile is 128 queries x
+// all 512 (padded) keys, so every score row is complete in the accumulators.
+// 8 waves (2 x 4) of 64 x 128 (2 x 4 blocks); Q and K staged directly in
+// 64-half slices (two stages of 16 + 64 KiB).  The epilogue computes the row
+// max and the sum of exp over keys < n (lane, lane ^ 32, then the four key
+// waves through LDS -- the stage just consumed is free by then) and writes the
+// P' row [H | L] (2 * sp halves) with 2^14 p = H + 2^-11 L, as
+// softmax_split_kernel does, without the fp32 score round trip.
+// ---------------------------------------------------------------------------
+struct QkSoftmaxParams {
+    const _Float16* Q;
+    const _Float16* K;
+    _Float16* P;
+    int n, sp, E;
+    int64_t head_elems;  // Q / K elements per head (n * E)
+    float scale;         // 1 / sqrt(E)
+};
+
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+    qk_softmax_kernel(const QkSoftmaxParams p, int heads) {
+    constexpr int BM = 128, BN = 512, WM = 64, WN = 128, TM = 2, TN = 4, BKH = 64;
+    using LA = DirectLoader<true, 8, 128, 32>;
+    using LB = DirectLoader<true, 8, 512, 32>;
+    __shared__ __attribute__((aligned(16))) float sA0[LA::ELEMS];
+    __shared__ __attribute__((aligned(16))) float sA1[LA::ELEMS];
+    __shared__ __attribute__((aligned(16))) float sB0[LB::ELEMS];
+    __shared__ __attribute__((aligned(16))) float sB1[LB::ELEMS];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 2, wn = wave & 3;
+    const int per_b = (p.n + BM - 1) / BM;
+    const int total = per_b * heads;
+    const int nk = p.E / BKH;
+    const int64_t ld = p.E / 2;  // floats
+
+    struct Work {
+        int b, tm;
+    };
+    auto decode = [&](int t) {
+        const int id = xcd_remap(t, total);
+        return Work{id / per_b, id % per_b};
+    };
+    uint32_t voA[LA::PER_WAVE], voB[LB::PER_WAVE];
+    auto set_offsets = [&](const Work& w) __attribute__((always_inline)) {
+        LA::offsets(ld, w.tm * BM, p.n, wave, lane, voA);
+        LB::offsets(ld, 0, p.n, wave, lane, voB);  // key rows past n read row n - 1
+    };
+    auto issue = [&](const Work& w, int it, float* dA, float* dB) __attribute__((always_inline)) {
+        const int k0 = it * BKH;
+        const float* A = reinterpret_cast<const float*>(p.Q + (int64_t)w.b * p.head_elems);
+        const float* B = reinterpret_cast<const float*>(p.K + (int64_t)w.b * p.head_elems);
+        LA::load(A, ld, w.tm * BM, k0 / 2, voA, dA, wave);
+        LB::load(B, ld, 0, k0 / 2, voB, dB, wave);
+    };
+
+    f16v acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+    h8 fa[2][TM], fb[2][TN];
+    auto frags = [&](const float* As, const float* Bs, int ks) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            float t[4];
+            LA::frag(As, wm * WM + i * 32, ks, lane, t);
+            fa[ks & 1][i] = __builtin_bit_cast(h8, f4{t[0], t[1], t[2], t[3]});
+        }
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            float t[4];
+            LB::frag(Bs, wn * WN + j * 32, ks, lane, t);
+            fb[ks & 1][j] = __builtin_bit_cast(h8, f4{t[0], t[1], t[2], t[3]});
+        }
+    };
+    auto compute = [&](const float* As, const float* Bs, auto&& loads) __attribute__((always_inline)) {
+        frags(As, Bs, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        loads();
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int ks = 0; ks < BKH / 16; ++ks) {
+            if (ks + 1 < BKH / 16) frags(As, Bs, ks + 1);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    // B fragment as the row operand: the block holds C^T
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[ks & 1][j], fa[ks & 1][i],
+                                                                       acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    // Epilogue.  Lane l holds, for query row 32 i + l % 32 of the wave, the
+    // keys wn * 128 + 32 j + 8 g + 4 (l / 32) + e (register 4 g + e of block
+    // j).  red: [2 wm][4 wn][64 rows] floats for the max, then for the sum.
+    auto softmax_store = [&](const Work& w, float* red) __attribute__((always_inline)) {
+        const int h = lane >> 5, l32 = lane & 31;
+        float sm[TM];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            float m = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = wn * WN + 32 * j + 8 * (r >> 2) + 4 * h + (r & 3);
+                    const float v = key < p.n ? acc[i][j][r] * p.scale : -INFINITY;
+                    acc[i][j][r] = v;
+                    m = fmaxf(m, v);
+                }
+            m = fmaxf(m, __shfl_xor(m, 32, 64));
+            if (h == 0) red[(wm * 4 + wn) * 64 + 32 * i + l32] = m;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            float m = -INFINITY;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) m = fmaxf(m, red[(wm * 4 + q) * 64 + 32 * i + l32]);
+            float ssum = 0.f;
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const float e = expf(acc[i][j][r] - m);  // exp(-inf) = 0 past n
+                    acc[i][j][r] = e;
+                    ssum += e;
+                }
+            ssum += __shfl_xor(ssum, 32, 64);
+            if (h == 0) red[512 + (wm * 4 + wn) * 64 + 32 * i + l32] = ssum;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            float ssum = 0.f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) ssum += red[512 + (wm * 4 + q) * 64 + 32 * i + l32];
+            sm[i] = 16384.0f / ssum;
+        }
+        __syncthreads();  // red is overwritten by the next slice's loads
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            const int row = w.tm * BM + wm * WM + 32 * i + l32;
+            if (row >= p.n) continue;
+            _Float16* out = p.P + ((int64_t)w.b * p.n + row) * (2 * (int64_t)p.sp);
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int key = wn * WN + 32 * j + 8 * g + 4 * h;
+                    if (key >= p.sp) continue;
+                    h4 hi, lo;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        float pv = acc[i][j][4 * g + e] * sm[i];  // 2^14 p <= 2^14
+                        // pv opaque: otherwise the compiler rounds the exact
+                        // product to fp16 once (v_fma_mixlo) for L's H but
+                        // stores H rounded via fp32, which differ at fp16 ties
+                        asm volatile("" : "+v"(pv));
+                        hi[e] = (_Float16)pv;
+                        lo[e] = (_Float16)((pv - (float)hi[e]) * 2048.0f);
+                    }
+                    *reinterpret_cast<h4*>(out + key) = hi;
+                    *reinterpret_cast<h4*>(out + p.sp + key) = lo;
+                }
+        }
+    };
+
+    int t = blockIdx.x;
+    if (t >= total) return;
+    Work cur = decode(t);
+    int it = 0;
+    set_offsets(cur);
+    issue(cur, 0, sA0, sB0);
+    __syncthreads();
+    auto slice = [&](auto cb_tag) __attribute__((always_inline)) -> bool {
+        constexpr int CB = decltype(cb_tag)::value;
+        const float* const curA = CB == 0 ? sA0 : sA1;
+        const float* const curB = CB == 0 ? sB0 : sB1;
+        float* const nxtA = CB == 0 ? sA1 : sA0;
+        float* const nxtB = CB == 0 ? sB1 : sB0;
+        float* const red = CB == 0 ? sB0 : sB1;  // free once this slice is consumed
+        const bool last = it + 1 >= nk;
+        int nt = t;
+        bool has_next = true;
+        Work nw = cur;
+        int nit = it + 1;
+        if (last) {
+            nt = t + gridDim.x;
+            has_next = nt < total;
+            nit = has_next ? 0 : it;
+            if (has_next) {
+                nw = decode(nt);
+                set_offsets(nw);
+            }
+        }
+        compute(curA, curB, [&]() __attribute__((always_inline)) { issue(nw, nit, nxtA, nxtB); });
+        __syncthreads();
+        if (!last) {
+            ++it;
+            return false;
+        }
+        softmax_store(cur, red);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+        if (!has_next) return true;
+        t = nt;
+        cur = nw;
+        it = 0;
+        return false;
+    };
+    for (;;) {
+        if (slice(std::integral_constant<int, 0>{})) break;
+        if (slice(std::integral_constant<int, 1>{})) break;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Row softmax with the two-term fp16 split.  One wave per row of S (n values,
 // row stride lds floats); writes the P' row (2 * sp halves) [H | 0 pad | L | 0 pad]
 // with 2^14 p = H + 2^-11 L.  Rows up to 64 * VPL values stay in registers
@@ -367,7 +597,10 @@ __global__ void __launch_bounds__(256)
     const float* s = S + row * lds;
     _Float16* out = P + row * (2 * (int64_t)sp);
     auto emit = [&](int c, float e, float scale) {
-        const float pv = e * scale;  // 2^14 p <= 2^14
+        float pv = e * scale;  // 2^14 p <= 2^14
+        // H and the H inside L must be one rounding of one fp32 value: opaque
+        // pv keeps the compiler from folding the product into either of them
+        asm volatile("" : "+v"(pv));
         const _Float16 hi = (_Float16)pv;
         out[c] = hi;
         out[sp + c] = (_Float16)((pv - (float)hi) * 2048.0f);
@@ -442,63 +675,95 @@ hipError_t launch_hgemm_direct(HgemmParams p, int batch, hipStream_t s) {
     return hipGetLastError();
 }
 
+hipError_t launch_qk_softmax(const QkSoftmaxParams& p, int heads, hipStream_t s) {
+    const int total = ((p.n + 127) / 128) * heads;
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) == hipSuccess) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+            cus = v;
+    }
+    const int grid = total < cus ? total : cus;
+    hipLaunchKernelGGL(qk_softmax_kernel, dim3((unsigned)grid), dim3(512), 0, s, p, heads);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 int64_t sdpa_chunk_heads(int64_t heads) { return heads < kSdpaChunkHeads ? heads : kSdpaChunkHeads; }
+
+// seq <= 512: the QK kernel writes P' straight from its accumulators, no S
+bool sdpa_fused(int sp, int embed) { return sp <= 512 && embed < (1 << 22); }
 
 size_t sdpa_workspace_bytes(int64_t heads, int seq, int embed) {
     if (heads <= 0 || seq <= 0 || embed <= 0) return 0;
     const int64_t hc = sdpa_chunk_heads(heads);
     const int64_t sp = round_up(seq, kSdpaKeyPad);
-    (void)embed;  // V is read in place
-    return (size_t)hc * (seq * sp * 4         // S (fp32)
-                         + seq * 2 * sp * 2);  // P' (fp16)
+    // V is read in place
+    const int64_t s_bytes = sdpa_fused((int)sp, embed) ? 0 : seq * sp * 4;  // S (fp32)
+    return (size_t)hc * (s_bytes + seq * 2 * sp * 2);                      // + P' (fp16)
 }
 
 hipError_t launch_sdpa(const _Float16* Q, const _Float16* K, const _Float16* V, _Float16* O,
                        int64_t heads, int seq, int embed, void* ws, hipStream_t s) {
     const int sp = round_up(seq, kSdpaKeyPad);
     const int64_t hc_max = sdpa_chunk_heads(heads);
+    const bool fused = sdpa_fused(sp, embed);
     float* S = static_cast<float*>(ws);
-    _Float16* P = reinterpret_cast<_Float16*>(S + hc_max * seq * sp);
+    _Float16* P = fused ? static_cast<_Float16*>(ws) : reinterpret_cast<_Float16*>(S + hc_max * seq * sp);
     const int64_t head_elems = (int64_t)seq * embed;
     const float scale = 1.0f / sqrtf((float)embed);
     for (int64_t h0 = 0; h0 < heads; h0 += hc_max) {
         const int hc = (int)(heads - h0 < hc_max ? heads - h0 : hc_max);
-        // 1. S = scale * Q K^T (seq x seq, row stride sp)
-        HgemmParams q{};
-        q.A = Q + h0 * head_elems;
-        q.B = K + h0 * head_elems;
-        q.C = S;
-        q.M = seq;
-        q.N = seq;
-        q.K = embed;
-        q.n_store = sp;
-        q.lda = embed;
-        q.ldb = embed;
-        q.ldc = sp;
-        q.sa = head_elems;
-        q.sb = head_elems;
-        q.sc = (int64_t)seq * sp;
-        q.alpha = scale;
-        q.k_switch = -1;
-        q.switch_mul = 1.0f;
-        q.b_kwrap = 0;
-        hipError_t e = launch_hgemm_direct<false>(q, hc, s);
-        if (e != hipSuccess) return e;
-        // 2. P' = split softmax rows
-        const int64_t rows = (int64_t)hc * seq;
-        const dim3 sm_grid((unsigned)((rows + 3) / 4));
-        if (sp <= 512)
-            hipLaunchKernelGGL((softmax_split_kernel<8>), sm_grid, dim3(256), 0, s, S, P, rows, seq, sp,
-                               (int64_t)sp);
-        else if (sp <= 1024)
-            hipLaunchKernelGGL((softmax_split_kernel<16>), sm_grid, dim3(256), 0, s, S, P, rows, seq, sp,
-                               (int64_t)sp);
-        else
-            hipLaunchKernelGGL((softmax_split_kernel<0>), sm_grid, dim3(256), 0, s, S, P, rows, seq, sp,
-                               (int64_t)sp);
-        if ((e = hipGetLastError()) != hipSuccess) return e;
+        hipError_t e;
+        if (fused) {
+            // 1+2. P' straight from the scores (one tile holds whole rows)
+            QkSoftmaxParams f{};
+            f.Q = Q + h0 * head_elems;
+            f.K = K + h0 * head_elems;
+            f.P = P;
+            f.n = seq;
+            f.sp = sp;
+            f.E = embed;
+            f.head_elems = head_elems;
+            f.scale = scale;
+            if ((e = launch_qk_softmax(f, hc, s)) != hipSuccess) return e;
+        } else {
+            // 1. S = scale * Q K^T (seq x seq, row stride sp)
+            HgemmParams q{};
+            q.A = Q + h0 * head_elems;
+            q.B = K + h0 * head_elems;
+            q.C = S;
+            q.M = seq;
+            q.N = seq;
+            q.K = embed;
+            q.n_store = sp;
+            q.lda = embed;
+            q.ldb = embed;
+            q.ldc = sp;
+            q.sa = head_elems;
+            q.sb = head_elems;
+            q.sc = (int64_t)seq * sp;
+            q.alpha = scale;
+            q.k_switch = -1;
+            q.switch_mul = 1.0f;
+            q.b_kwrap = 0;
+            e = launch_hgemm_direct<false>(q, hc, s);
+            if (e != hipSuccess) return e;
+            // 2. P' = split softmax rows
+            const int64_t rows = (int64_t)hc * seq;
+            const dim3 sm_grid((unsigned)((rows + 3) / 4));
+            if (sp <= 512)
+                hipLaunchKernelGGL((softmax_split_kernel<8>), sm_grid, dim3(256), 0, s, S, P, rows, seq, sp,
+                                   (int64_t)sp);
+            else if (sp <= 1024)
+                hipLaunchKernelGGL((softmax_split_kernel<16>), sm_grid, dim3(256), 0, s, S, P, rows, seq, sp,
+                                   (int64_t)sp);
+            else
+                hipLaunchKernelGGL((softmax_split_kernel<0>), sm_grid, dim3(256), 0, s, S, P, rows, seq, sp,
+                                   (int64_t)sp);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+        }
         // 3. O = P' . [V ; V] (seq x E, fp16): the B operand's key index wraps
         // at sp (keys sp .. 2 sp - 1 read keys 0 .. sp - 1 again); keys past
         // seq carry zero weights

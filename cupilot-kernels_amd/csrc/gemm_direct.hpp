@@ -78,14 +78,17 @@ __device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, uint32_t vo
 // so the fragment reads are too.
 template <bool KCONTIG, int NW, int ROWS = 256, int BK = 32, int VB = 16>
 struct DirectLoader {
-    static_assert((ROWS == 256 && BK == 32) || (ROWS == 128 && BK == 16), "slice shapes built");
+    static_assert((ROWS == 256 && BK == 32) || (ROWS == 128 && BK == 16) ||
+                      ((ROWS == 128 || ROWS == 512) && BK == 32 && KCONTIG && VB == 16),
+                  "slice shapes built");
     static_assert(VB == 16 || VB == 4, "dwordx4 or dword loads");
     // K-contiguous: a row is CH 16-byte chunks, swizzled; RPW rows share one
     // 256-byte window of the 64 banks.
     static constexpr int CH = BK / 4, RPW = 64 / BK;
     // MN-contiguous: LDS rows of ROWS floats, KPI rows (1 KiB) followed by 4
-    // floats of padding.
-    static constexpr int KPI = 256 / ROWS, IPITCH = KPI * ROWS + 4;
+    // floats of padding (MN-contiguous slices have at most 256 rows; the
+    // 512-row K-contiguous shape never uses KPI).
+    static constexpr int KPI = ROWS <= 256 ? 256 / ROWS : 1, IPITCH = KPI * ROWS + 4;
     // floats one wave instruction writes (64 lanes x VB bytes)
     static constexpr int IFL = 16 * VB;
     static constexpr int INSTR = KCONTIG ? ROWS * BK / IFL : BK * (VB == 16 ? 1 : ROWS / 64) / (VB == 16 ? KPI : 1);

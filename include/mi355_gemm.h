@@ -207,8 +207,8 @@ MI_API int mi_pointwise_conv_f32(const float* input, const float* weight, const 
  * with Q, K, V, O contiguous fp16 (IEEE binary16) arrays of batch_heads x seq
  * x embed, fp32 arithmetic inside, one rounding to fp16 at the end.  embed
  * must be a multiple of 64 and the four pointers 16-byte aligned.  The
- * workspace (device memory, mi_sdpa_workspace_bytes) holds the scores and
- * attention weights of up to 128 heads at a time. */
+ * workspace (device memory, mi_sdpa_workspace_bytes) holds the attention
+ * weights of up to 128 heads at a time, and for seq > 512 their fp32 scores. */
 MI_API size_t mi_sdpa_workspace_bytes(int64_t batch_heads, int64_t seq, int64_t embed);
 MI_API int mi_sdpa_f16(const void* Q, const void* K, const void* V, void* O, int64_t batch_heads,
                 int64_t seq, int64_t embed, void* workspace, size_t workspace_bytes,

@@ -261,8 +261,11 @@ def test_workspace_queries(ck):
     # per head of a 128-head chunk; V is read in place (no transposed copy)
     L.mi_sdpa_workspace_bytes.restype = ctypes.c_size_t
     L.mi_sdpa_workspace_bytes.argtypes = [ctypes.c_int64] * 3
-    assert L.mi_sdpa_workspace_bytes(1024, 512, 1024) == 128 * (512 * 512 * 4 + 512 * 1024 * 2)
-    assert L.mi_sdpa_workspace_bytes(2, 300, 1024) == 2 * (300 * 320 * 4 + 300 * 640 * 2)
+    # seq <= 512: the attention weights P' only (2 x 64-padded keys, fp16 per row,
+    # 128 heads at a time); longer rows also hold the fp32 scores S
+    assert L.mi_sdpa_workspace_bytes(1024, 512, 1024) == 128 * 512 * 1024 * 2
+    assert L.mi_sdpa_workspace_bytes(2, 300, 1024) == 2 * 300 * 640 * 2
+    assert L.mi_sdpa_workspace_bytes(3, 600, 128) == 3 * (600 * 640 * 4 + 600 * 1280 * 2)
     assert L.mi_sdpa_workspace_bytes(1, 3, 1 << 17) == 0  # embed beyond the entry point's limit
 
 

@@ -34,6 +34,8 @@ def _check(orc, got, q, k, v, what):
     return worst
 
 
+# (1, 130, 64, 1024) holds weights whose fp32 2^14 p falls exactly on an fp16
+# rounding tie: an H / L split whose two roundings of H differ fails it.
 @pytest.mark.parametrize("shape", [(1, 1, 512, 1024), (2, 3, 100, 1024), (1, 2, 1, 1024),
                                    (1, 1, 33, 1024), (1, 96, 512, 1024), (1, 130, 64, 1024),
                                    (2, 5, 300, 1024)])
