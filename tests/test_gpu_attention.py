@@ -82,6 +82,26 @@ def test_sdpa_abi_general_sizes_and_errors(ck, orc, dev):
     assert L.mi_sdpa_f16(None, None, None, None, 0, seq, embed, None, 0, cur_stream()) == 0
 
 
+@pytest.mark.parametrize("heads,seq,embed", [(3, 512, 64), (2, 513, 64), (2, 700, 128), (1, 1100, 64)])
+def test_sdpa_abi_kernel_paths(ck, orc, dev, heads, seq, embed):
+    """Both schedules of the C entry point: seq <= 512 fuses the softmax into
+    the QK kernel (here with a one-slice embed); longer rows keep fp32 scores
+    in the workspace and split them with the register (seq <= 1024) or the
+    three-pass row softmax, at and past the boundary."""
+    L = ck.abi.lib()
+    q, k, v = _inputs(orc, (heads, seq, embed), 70)
+    Q, K, V = to_dev(q), to_dev(k), to_dev(v)
+    O = torch.empty_like(Q)
+    nbytes = L.mi_sdpa_workspace_bytes(heads, seq, embed)
+    sp = -(-seq // 64) * 64
+    assert nbytes == heads * (seq * 2 * sp * 2 + (0 if sp <= 512 else seq * sp * 4))
+    ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    vp = lambda t: ctypes.c_void_p(t.data_ptr())
+    ck.abi.check(L.mi_sdpa_f16(vp(Q), vp(K), vp(V), vp(O), heads, seq, embed, vp(ws), nbytes,
+                               cur_stream()))
+    _check(orc, to_host(O), q, k, v, f"abi {heads}x{seq}x{embed}")
+
+
 def test_fused_attention_empty(ck, dev):
     e = torch.empty((0, 2, 16, 1024), dtype=torch.float16, device="cuda")
     assert tuple(ck.p97.fused_attention_cuda(e, e, e).shape) == (0, 2, 16, 1024)
