@@ -188,8 +188,11 @@ int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
             const int64_t tiles = cdiv(a.M, ci.bm) * cdiv(a.N, ci.bn) * batch;
             for (int s = 1; s <= 1024; s *= 2) {
                 if (s > 1) {
-                    // split only to fill the machine, with >= kMinSplitK of K per split
-                    if (tiles * (s / 2) >= (int64_t)num_cus) break;
+                    // split only to fill the machine, with >= kMinSplitK of K per
+                    // split; up to twice the CUs in items, since the per-CU
+                    // quantisation above decides (1536^3, 144 tiles: split 2
+                    // leaves some CUs two items, split 4 measured 86 vs 104 us)
+                    if (tiles * (s / 2) >= 2 * (int64_t)num_cus) break;
                     if (a.K / s < kMinSplitK) break;
                     const size_t need = (size_t)s * batch * a.M * a.N * sizeof(float);
                     if (a.workspace_bytes < need) break;

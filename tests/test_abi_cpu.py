@@ -146,6 +146,18 @@ def test_plan_shallow_k_takes_the_128_tile(ck, M, N, K, want):
     assert rc == 0 and p.plan_id == want, (M, N, K, p.plan_id)
 
 
+@pytest.mark.parametrize("M,N,K,split", [
+    (1536, 1536, 1536, 4),  # 144 tiles: split 2 leaves some CUs two items (88 vs 104 us)
+    (2304, 2304, 2304, 2),  # 227 vs 290 us on the 256 tile
+    (2048, 2048, 2048, 1),  # 256 tiles fill the machine: no split
+])
+def test_plan_splits_by_per_cu_load(ck, M, N, K, split):
+    """Splits are priced by the most loaded CU's share of K, up to twice the
+    CUs in items, not stopped at the first split that covers every CU."""
+    rc, p = ck.abi.plan(M, N, K, workspace_bytes=1 << 30)
+    assert rc == 0 and p.plan_id == 2 and p.split_k == split, (M, N, K, p.plan_id, p.split_k)
+
+
 def _cover(ck, args, num_cus=256):
     rc, p = ck.abi.plan(args.M, args.N, args.K, num_cus=num_cus, batch=args.batch,
                         op_a=args.op_a, op_b=args.op_b, structure=args.structure,
