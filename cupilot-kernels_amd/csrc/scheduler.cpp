@@ -179,12 +179,13 @@ int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
             const CfgInfo ci = cfg_info(m.id);
             if ((m.id == kCfg128K32 || m.id == kCfg128K64) && a.K > ci.bk) continue;
             double eff = m.id == kCfg256 && !full16 ? 0.75 * m.efficiency : m.efficiency;
-            // One 256 tile per CU: at K <= 256 its 256 KiB store is barely
+            // One 256 tile per CU: at K <= 512 its 256 KiB store is barely
             // covered by the next tile's short MFMA run.  Measured, 128 vs 256
             // tile at K = 256: 65536x512 135 vs 139 us, 16384x2048 136 vs 149,
-            // 8192^2 270 vs 275; equal at 131072x512 and 65536x768; within
-            // 1 % at K = 384 and 512.
-            if (m.id == kCfg256 && a.K <= 256) eff *= 0.93;
+            // 8192^2 270 vs 275, equal at 131072x512 and 65536x768; K = 512:
+            // 4096^2 129 vs 137, 4096x8192 256 vs 261, 65536x512 250 vs 253;
+            // within 1.6 % at K = 1024 - 2048, the 256 tile 1-1.5 % ahead at 4096.
+            if (m.id == kCfg256 && a.K <= 512) eff *= 0.92;
             const int64_t tiles = cdiv(a.M, ci.bm) * cdiv(a.N, ci.bn) * batch;
             for (int s = 1; s <= 1024; s *= 2) {
                 if (s > 1) {

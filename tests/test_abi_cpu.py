@@ -136,11 +136,12 @@ def test_plan_steers_unaligned_shapes_to_the_direct_128_tile(ck, M, N, K, ops, w
     (65536, 512, 256, 2),   # kernels/11_... 4-D product flattened: 128 tile 135 vs 139 us
     (8192, 8192, 128, 2),   # 155 vs 174 us
     (32768, 1024, 192, 2),  # 107 vs 122 us
-    (65536, 512, 512, 3),   # deeper slices: the 256 tile again
+    (4096, 4096, 512, 2),   # 129 vs 137 us
+    (4096, 4096, 4096, 3),  # deep K: the 256 tile again (934 vs 945 us)
     (8192, 8192, 8192, 3),
 ])
 def test_plan_shallow_k_takes_the_128_tile(ck, M, N, K, want):
-    """At K <= 256 the 256 tile (one per CU) cannot hide its tile store behind
+    """At K <= 512 the 256 tile (one per CU) cannot hide its tile store behind
     the next tile's short MFMA run; the cost model discounts it there."""
     rc, p = ck.abi.plan(M, N, K)
     assert rc == 0 and p.plan_id == want, (M, N, K, p.plan_id)
