@@ -648,21 +648,14 @@ inline bool direct4_ok(const GemmLaunch& g) {
 // zero triangle.
 inline hipError_t launch_direct_tri(const GemmLaunch& g, hipStream_t s) {
     const GemmParams p = make_params(g);
-    unsigned n_wg = (unsigned)g.num_tiles;
-    if (g.tri_cap >= 2) {  // dynamic order (see the kernel): one persistent workgroup per CU
+    if (g.tri_cap >= 2) {  // dynamic order (see the kernel): the item counter starts at 0
         float* const ctr = g.structure == kLower ? g.C + 256 : g.C + 256 * g.ldc;
         hipError_t e = launch_zero_word(ctr, s);
         if (e != hipSuccess) return e;
-        int dev = 0, cus = 256;
-        if (hipGetDevice(&dev) == hipSuccess) {
-            int v = 0;
-            if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-                v > 0)
-                cus = v;
-        }
-        if ((unsigned)cus < n_wg) n_wg = (unsigned)cus;
     }
-    dim3 grid(n_wg, 1, 1);
+    // the planner's grid: one persistent workgroup per CU for the dynamic
+    // order, one per item otherwise
+    dim3 grid((unsigned)g.grid_x, 1, 1);
     if (g.structure == kLower)
         hipLaunchKernelGGL((gemm_f32_direct_kernel<Tile256, false, false, false, kLower>), grid,
                            dim3(Tile256::NT), 0, s, p);

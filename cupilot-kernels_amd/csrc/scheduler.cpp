@@ -235,8 +235,10 @@ int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
     grid = std::min(grid, num_tiles);
     // Triangular tiles differ in length: one tile per workgroup, and the
     // hardware's dispatch as slots free up balances them better than a
-    // static stride.
-    if (a.structure != MI_DENSE) grid = num_tiles;
+    // static stride.  The chunked work list with cap >= 2 claims its items
+    // from a counter instead: one persistent workgroup per CU.
+    if (a.structure != MI_DENSE)
+        grid = tri_cap >= 2 ? std::min<int64_t>(num_cus, num_tiles) : num_tiles;
     // Panel configs: each work item is one A row panel times a run of column
     // tiles; enough runs per panel to give every resident workgroup one.
     int64_t col_splits = 1;

@@ -59,9 +59,10 @@ typedef enum {
                        (both: while the call runs, C's zero triangle may hold
                        partial sums and a work counter; it is +0.0 when the
                        stream reaches the next operation) */
-    MI_SYMMETRIC = 3 /* C = A . B with A = A^T and B = B^T (square, per batch): the
-                        operands are read in the fastest orientation (A as stored,
-                        B as its transpose), which the symmetry makes identical */
+    MI_SYMMETRIC = 3 /* C = op_a(A) . op_b(B) for square operands (the reference's
+                        symmetric operator): planned and computed exactly as the
+                        dense product, so a non-symmetric input gets its own
+                        product, as in kernels/13_...:134-151 */
 } mi_structure;
 
 /*
@@ -215,8 +216,9 @@ MI_API int mi_sdpa_f16(const void* Q, const void* K, const void* V, void* O, int
                 void* stream);
 
 /* kernels/13_Matmul_for_symmetric_matrices_best_kernel.cu:134
- * symmetric_matmul_cuda: C = A . B for symmetric N x N A and B.  The kernel
- * reads both operands K-contiguous (valid because A = A^T and B = B^T). */
+ * symmetric_matmul_cuda: C = A . B for N x N A and B (meant for symmetric
+ * inputs; like the reference kernel, :57 and :134-151, it relies on no
+ * symmetry and returns A . B for any input). */
 MI_API int mi_symmetric_matmul_f32(const float* A, const float* B, float* C, int64_t N,
                             void* stream);
 

@@ -531,6 +531,28 @@ def test_symmetric_structure(ck, orc, dev):
     np.testing.assert_array_equal(to_host(C), to_host(C2))
 
 
+@pytest.mark.parametrize("n", [300, 1024])
+def test_symmetric_operator_on_non_symmetric_inputs(ck, orc, dev, n):
+    """PID 13 returns A.B for any input, as kernels/13_...:57,134-151 does
+    (it loads B row-major and uses no symmetry): non-symmetric A and B through
+    the C entry point, the ATen operator and MI_SYMMETRIC all match the fp64
+    A.B, and not A.B^T."""
+    a, b = orc.uniform((n, n), 143), orc.uniform((n, n), 144)
+    A, B = to_dev(a), to_dev(b)
+    ref = orc.gemm(a, b)
+    C = torch.empty((n, n), device="cuda")
+    ck.abi.check(ck.abi.lib().mi_symmetric_matmul_f32(vp(A), vp(B), vp(C), n, cur_stream()))
+    got = to_host(C)
+    assert_close(orc, got, ref, n, what="mi_symmetric_matmul_f32, non-symmetric")
+    wrong = orc.gemm(a, b.T)
+    assert orc.norm_err(got, wrong, n, 1.0, 1.0) > 1e-2   # it is not A.B^T
+    assert_close(orc, to_host(ck.p13.symmetric_matmul_cuda(A, B)), ref, n,
+                 what="p13.symmetric_matmul_cuda, non-symmetric")
+    C3 = torch.empty((n, n), device="cuda")
+    ck.abi.check(run_gemm(ck, gemm_args(ck, A, B, C3, n, n, n, structure=3)))
+    np.testing.assert_array_equal(to_host(C3), got)
+
+
 def test_named_entry_points(ck, orc, dev):
     """Every per-operator C entry point against the oracle on a moderate shape."""
     L = ck.abi.lib()
