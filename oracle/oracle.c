@@ -40,6 +40,11 @@
  *                     batch x heads x seq x embed fp16, scale 1/sqrt(embed)
  *                     at :275, output empty_like(Q)) and :136-250 (scores, row
  *                     softmax with max subtraction, weighted sum of V rows)
+ *   orc_matvec_f64 / orc_checksums_f32
+ *                     fp64 y = A.v of a strided fp32 matrix, and fp64 row / column
+ *                     checksums C.v, u^T.C of an fp32 output block: the
+ *                     whole-output (Freivalds) checks of the full-size tests
+ *                     compare C.v with A.(B.v) and u^T.C with (u^T.A).B.
  *   orc_fill_uniform_f32 / orc_fill_int_f32
  *                     counter-based splitmix64 input generator shared with the
  *                     device fill kernel, so any element can be regenerated on
@@ -281,6 +286,48 @@ ORC_EXPORT void orc_sdpa_f64(const uint16_t* q, const uint16_t* k, const uint16_
             }
             free(s);
         }
+}
+
+/* y[r] = sum_c A(r, c) * v[c] in fp64, A(r, c) = A[r * rs + c * cs]: a
+ * strided fp32 matrix (a transposed view is the same data with rs and cs
+ * swapped).  Used for the whole-output checksums of the full-size tests:
+ * A.(B.v) needs two of these, O(MK + KN) instead of the O(MNK) product. */
+ORC_EXPORT void orc_matvec_f64(const float* A, int64_t rows, int64_t cols, int64_t rs, int64_t cs,
+                               const double* v, double* y) {
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; ++r) {
+        double s = 0.0;
+        const float* a = A + r * rs;
+        for (int64_t c = 0; c < cols; ++c) s += (double)a[c * cs] * v[c];
+        y[r] = s;
+    }
+}
+
+/* Row and column checksums of an fp32 block C (rows x cols, row stride ldc),
+ * in fp64: cv[r] = sum_c C[r][c] * v[c] (written) and utc[c] += sum_r u[r] *
+ * C[r][c] (accumulated, so a large output can be reduced block by block).
+ * Every element of the block enters both. */
+ORC_EXPORT void orc_checksums_f32(const float* C, int64_t rows, int64_t cols, int64_t ldc,
+                                  const double* v, const double* u, double* cv, double* utc) {
+#pragma omp parallel
+    {
+        double* acc = (double*)calloc((size_t)cols, sizeof(double));
+#pragma omp for schedule(static)
+        for (int64_t r = 0; r < rows; ++r) {
+            const float* c = C + r * ldc;
+            const double ur = u[r];
+            double s = 0.0;
+            for (int64_t j = 0; j < cols; ++j) {
+                const double x = (double)c[j];
+                s += x * v[j];
+                acc[j] += ur * x;
+            }
+            cv[r] = s;
+        }
+#pragma omp critical
+        for (int64_t j = 0; j < cols; ++j) utc[j] += acc[j];
+        free(acc);
+    }
 }
 
 /* max_t |got[t] - ref[t]| over n elements (fp32 result vs fp64 reference). */

@@ -60,6 +60,8 @@ def lib():
         L.orc_half_to_double.restype = ctypes.c_double
         _u16p = ctypes.POINTER(ctypes.c_uint16)
         L.orc_sdpa_f64.argtypes = [_u16p, _u16p, _u16p, _f64p, _i64, _i64, _i64, ctypes.c_double]
+        L.orc_matvec_f64.argtypes = [_f32p, _i64, _i64, _i64, _i64, _f64p, _f64p]
+        L.orc_checksums_f32.argtypes = [_f32p, _i64, _i64, _i64, _f64p, _f64p, _f64p, _f64p]
         L.orc_max_abs_diff.restype = ctypes.c_double
         L.orc_max_abs_diff.argtypes = [_f32p, _f64p, _i64]
         L.orc_num_threads.restype = ctypes.c_int
@@ -189,6 +191,38 @@ def gemv_generated(seed_a: int, x: np.ndarray, rows: Sequence[int]) -> np.ndarra
     lib().orc_gemv_generated_f64(seed_a, _fp(x), _dp(out), x.shape[0],
                                  rows_arr.ctypes.data_as(_i64p), len(rows_arr))
     return out
+
+
+def matvec(a: np.ndarray, v: np.ndarray) -> np.ndarray:
+    """fp64 ``a @ v`` for a 2-D fp32 array or view (any non-negative strides,
+    so ``x.T`` needs no copy) and a length-cols vector."""
+    assert a.dtype == np.float32 and a.ndim == 2 and min(a.strides) >= 0
+    v = np.ascontiguousarray(v, dtype=np.float64).reshape(-1)
+    rows, cols = a.shape
+    assert v.shape[0] == cols
+    rs, cs = _strides2(a)
+    out = np.empty(rows, dtype=np.float64)
+    lib().orc_matvec_f64(ctypes.cast(a.ctypes.data, _f32p), rows, cols, rs, cs, _dp(v), _dp(out))
+    return out
+
+
+def checksums(c: np.ndarray, v: np.ndarray, u: np.ndarray, utc: Optional[np.ndarray] = None):
+    """fp64 row checksums ``c @ v`` and column checksums ``u @ c`` of an fp32
+    block with unit column stride.  ``utc`` (float64, length cols) is
+    accumulated into when given, so a large output can be reduced in row
+    blocks; returns (c @ v, utc)."""
+    assert c.dtype == np.float32 and c.ndim == 2 and c.strides[1] == 4
+    rows, cols = c.shape
+    v = np.ascontiguousarray(v, dtype=np.float64).reshape(-1)
+    u = np.ascontiguousarray(u, dtype=np.float64).reshape(-1)
+    assert v.shape[0] == cols and u.shape[0] == rows
+    if utc is None:
+        utc = np.zeros(cols, dtype=np.float64)
+    assert utc.dtype == np.float64 and utc.shape == (cols,) and utc.flags["C_CONTIGUOUS"]
+    cv = np.empty(rows, dtype=np.float64)
+    lib().orc_checksums_f32(ctypes.cast(c.ctypes.data, _f32p), rows, cols, c.strides[0] // 4,
+                            _dp(v), _dp(u), _dp(cv), _dp(utc))
+    return cv, utc
 
 
 def diag_mult(a: np.ndarray, b: np.ndarray) -> np.ndarray:

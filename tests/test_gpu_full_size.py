@@ -1,16 +1,22 @@
 """Parity at BASELINE.json's full sizes, on the GPU, through the drop-in operators.
 
 Inputs come from the device generator with the BASELINE seeds (16*cfg + tensor);
-the host regenerates or copies them for the fp64 oracle.  Where a dense fp64
-reference of the whole output would not fit the test budget, the check is on
-sampled rows (including tile-boundary rows) and sampled entries, plus
-size-independent properties: exact structural zeros, symmetry of the inputs,
-bitwise repeatability of split-K.  Tolerance: the north-star bound 1e-4.
+the host regenerates or copies them for the fp64 oracle.  Every output element
+of every config is checked:
+  * outputs small enough for an fp64 reference of the whole product (1024^3,
+    small-K, diag, GEMV) are compared element by element;
+  * the others enter fp64 row and column checksums, C.v against A.(B.v) and
+    u^T.C against (u^T.A).B with random +-1 vectors (tests/freivalds.py gives
+    the bounds), reduced on the host in row blocks, plus exact fp64 values of
+    sampled rows (tile-boundary rows included) and entries;
+plus size-independent properties: exact structural zeros, symmetry of the
+inputs, bitwise repeatability of split-K.  Tolerance: the north-star bound 1e-4.
 """
 import numpy as np
 import pytest
 import torch
 
+import freivalds as fv
 from gpu_util import assert_close, dev_uniform, to_host
 
 pytestmark = pytest.mark.gpu
@@ -27,6 +33,28 @@ def _entries(M, N, count=1024, seed=1):
     rng = np.random.default_rng(seed)
     return np.stack([np.zeros(count, np.int64), rng.integers(0, M, count),
                      rng.integers(0, N, count)], axis=1)
+
+
+def _dev_checksums(orc, C, v, u, block_bytes=1 << 29):
+    """fp64 C.v and u^T.C of a 2-D device tensor, copied to the host in row
+    blocks of at most block_bytes."""
+    M, N = C.shape
+    rows = max(1, block_bytes // (4 * N))
+    cv = np.empty(M, dtype=np.float64)
+    utc = np.zeros(N, dtype=np.float64)
+    for r0 in range(0, M, rows):
+        blk = to_host(C[r0:r0 + rows])
+        cv[r0:r0 + rows], utc = orc.checksums(blk, v, u[r0:r0 + rows], utc)
+    return cv, utc
+
+
+def _whole(orc, C, a, b, K, seed, what):
+    """Every element of device output C (M x N) against the fp64 a.b (host
+    fp32 operands or views) through row and column checksums."""
+    M, N = C.shape
+    v, u = fv.signs(N, seed), fv.signs(M, seed + 1)
+    ref = fv.reference(orc, a, b, v, u)
+    return fv.check(orc, *_dev_checksums(orc, C, v, u), *ref, K, 1.0, 1.0, what)
 
 
 def test_cfg0_square_1024_full(ck, orc):
@@ -53,6 +81,7 @@ def test_cfg1_8192_four_layouts(ck, orc, layout):
     bij = _entries(n, n, 2048)
     got = to_host(C)[bij[:, 1], bij[:, 2]]
     assert_close(orc, got, orc.gemm_entries(la, lb, bij), n, what=f"8192 {layout} entries")
+    _whole(orc, C, la, lb, n, 100, f"8192 {layout} every element")
 
 
 def test_cfg2_batched(ck, orc):
@@ -60,9 +89,11 @@ def test_cfg2_batched(ck, orc):
     A = dev_uniform(ck, (bsz, M, K), 32)
     B = dev_uniform(ck, (bsz, K, N), 33)
     C = ck.p03.batched_matmul_cuda(A, B)
+    Ah, Bh = to_host(A), to_host(B)
     for bi in (0, 77, 127):
-        a, b = to_host(A[bi]), to_host(B[bi])
-        assert_close(orc, to_host(C[bi]), orc.gemm(a, b), K, what=f"batched b={bi}")
+        assert_close(orc, to_host(C[bi]), orc.gemm(Ah[bi], Bh[bi]), K, what=f"batched b={bi}")
+    for bi in range(bsz):   # every batch, every element
+        _whole(orc, C[bi], Ah[bi], Bh[bi], K, 200 + 2 * bi, f"batched b={bi} every element")
 
 
 def test_cfg2_tensor3d(ck, orc):
@@ -75,6 +106,7 @@ def test_cfg2_tensor3d(ck, orc):
     rows = _rows(n * M, extra=16)
     assert_close(orc, to_host(out.reshape(-1, L)[rows]), orc.gemm(flat, to_host(B), rows=rows), K,
                  what="3d")
+    _whole(orc, out.reshape(-1, L), flat, to_host(B), K, 300, "3d every element")
 
 
 def test_cfg2_tensor4d(ck, orc):
@@ -87,6 +119,7 @@ def test_cfg2_tensor4d(ck, orc):
     rows = _rows(b * i * j, extra=16)
     assert_close(orc, to_host(out.reshape(-1, k)[rows]), orc.gemm(flat, to_host(B), rows=rows), l,
                  what="4d")
+    _whole(orc, out.reshape(-1, k), flat, to_host(B), l, 400, "4d every element")
 
 
 def test_cfg3_gemv_full_size(ck, orc):
@@ -94,9 +127,9 @@ def test_cfg3_gemv_full_size(ck, orc):
     A = dev_uniform(ck, (M, K), 48)
     x = dev_uniform(ck, (K, 1), 50)
     y = to_host(ck.p04.gemv_cuda(A, x))[:, 0]
-    rows = _rows(M, extra=64)
-    ref = orc.gemv_generated(48, to_host(x)[:, 0], rows)   # A regenerated row by row on the host
-    assert_close(orc, y[rows], ref, K, what="gemv rows")
+    # every row; A (8 GiB) is regenerated row by row on the host
+    ref = orc.gemv_generated(48, to_host(x)[:, 0], np.arange(M))
+    assert_close(orc, y, ref, K, what="gemv every row")
     assert np.all(np.isfinite(y))
 
 
@@ -121,12 +154,15 @@ def test_cfg4_large_k_split_deterministic(ck, orc):
     K = 1 << 20
     A = dev_uniform(ck, (M, K), 64)
     B = dev_uniform(ck, (K, N), 65)
-    C1 = to_host(ck.p06.matmul_cuda(A, B))
+    Cd = ck.p06.matmul_cuda(A, B)
+    C1 = to_host(Cd)
     C2 = to_host(ck.p06.matmul_cuda(A, B))
     np.testing.assert_array_equal(C1, C2)
+    a, b = to_host(A), to_host(B)
     bij = _entries(M, N, 512)
-    assert_close(orc, C1[bij[:, 1], bij[:, 2]], orc.gemm_entries(to_host(A), to_host(B), bij), K,
+    assert_close(orc, C1[bij[:, 1], bij[:, 2]], orc.gemm_entries(a, b, bij), K,
                  what="large-K entries")
+    _whole(orc, Cd, a, b, K, 500, "large-K every element")
 
 
 def test_cfg4_tall_skinny(ck, orc):
@@ -142,6 +178,8 @@ def test_cfg4_tall_skinny(ck, orc):
     got = to_host(C[:, cols])
     ref = orc.gemm(a, np.ascontiguousarray(b[:, cols]))
     assert_close(orc, got, ref, K, what="tall-skinny cols")
+    # the 16 GiB output, every element, reduced in 512 MiB row blocks
+    _whole(orc, C, a, b, K, 600, "tall-skinny every element")
 
 
 @pytest.mark.parametrize("structure", ["lower", "upper"])
@@ -154,8 +192,12 @@ def test_cfg4_triangular(ck, orc, structure):
     C = fn(A, B)
     s = orc.LOWER if structure == "lower" else orc.UPPER
     rows = _rows(n, extra=6)
+    a, b = to_host(A), to_host(B)
     got = to_host(C[rows])
-    assert_close(orc, got, orc.gemm(to_host(A), to_host(B), s, rows=rows), n, what=structure)
+    assert_close(orc, got, orc.gemm(a, b, s, rows=rows), n, what=structure)
+    # tril(A).tril(B) is itself lower triangular (triu likewise), so the
+    # whole C equals a.b with the masked inputs
+    _whole(orc, C, a, b, n, 700, f"{structure} every element")
     # every element on the wrong side of the diagonal is exactly +0.0
     Ch = to_host(C)
     wrong = np.triu(np.ones((n, n), bool), 1) if structure == "lower" else np.tril(np.ones((n, n), bool), -1)
@@ -172,5 +214,6 @@ def test_cfg4_symmetric(ck, orc):
     assert torch.equal(A, A.t()) and torch.equal(B, B.t())
     C = ck.p13.symmetric_matmul_cuda(A, B)
     rows = _rows(n, extra=4)
-    assert_close(orc, to_host(C[rows]), orc.gemm(to_host(A), to_host(B), rows=rows), n,
-                 what="symmetric")
+    a, b = to_host(A), to_host(B)
+    assert_close(orc, to_host(C[rows]), orc.gemm(a, b, rows=rows), n, what="symmetric")
+    _whole(orc, C, a, b, n, 800, "symmetric every element")

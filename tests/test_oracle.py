@@ -372,3 +372,57 @@ def test_fp32_accumulation_error_is_far_below_tolerance(orc):
         acc += np.outer(a[:, k], b[k, :]).astype(np.float32)
     err = orc.norm_err(acc, ref, K, 1, 1)
     assert err < 1e-5
+
+
+# ---- whole-output checksums (full-size tests) ------------------------------------
+
+def test_matvec_and_checksums_vs_numpy(orc):
+    a = orc.uniform((300, 200), 901)
+    v = np.random.default_rng(0).standard_normal(200)
+    u = np.random.default_rng(1).standard_normal(300)
+    np.testing.assert_allclose(orc.matvec(a, v), a.astype(np.float64) @ v, rtol=1e-13, atol=1e-12)
+    # a transposed view is read in place through its strides
+    np.testing.assert_allclose(orc.matvec(a.T, u), a.astype(np.float64).T @ u, rtol=1e-13, atol=1e-12)
+    cv, utc = orc.checksums(a, v, u)
+    np.testing.assert_allclose(cv, a.astype(np.float64) @ v, rtol=1e-13, atol=1e-12)
+    np.testing.assert_allclose(utc, u @ a.astype(np.float64), rtol=1e-13, atol=1e-12)
+    # block by block (row slices, a padded row stride) accumulates the same
+    # column checksums
+    big = orc.uniform((300, 256), 902)
+    blk = big[:, :200]
+    acc = np.zeros(200)
+    parts = []
+    for r0 in range(0, 300, 64):
+        c, acc = orc.checksums(blk[r0:r0 + 64], v, u[r0:r0 + 64], acc)
+        parts.append(c)
+    np.testing.assert_allclose(np.concatenate(parts), blk.astype(np.float64) @ v, rtol=1e-13, atol=1e-12)
+    np.testing.assert_allclose(acc, u @ blk.astype(np.float64), rtol=1e-12, atol=1e-11)
+
+
+def test_freivalds_accepts_fp32_products_and_catches_planted_mistakes(orc):
+    import freivalds as fv
+    M, K, N = 512, 1024, 384
+    a, b = orc.uniform((M, K), 903), orc.uniform((K, N), 904)
+    v, u = fv.signs(N, 5), fv.signs(M, 6)
+    ref_cv, ref_utc = fv.reference(orc, a, b, v, u)
+    np.testing.assert_allclose(ref_cv, orc.gemm(a, b) @ v, rtol=1e-10, atol=1e-8)
+    np.testing.assert_allclose(ref_utc, u @ orc.gemm(a, b), rtol=1e-10, atol=1e-8)
+    c = (a @ b).astype(np.float32)             # an fp32-accumulated product passes
+    fv.check(orc, *orc.checksums(c, v, u), ref_cv, ref_utc, K, 1.0, 1.0, "fp32 product")
+    # transposed-operand layouts through views
+    at = np.ascontiguousarray(a.T)
+    cv_t, utc_t = fv.reference(orc, at.T, b, v, u)
+    np.testing.assert_allclose(cv_t, ref_cv, rtol=1e-13, atol=1e-10)
+    plants = {
+        "one 32x32 block zero": lambda x: x.__setitem__((slice(64, 96), slice(32, 64)), 0.0),
+        "one tile from the wrong K range": lambda x: x.__setitem__(
+            (slice(0, 128), slice(0, 128)), (a[:128, :512] @ b[:512, :128]).astype(np.float32)),
+        "one row shifted": lambda x: x.__setitem__(7, np.roll(x[7], 1)),
+        "one element off by 1": lambda x: x.__setitem__((100, 200), x[100, 200] + 1.0),
+        "sign flip of one column": lambda x: x.__setitem__((slice(None), 5), -x[:, 5]),
+    }
+    for name, plant in plants.items():
+        bad = c.copy()
+        plant(bad)
+        with pytest.raises(AssertionError):
+            fv.check(orc, *orc.checksums(bad, v, u), ref_cv, ref_utc, K, 1.0, 1.0, name)
