@@ -23,6 +23,8 @@ MI_ERR_NOT_SQUARE = -5
 MI_ERR_WORKSPACE = -6
 MI_ERR_NO_DEVICE = -7
 MI_ERR_ALIGNMENT = -8
+MI_ERR_SCRATCH_LIMIT = -9
+NOALLOC_SCRATCH_BYTES = 64 << 20
 
 MI_OP_N, MI_OP_T = 0, 1
 MI_DENSE, MI_LOWER, MI_UPPER, MI_SYMMETRIC = 0, 1, 2, 3
@@ -60,6 +62,7 @@ class Plan(ctypes.Structure):
 # name -> (restype, argtypes); every symbol include/mi355_gemm.h declares
 SIGNATURES = {
     "mi_gemm_f32": (ctypes.c_int, [ctypes.POINTER(GemmArgs), _vp]),
+    "mi_gemm_f32_noalloc": (ctypes.c_int, [ctypes.POINTER(GemmArgs), _vp]),
     "mi_gemm_workspace_bytes": (_sz, [ctypes.POINTER(GemmArgs)]),
     "mi_gemm_plan": (ctypes.c_int, [ctypes.POINTER(GemmArgs), ctypes.c_int32, ctypes.POINTER(Plan)]),
     "mi_gemm_tile_of": (ctypes.c_int, [ctypes.POINTER(GemmArgs), ctypes.c_int32, _i64, ctypes.c_int32,

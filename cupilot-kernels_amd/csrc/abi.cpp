@@ -94,6 +94,9 @@ const char* mi_status_string(int status) {
         case MI_ERR_WORKSPACE: return "workspace missing or too small";
         case MI_ERR_NO_DEVICE: return "no HIP device available";
         case MI_ERR_ALIGNMENT: return "pointer not 16-byte aligned";
+        case MI_ERR_SCRATCH_LIMIT:
+            return "problem needs more split-K scratch than mi_gemm_f32_noalloc's fixed "
+                   "64 MiB device array holds (use mi_gemm_f32 with a workspace)";
         default: break;
     }
     if (status > 0) return hipGetErrorString(static_cast<hipError_t>(status));

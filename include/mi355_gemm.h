@@ -15,7 +15,9 @@
  *     Work is enqueued asynchronously; nothing synchronises the host.
  *   - The library never allocates or frees device memory and keeps no pointer
  *     after returning.  Entry points that need scratch take a workspace; its
- *     size comes from the matching *_workspace_bytes query.
+ *     size comes from the matching *_workspace_bytes query.  (The one
+ *     exception, mi_gemm_f32_noalloc, keeps its scratch in a fixed array the
+ *     library holds on each device.)
  *   - Return value: MI_OK (0); a negative mi_status for an invalid argument
  *     (checked before any launch); a positive hipError_t for a launch failure.
  *     mi_status_string() turns either into text.
@@ -47,7 +49,9 @@ typedef enum {
     MI_ERR_NOT_SQUARE = -5,     /* structured op on a non-square problem */
     MI_ERR_WORKSPACE = -6,      /* workspace missing or too small */
     MI_ERR_NO_DEVICE = -7,      /* no HIP device / device query failed */
-    MI_ERR_ALIGNMENT = -8       /* a pointer is not 16-byte aligned where required */
+    MI_ERR_ALIGNMENT = -8,      /* a pointer is not 16-byte aligned where required */
+    MI_ERR_SCRATCH_LIMIT = -9   /* mi_gemm_f32_noalloc: the problem's plan needs more
+                                   scratch than MI_NOALLOC_SCRATCH_BYTES */
 } mi_status;
 
 typedef enum { MI_OP_N = 0, MI_OP_T = 1 } mi_op;
@@ -107,6 +111,24 @@ typedef struct {
 
 MI_API int mi_gemm_f32(const mi_gemm_args* args, void* stream);
 MI_API size_t mi_gemm_workspace_bytes(const mi_gemm_args* args);
+/* Allocation-free variant of mi_gemm_f32 (no counterpart in the reference; for
+ * callers that cannot allocate device memory: code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Same arguments and
+ * result as mi_gemm_f32 -- the same plan, kernels and reduction order as a
+ * call given a workspace of mi_gemm_workspace_bytes(args) bytes, so the same
+ * bits -- but args->workspace and args->workspace_bytes are ignored: the
+ * split-K partial tiles go to a fixed MI_NOALLOC_SCRATCH_BYTES array the
+ * library holds on each device (for the life of the process) instead.
+ *   - A problem whose plan needs more scratch than that returns
+ *     MI_ERR_SCRATCH_LIMIT before anything is launched.
+ *   - The first call on a device looks up that device's copy of the array
+ *     (hipGetSymbolAddress, once per device); make that first call outside
+ *     graph capture.  Calls, and captures, after it allocate nothing.
+ *   - Every call on one device shares its array: calls that overlap on one
+ *     device (unordered streams or host threads) race.  Nothing in the array
+ *     needs clearing between calls. */
+#define MI_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+MI_API int mi_gemm_f32_noalloc(const mi_gemm_args* args, void* stream);
 /* Pure host function: what mi_gemm_f32 would launch on a device with num_cus
  * compute units.  Exposed for tests and tuning. */
 MI_API int mi_gemm_plan(const mi_gemm_args* args, int32_t num_cus, mi_plan* out);

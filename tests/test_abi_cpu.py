@@ -35,6 +35,9 @@ def test_every_named_entry_point_cites_a_reference_file():
         if n in ("mi_gemm_f32", "mi_gemm_workspace_bytes", "mi_gemm_plan", "mi_gemm_tile_of",
                  "mi_fill_uniform_f32", "mi_status_string", "mi_version"):
             continue
+        if n == "mi_gemm_f32_noalloc":   # says it has none, and whom it is for
+            assert "no counterpart in the reference" in block and "cannot allocate" in block
+            continue
         if n.endswith("_workspace_bytes"):
             continue
         assert "kernels/" in block, f"{n} has no reference citation"
@@ -43,7 +46,7 @@ def test_every_named_entry_point_cites_a_reference_file():
 def test_status_strings(ck):
     L = ck.abi.lib()
     assert L.mi_status_string(0) == b"ok"
-    for s in range(-7, 0):
+    for s in range(-9, 0):
         assert L.mi_status_string(s) != b"unknown status"
     assert b"gfx950" in L.mi_version()
 
