@@ -56,6 +56,15 @@ class Plan(ctypes.Structure):
         ("block_k", ctypes.c_int32), ("tiles_m", ctypes.c_int32), ("tiles_n", ctypes.c_int32),
         ("split_k", ctypes.c_int32), ("k_chunk", _i64), ("group_m", ctypes.c_int32),
         ("num_tiles", _i64), ("grid", _i64), ("workspace_bytes", _sz),
+        ("stream_k", ctypes.c_int32), ("sk_tiles", _i64),
+    ]
+
+
+class WorkItem(ctypes.Structure):
+    """mirror of mi_work_item"""
+    _fields_ = [
+        ("tile_m", ctypes.c_int32), ("tile_n", ctypes.c_int32),
+        ("k_begin", _i64), ("k_end", _i64), ("dest", ctypes.c_int32), ("slot", ctypes.c_int32),
     ]
 
 
@@ -63,6 +72,11 @@ class Plan(ctypes.Structure):
 SIGNATURES = {
     "mi_gemm_f32": (ctypes.c_int, [ctypes.POINTER(GemmArgs), _vp]),
     "mi_gemm_f32_noalloc": (ctypes.c_int, [ctypes.POINTER(GemmArgs), _vp]),
+    "mi_gemm_work_item": (ctypes.c_int, [ctypes.POINTER(GemmArgs), ctypes.c_int32, _i64, ctypes.c_int32,
+                                         _i64, ctypes.POINTER(WorkItem)]),
+    "mi_gemm_sk_fixup_of": (ctypes.c_int, [ctypes.POINTER(GemmArgs), ctypes.c_int32, _i64,
+                                           ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32),
+                                           ctypes.POINTER(_i64), ctypes.POINTER(_i64)]),
     "mi_gemm_workspace_bytes": (_sz, [ctypes.POINTER(GemmArgs)]),
     "mi_gemm_plan": (ctypes.c_int, [ctypes.POINTER(GemmArgs), ctypes.c_int32, ctypes.POINTER(Plan)]),
     "mi_gemm_tile_of": (ctypes.c_int, [ctypes.POINTER(GemmArgs), ctypes.c_int32, _i64, ctypes.c_int32,
@@ -146,6 +160,30 @@ def plan(M, N, K, num_cus=256, **kw):
     p = Plan()
     rc = lib().mi_gemm_plan(ctypes.byref(a), num_cus, ctypes.byref(p))
     return rc, p
+
+
+def work_items(args, wg, split=0, num_cus=256):
+    """Every work item of workgroup wg in run order (mi_gemm_work_item):
+    [(tile_m, tile_n, k_begin, k_end, dest, slot), ...]."""
+    out, item = [], 0
+    w = WorkItem()
+    while True:
+        rc = lib().mi_gemm_work_item(ctypes.byref(args), num_cus, wg, split, item, ctypes.byref(w))
+        if rc < 0:
+            raise RuntimeError(f"mi_gemm_work_item: {rc}")
+        if rc == 0:
+            return out
+        out.append((w.tile_m, w.tile_n, w.k_begin, w.k_end, w.dest, w.slot))
+        item += 1
+
+
+def sk_fixup_of(args, t, num_cus=256):
+    """(status, tile_m, tile_n, first_slot, n_slots) of stream-K tile t."""
+    tm, tn = ctypes.c_int32(), ctypes.c_int32()
+    f, n = _i64(), _i64()
+    rc = lib().mi_gemm_sk_fixup_of(ctypes.byref(args), num_cus, t, ctypes.byref(tm), ctypes.byref(tn),
+                                   ctypes.byref(f), ctypes.byref(n))
+    return rc, tm.value, tn.value, f.value, n.value
 
 
 def tile_of(args, wg, split=0, num_cus=256):

@@ -124,6 +124,7 @@ int mi_gemm_tile_of(const mi_gemm_args* args, int32_t num_cus, int64_t item, int
     rc = plan_gemm(ca, num_cus, p, &g);
     if (rc != MI_OK) return rc;
     if (item < 0 || item >= g.num_tiles || split < 0 || split >= g.split_k) return MI_ERR_BAD_SIZE;
+    if (g.sk_tiles > 0) return MI_ERR_BAD_LAYOUT;  // stream-K: mi_gemm_work_item
     const GemmParams kp = make_params(g);
     int tm = 0, tn = 0, kb = 0, ke = 0;
     bool compute;
@@ -166,6 +167,72 @@ int mi_gemm_tile_of(const mi_gemm_args* args, int32_t num_cus, int64_t item, int
     return compute ? 1 : 0;
 }
 
+int mi_gemm_work_item(const mi_gemm_args* args, int32_t num_cus, int64_t wg, int32_t split,
+                      int64_t item, mi_work_item* out) {
+    if (!args || !out) return MI_ERR_NULL_POINTER;
+    mi_gemm_args ca = *args;
+    int rc = canonical(ca);
+    if (rc != MI_OK) return rc;
+    mi_plan p{};
+    GemmLaunch g{};
+    rc = plan_gemm(ca, num_cus, p, &g);
+    if (rc != MI_OK) return rc;
+    if (is_panel_cfg(g.cfg) || g.structure != kDense) return MI_ERR_BAD_LAYOUT;
+    if (wg < 0 || wg >= g.grid_x || split < 0 || split >= g.split_k || item < 0) return MI_ERR_BAD_SIZE;
+    if (item > INT32_MAX) return 0;
+    const CfgInfo ci = cfg_info(g.cfg);
+    if (g.sk_tiles > 0) {
+        int lt, s0, s1, to_ws;
+        if (!sk_work((int)wg, (int)item, g.grid_x, g.sk_dp, g.sk_tiles, g.sk_ipt, lt, s0, s1, to_ws))
+            return 0;
+        int tm, tn;
+        raster(lt, g.tiles_m, g.tiles_n, g.group_m, tm, tn);
+        out->tile_m = tm;
+        out->tile_n = tn;
+        out->k_begin = (int64_t)s0 * ci.bk;
+        out->k_end = (int64_t)s1 * ci.bk;
+        out->dest = to_ws;
+        out->slot = to_ws ? xcd_remap((int)wg, g.grid_x) : 0;
+        return 1;
+    }
+    const int64_t t = wg + item * g.grid_x;
+    if (t >= g.num_tiles) return 0;
+    const GemmParams kp = make_params(g);
+    int tm = 0, tn = 0, kb = 0, ke = 0;
+    switch (g.cfg) {
+        case kCfg64: tile_of<64, 64, kDense>(kp, (int)t, g.num_tiles, split, tm, tn, kb, ke); break;
+        case kCfg256: tile_of<256, 256, kDense>(kp, (int)t, g.num_tiles, split, tm, tn, kb, ke); break;
+        default: tile_of<128, 128, kDense>(kp, (int)t, g.num_tiles, split, tm, tn, kb, ke); break;
+    }
+    out->tile_m = tm;
+    out->tile_n = tn;
+    out->k_begin = kb;
+    out->k_end = ke;
+    out->dest = g.split_k > 1 ? 1 : 0;
+    out->slot = g.split_k > 1 ? split : 0;
+    return 1;
+}
+
+int mi_gemm_sk_fixup_of(const mi_gemm_args* args, int32_t num_cus, int64_t t, int32_t* tile_m,
+                        int32_t* tile_n, int64_t* first_slot, int64_t* n_slots) {
+    if (!args || !tile_m || !tile_n || !first_slot || !n_slots) return MI_ERR_NULL_POINTER;
+    mi_gemm_args ca = *args;
+    int rc = canonical(ca);
+    if (rc != MI_OK) return rc;
+    mi_plan p{};
+    GemmLaunch g{};
+    rc = plan_gemm(ca, num_cus, p, &g);
+    if (rc != MI_OK) return rc;
+    if (g.sk_tiles <= 0) return MI_ERR_BAD_LAYOUT;
+    if (t < 0 || t >= g.sk_tiles) return MI_ERR_BAD_SIZE;
+    int tm, tn;
+    raster(g.sk_dp + (int)t, g.tiles_m, g.tiles_n, g.group_m, tm, tn);
+    *tile_m = tm;
+    *tile_n = tn;
+    sk_fixup_slots(t, g.sk_tiles, g.sk_ipt, g.grid_x, *first_slot, *n_slots);
+    return 1;
+}
+
 size_t mi_gemm_workspace_bytes(const mi_gemm_args* args) {
     if (!args) return 0;
     mi_gemm_args a = *args;
@@ -200,7 +267,8 @@ int mi_gemm_f32(const mi_gemm_args* args, void* stream) {
     GemmLaunch g{};
     rc = plan_gemm(a, cus, p, &g);
     if (rc != MI_OK) return rc;
-    if (g.split_k > 1 && (!a.workspace || a.workspace_bytes < p.workspace_bytes))
+    if ((g.split_k > 1 || g.sk_tiles > 0) &&
+        (!a.workspace || a.workspace_bytes < p.workspace_bytes))
         return MI_ERR_WORKSPACE;
 
     hipError_t e;

@@ -222,7 +222,10 @@ struct DirectLoader {
 // Triangular modes write +0.0 on the wrong side of the diagonal, except for a
 // chunk whose partial sum goes to the mirror tile: it is stored unmasked at
 // (tn, tm) -- the same offsets within the tile -- for tri_finish to add in.
-template <class T, bool A_IL, bool B_IL, bool BIAS, int MODE>
+// LOCAL: C points at a BM x BN workspace tile (row stride ldc) that receives
+// the tile's elements at their offsets within the tile (a stream-K partial);
+// rows and columns past M / N are still skipped.
+template <class T, bool A_IL, bool B_IL, bool BIAS, int MODE, bool LOCAL = false>
 __device__ __forceinline__ void store_tile_direct(const GemmParams& p, float* C, int64_t ldc,
                                                   bool c_vec, const TileWork& w,
                                                   const f16v (&acc)[T::TM][T::TN], int wm, int wn,
@@ -241,7 +244,7 @@ __device__ __forceinline__ void store_tile_direct(const GemmParams& p, float* C,
         const int row = r0 + wm * T::WM + (A_IL ? 64 * (i / 2) + 2 * l32 + (i & 1) : 32 * i + l32);
         if (row >= p.M) continue;
         const float bv = add_bias ? p.bias[row] : 0.f;
-        float* const crow = C + (int64_t)row * ldc;
+        float* const crow = LOCAL ? C + (int64_t)(row - r0) * ldc : C + (int64_t)row * ldc;
         // one 16-byte group: columns col .. col + 3 get v
         auto put = [&](int col, f4 v) __attribute__((always_inline)) {
             if (add_bias) v += bv;
@@ -250,12 +253,13 @@ __device__ __forceinline__ void store_tile_direct(const GemmParams& p, float* C,
                 for (int e = 0; e < 4; ++e)
                     if (MODE == kLower ? col + e > row : col + e < row) v[e] = 0.f;
             }
+            float* const dst = LOCAL ? crow + (col - c0) : crow + col;
             if (c_vec && col + 3 < p.N) {
-                *reinterpret_cast<f4*>(crow + col) = v;
+                *reinterpret_cast<f4*>(dst) = v;
             } else {
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    if (col + e < p.N) crow[col + e] = v[e];
+                    if (col + e < p.N) dst[e] = v[e];
             }
         };
 #pragma unroll
@@ -297,13 +301,19 @@ __device__ __forceinline__ void store_tile_direct(const GemmParams& p, float* C,
 // per workgroup (grid = items, dispatched longest first).  Operand entries on
 // the wrong side of the diagonal are zeroed in the fragments of the diagonal
 // K unit (tril(A) tril(B) / triu(A) triu(B) for any input).
-template <class T, bool AT, bool BT, bool BIAS, int MODE = kDense, int VB = 16>
+//
+// SK: the stream-K schedule (sk_work): workgroup b runs its items 0, 1, ...
+// -- whole tiles, then the segments of its K-slice range -- and stores a
+// segment that does not start at k = 0 into its workspace slot
+// (xcd_remap(b, grid)), tile-local, for sk_fixup to add in.
+template <class T, bool AT, bool BT, bool BIAS, int MODE = kDense, int VB = 16, bool SK = false>
 __global__ void __launch_bounds__(T::NT)
     __attribute__((amdgpu_waves_per_eu(T::WAVES_PER_SIMD, T::WAVES_PER_SIMD)))
     gemm_f32_direct_kernel(const GemmParams p) {
     static_assert(T::STAGES == 2 && T::BM == T::BN, "double-buffered square tiles");
     static_assert(MODE == kDense || (!AT && !BT && T::BM == 256 && VB == 16),
                   "triangular products are N/N on the 256 tile");
+    static_assert(!SK || (MODE == kDense && VB == 16 && !BIAS), "stream-K: dense, 16-byte, no bias");
     constexpr bool A_KC = !AT;  // A row-major (M x K) is contiguous along K
     constexpr bool B_KC = BT;   // B stored N x K is contiguous along K
     using LA = DirectLoader<A_KC, T::NW, T::BM, T::BK, VB>;
@@ -367,7 +377,22 @@ __global__ void __launch_bounds__(T::NT)
         LB::load(B, p.ldb, w.tn * T::BN, k0, voB, dB, wave);
     };
     auto decode = [&](int item) __attribute__((always_inline)) -> TileWork {
-        if constexpr (MODE == kDense) {
+        if constexpr (SK) {
+            // compute = 0: past the workgroup's last item
+            TileWork w;
+            int lt, s0, s1, to_ws;
+            w.compute = sk_work(blockIdx.x, item, gridDim.x, p.sk_dp, p.sk_tiles, p.sk_ipt, lt,
+                                s0, s1, to_ws)
+                            ? 1
+                            : 0;
+            if (!w.compute) lt = s0 = s1 = to_ws = 0;
+            raster(lt, p.tiles_m, p.tiles_n, p.group_m, w.tm, w.tn);
+            w.k_begin = s0 * T::BK;
+            w.k_end = s1 * T::BK;
+            w.nk = s1 - s0;
+            w.mirror = to_ws;
+            return w;
+        } else if constexpr (MODE == kDense) {
             return decode_tile<T, kDense>(p, item);
         } else {
             TileWork w;
@@ -524,14 +549,18 @@ __global__ void __launch_bounds__(T::NT)
     __shared__ int s_item;
     int* const ctr = MODE == kLower ? reinterpret_cast<int*>(p.C + 256)
                                     : reinterpret_cast<int*>(p.C + 256 * p.ldc);
-    int t = blockIdx.x;
+    int t = SK ? 0 : blockIdx.x;
     if (dyn) {
         if (tid == 0) s_item = atomicAdd(ctr, 1);
         __syncthreads();
         t = s_item;
     }
-    if (t >= p.num_tiles) return;
+    if (!SK && t >= p.num_tiles) return;
     TileWork cur = decode(t);
+    if (SK && !cur.compute) return;
+    // stream-K: this workgroup's workspace slot (tile-local, BM x BN)
+    float* const sk_slot =
+        SK ? p.ws + (int64_t)xcd_remap(blockIdx.x, gridDim.x) * (T::BM * T::BN) : nullptr;
     int it = 0;
     set_offsets(cur);
     issue(cur, 0, sA0, sB0);
@@ -555,13 +584,18 @@ __global__ void __launch_bounds__(T::NT)
             if (dyn && it == cur.nk - 2 && tid == 0) s_item = atomicAdd(ctr, 1);
         }
         if (last) {
-            nt = dyn ? s_item : t + gridDim.x;
-            has_next = nt < p.num_tiles;
-            nit = has_next ? 0 : it;
-            if (has_next) {
-                nw = decode(nt);
-                set_offsets(nw);
+            if constexpr (SK) {
+                nt = t + 1;
+                const TileWork cand = decode(nt);
+                has_next = cand.compute != 0;
+                if (has_next) nw = cand;
+            } else {
+                nt = dyn ? s_item : t + gridDim.x;
+                has_next = nt < p.num_tiles;
+                if (has_next) nw = decode(nt);
             }
+            nit = has_next ? 0 : it;
+            if (has_next) set_offsets(nw);
         }
         // (the scheduling barriers keep the loads ahead of the MFMAs: the
         // scheduler would sink them to the barrier, exposing their latency)
@@ -581,7 +615,11 @@ __global__ void __launch_bounds__(T::NT)
             ++it;
             return false;
         }
-        store_tile_direct<T, !A_KC, !B_KC, BIAS, MODE>(p, C, ldc, c_vec, cur, acc, wm, wn, lane);
+        if (SK && cur.mirror)
+            store_tile_direct<T, !A_KC, !B_KC, BIAS, MODE, true>(p, sk_slot, T::BN, true, cur, acc,
+                                                                 wm, wn, lane);
+        else
+            store_tile_direct<T, !A_KC, !B_KC, BIAS, MODE>(p, C, ldc, c_vec, cur, acc, wm, wn, lane);
 #pragma unroll
         for (int i = 0; i < T::TM; ++i)
 #pragma unroll
@@ -598,48 +636,6 @@ __global__ void __launch_bounds__(T::NT)
         if (slice(std::integral_constant<int, 0>{})) break;
         if (slice(std::integral_constant<int, 1>{})) break;
     }
-}
-
-// Launches of the 256 tile on dense problems with every slice full (K and
-// the split chunk multiples of 32) and 16-byte operands take direct staging
-// when each split is deep enough.  Measured against the register-staged
-// kernel (same process, interleaved, MI355X): direct wins on every layout
-// from K = 512 per split (8192^3: +3-6 %; 8192^2 x 512: +2-5 %); at K = 256
-// N/N still wins (65536 x 512 x 256: +3 %, 8192^2 x 256: +5 %) but the other
-// layouts lose up to 6 % (65536 x 512 x 256 T/T).  The 128 tile (16-deep
-// slices) takes it at any depth with K and the chunk multiples of 16 (it won
-// on every shape measured, K = 96 ... 3072).
-
-inline bool direct_ok(const GemmLaunch& g) {
-    if (g.structure != kDense || g.vec != 4) return false;
-    if (g.cfg == kCfg256) {
-        // byte offsets within a slice (256 rows of a K-contiguous operand, 32
-        // rows of an MN-contiguous one) fit 32 bits
-        const int64_t lim_a = g.op_a == 0 ? (INT64_C(1) << 21) : (INT64_C(1) << 24);
-        const int64_t lim_b = g.op_b != 0 ? (INT64_C(1) << 21) : (INT64_C(1) << 24);
-        const int64_t min_chunk = (g.op_a == 0 && g.op_b == 0) ? 256 : 512;
-        return g.K % 32 == 0 && g.k_chunk % 32 == 0 && g.k_chunk >= min_chunk &&
-               g.lda <= lim_a && g.ldb <= lim_b;
-    }
-    if (g.cfg == kCfg128) {
-        // 128 rows of a K-contiguous operand, 16 rows of an MN-contiguous one
-        const int64_t lim_a = g.op_a == 0 ? (INT64_C(1) << 22) : (INT64_C(1) << 25);
-        const int64_t lim_b = g.op_b != 0 ? (INT64_C(1) << 22) : (INT64_C(1) << 25);
-        return g.K % 16 == 0 && g.k_chunk % 16 == 0 && g.lda <= lim_a && g.ldb <= lim_b;
-    }
-    return false;
-}
-
-// Dense 128-tile launches the 16-byte path cannot take (operands not 16-byte
-// aligned, or K not a multiple of 16) stage with 4-byte direct loads; only
-// the last slice of each K range may be partial (the split chunk is a
-// multiple of 16).  (The 256 tile with 4-byte loads needs 16 offset VGPRs
-// per operand and spilled.)
-inline bool direct4_ok(const GemmLaunch& g) {
-    const int64_t lim_a = g.op_a == 0 ? (INT64_C(1) << 22) : (INT64_C(1) << 25);
-    const int64_t lim_b = g.op_b != 0 ? (INT64_C(1) << 22) : (INT64_C(1) << 25);
-    return g.cfg == kCfg128 && g.structure == kDense && !direct_ok(g) && g.K > 0 &&
-           g.k_chunk % 16 == 0 && g.lda <= lim_a && g.ldb <= lim_b;
 }
 
 // Triangular N/N products on the chunked work list (the scheduler plans it
@@ -671,6 +667,15 @@ template <class T, bool AT, bool BT, int VB>
 inline hipError_t launch_direct_tile(const GemmLaunch& g, hipStream_t s) {
     const GemmParams p = make_params(g);
     dim3 grid((unsigned)g.grid_x, (unsigned)g.split_k, (unsigned)g.batch);
+    if constexpr (VB == 16) {
+        if (g.sk_tiles > 0) {  // stream-K (the scheduler plans it for batch 1, split 1, no bias)
+            hipLaunchKernelGGL((gemm_f32_direct_kernel<T, AT, BT, false, kDense, 16, true>),
+                               dim3((unsigned)g.grid_x), dim3(T::NT), 0, s, p);
+            const hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+            return launch_sk_fixup(g, s);
+        }
+    }
     if constexpr (!AT && !BT) {  // the row bias exists for N/N only
         if (g.bias != nullptr && g.split_k == 1) {
             hipLaunchKernelGGL((gemm_f32_direct_kernel<T, false, false, true, kDense, VB>), grid,

@@ -431,6 +431,9 @@ inline GemmParams make_params(const GemmLaunch& g) {
     p.num_tiles = g.num_tiles;
     p.col_splits = g.col_splits;
     p.tri_cap = g.tri_cap;
+    p.sk_dp = g.sk_dp;
+    p.sk_tiles = g.sk_tiles;
+    p.sk_ipt = g.sk_ipt;
     p.ws_batch_stride = (int64_t)g.M * g.N;
     p.ws_split_stride = p.ws_batch_stride * g.batch;
     return p;

@@ -128,6 +128,79 @@ __host__ __device__ __forceinline__ void tri_item(int pid, int nt, int cap, bool
     u1 = u0 + len;
 }
 
+// Stream-K schedule (dense products on a persistent grid of G workgroups).
+// The T output tiles of one product, in raster order, are split into n_dp
+// data-parallel tiles (a multiple of G: whole waves, each tile reduced by one
+// workgroup) followed by S = T - n_dp stream-K tiles, whose S * ipt K-slices
+// (ipt slices per tile) are dealt out as G contiguous, equal ranges:
+// logical workgroup lg (= xcd_remap of its hardware index, so the ranges of
+// one XCD are neighbours in the raster) takes slices
+// [sk_begin(lg), sk_begin(lg + 1)).  A range may start inside a tile only
+// once, at its first slice, so every workgroup produces at most one partial
+// tile that does not start at k = 0: it goes to workspace slot lg; every
+// segment that starts at k = 0 (a whole tile, or the head of a split one) is
+// written to C.  sk_fixup then adds the slots of each split tile into C in
+// increasing lg order (increasing k): a fixed order, so results are
+// deterministic.  Slices are indexed with 64-bit integers (S * ipt * G can
+// pass 2^31).
+__host__ __device__ __forceinline__ int64_t sk_begin(int64_t lg, int64_t iters, int G) {
+    return lg * iters / G;
+}
+
+// Logical workgroup whose range holds slice x (the largest lg with
+// sk_begin(lg) <= x).
+__host__ __device__ __forceinline__ int64_t sk_owner(int64_t x, int64_t iters, int G) {
+    return ((x + 1) * G - 1) / iters;
+}
+
+// Work item `item` of hardware workgroup b: first its n_dp / G data-parallel
+// tiles (walk index b + i G, placed by xcd_remap over n_dp), then the
+// segments of its stream-K range, one per tile it touches.  Returns false
+// past its last item; else the logical tile index lt (raster position), the
+// slice range [s0, s1) within that tile and whether the partial goes to the
+// workspace (slot = logical workgroup).
+__host__ __device__ __forceinline__ bool sk_work(int b, int item, int G, int n_dp, int64_t S,
+                                                 int ipt, int& lt, int& s0, int& s1, int& to_ws) {
+    const int dp_items = n_dp / G;
+    if (item < dp_items) {
+        lt = xcd_remap(b + item * G, n_dp);
+        s0 = 0;
+        s1 = ipt;
+        to_ws = 0;
+        return true;
+    }
+    const int j = item - dp_items;
+    const int64_t iters = S * ipt;
+    const int lg = xcd_remap(b, G);
+    const int64_t beg = sk_begin(lg, iters, G), end = sk_begin(lg + 1, iters, G);
+    int64_t x;
+    if (beg % ipt == 0) {
+        x = beg + (int64_t)j * ipt;
+    } else {
+        x = j == 0 ? beg : (beg / ipt + 1) * ipt + (int64_t)(j - 1) * ipt;
+    }
+    if (x >= end) return false;
+    const int64_t t = x / ipt;
+    const int64_t xe = end < (t + 1) * ipt ? end : (t + 1) * ipt;
+    lt = n_dp + (int)t;
+    s0 = (int)(x - t * ipt);
+    s1 = (int)(xe - t * ipt);
+    to_ws = s0 != 0;
+    return true;
+}
+
+// Workspace slots holding the partials of stream-K tile t (0 <= t < S), in
+// the order they are added: [first, first + count), count 0 when one
+// workgroup reduced the whole tile.
+__host__ __device__ __forceinline__ void sk_fixup_slots(int64_t t, int64_t S, int ipt, int G,
+                                                        int64_t& first, int64_t& count) {
+    const int64_t iters = S * ipt;
+    const int64_t head = sk_owner(t * ipt, iters, G);
+    const int64_t last = sk_owner((t + 1) * ipt - 1, iters, G);
+    first = head + 1;
+    count = last - head;
+}
+
 __device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
     uint64_t z = x + 0x9E3779B97F4A7C15ULL;
     z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;

@@ -65,7 +65,54 @@ struct GemmLaunch {
     int grid_x;           // workgroups per (split, batch), <= num_tiles; each walks its tiles
     int col_splits;       // panel configs: column runs per A row panel
     int tri_cap;          // > 0: chunked triangular work list (tri_item) of the direct kernel
+    // stream-K (sk_tiles > 0; direct-staged 128 / 256 tiles, batch 1, split 1):
+    // the first sk_dp tiles data-parallel, the last sk_tiles dealt out as
+    // K-slices (sk_ipt per tile) over the grid_x workgroups (sk_work); the
+    // workspace holds grid_x partial tiles, added in by sk_fixup
+    int sk_dp, sk_tiles, sk_ipt;
 };
+
+// Direct global -> LDS staging (gemm_direct.hpp) takes launches of the 256
+// tile on dense problems with every slice full (K and the split chunk
+// multiples of 32) and 16-byte operands when each split is deep enough.
+// Measured against the register-staged kernel (same process, interleaved,
+// MI355X): direct wins on every layout from K = 512 per split (8192^3:
+// +3-6 %; 8192^2 x 512: +2-5 %); at K = 256 N/N still wins (65536 x 512 x 256:
+// +3 %, 8192^2 x 256: +5 %) but the other layouts lose up to 6 %
+// (65536 x 512 x 256 T/T).  The 128 tile (16-deep slices) takes it at any
+// depth with K and the chunk multiples of 16 (it won on every shape
+// measured, K = 96 ... 3072).
+inline bool direct_ok(const GemmLaunch& g) {
+    if (g.structure != 0 || g.vec != 4) return false;
+    if (g.cfg == kCfg256) {
+        // byte offsets within a slice (256 rows of a K-contiguous operand, 32
+        // rows of an MN-contiguous one) fit 32 bits
+        const int64_t lim_a = g.op_a == 0 ? (INT64_C(1) << 21) : (INT64_C(1) << 24);
+        const int64_t lim_b = g.op_b != 0 ? (INT64_C(1) << 21) : (INT64_C(1) << 24);
+        const int64_t min_chunk = (g.op_a == 0 && g.op_b == 0) ? 256 : 512;
+        return g.K % 32 == 0 && g.k_chunk % 32 == 0 && g.k_chunk >= min_chunk &&
+               g.lda <= lim_a && g.ldb <= lim_b;
+    }
+    if (g.cfg == kCfg128) {
+        // 128 rows of a K-contiguous operand, 16 rows of an MN-contiguous one
+        const int64_t lim_a = g.op_a == 0 ? (INT64_C(1) << 22) : (INT64_C(1) << 25);
+        const int64_t lim_b = g.op_b != 0 ? (INT64_C(1) << 22) : (INT64_C(1) << 25);
+        return g.K % 16 == 0 && g.k_chunk % 16 == 0 && g.lda <= lim_a && g.ldb <= lim_b;
+    }
+    return false;
+}
+
+// Dense 128-tile launches the 16-byte path cannot take (operands not 16-byte
+// aligned, or K not a multiple of 16) stage with 4-byte direct loads; only
+// the last slice of each K range may be partial (the split chunk is a
+// multiple of 16).  (The 256 tile with 4-byte loads needs 16 offset VGPRs
+// per operand and spilled.)
+inline bool direct4_ok(const GemmLaunch& g) {
+    const int64_t lim_a = g.op_a == 0 ? (INT64_C(1) << 22) : (INT64_C(1) << 25);
+    const int64_t lim_b = g.op_b != 0 ? (INT64_C(1) << 22) : (INT64_C(1) << 25);
+    return g.cfg == kCfg128 && g.structure == 0 && !direct_ok(g) && g.K > 0 &&
+           g.k_chunk % 16 == 0 && g.lda <= lim_a && g.ldb <= lim_b;
+}
 
 // Kernel-side parameter block (passed by value).
 struct GemmParams {
@@ -79,6 +126,7 @@ struct GemmParams {
     int num_tiles;
     int col_splits;
     int tri_cap;
+    int sk_dp, sk_tiles, sk_ipt;  // stream-K schedule (GemmLaunch)
     int k_chunk, split_k;
     int64_t lda, ldb, ldc;
     int64_t sa, sb, sc;
@@ -91,6 +139,9 @@ hipError_t launch_gemm_tn(const GemmLaunch& g, hipStream_t s);
 hipError_t launch_gemm_nt(const GemmLaunch& g, hipStream_t s);
 hipError_t launch_gemm_tt(const GemmLaunch& g, hipStream_t s);
 
+// After a stream-K launch: adds each split tile's workspace partials into C
+// in slot order (sk_fixup_slots).
+hipError_t launch_sk_fixup(const GemmLaunch& g, hipStream_t s);
 hipError_t launch_splitk_reduce(const float* ws, float* C, int M, int N, int batch, int split_k,
                                 int64_t ldc, int64_t sc, const float* bias, hipStream_t s);
 // After the chunked triangular direct kernel: for every tile of the zero

@@ -46,6 +46,13 @@ constexpr CfgModel kModels[] = {
 constexpr double kPeakFlopsPerCuNs = 256.0 * 2.4;  // fp32 MFMA flop per ns per CU
 constexpr double kHbmBytesPerNs = 8000.0;
 constexpr double kWriteBytesPerNs = 5500.0;        // sustained write-only bandwidth (measured)
+// Stream-K: MFMA efficiency relative to whole tiles (segment starts and ends
+// inside the K loop), and the fixup launch.  Fitted to MI355X timings of
+// forced stream-K against the data-parallel plans: it must rank 6144^3 and
+// 5376^3 below the data-parallel 128 tile (147.1 vs 144.7, 145.6 vs 142.9
+// TFLOP/s) and 7168^2 x 4096 above it (143.8 vs 138.1): 0.884 < f < 0.926.
+constexpr double kSkEfficiency = 0.91;
+constexpr double kSkFixupNs = 4000.0;
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
@@ -107,12 +114,66 @@ int validate_shape(const mi_gemm_args& a) {
     return MI_OK;
 }
 
+namespace {
+
+// Stream-K schedule of a dense product on config cfg (sk_work in
+// mi_device.hpp), or sk.tiles = 0 where it does not apply: batch 1, no bias,
+// the direct-staged 16-byte kernel (every K-slice full), a tile count that
+// whole waves of the persistent grid do not cover exactly, at least two
+// slices per workgroup, and a workspace for one partial tile per workgroup.
+struct SkChoice {
+    int dp = 0, tiles = 0, ipt = 0, grid = 0;
+    size_t ws = 0;
+};
+
+SkChoice plan_stream_k(const mi_gemm_args& a, int cfg, int num_cus) {
+    SkChoice sk;
+    if (cfg != kCfg256 && cfg != kCfg128) return sk;
+    if (a.structure != MI_DENSE || a.batch > 1 || a.bias_m != nullptr) return sk;
+    if (((uintptr_t)a.workspace & 15u) != 0) return sk;
+    const CfgInfo ci = cfg_info(cfg);
+    GemmLaunch g{};
+    g.structure = 0;
+    g.vec = choose_vec(a);
+    g.cfg = cfg;
+    g.K = (int)a.K;
+    g.k_chunk = (int)a.K;
+    g.op_a = a.op_a;
+    g.op_b = a.op_b;
+    g.lda = a.lda;
+    g.ldb = a.ldb;
+    if (a.K <= 0 || !direct_ok(g)) return sk;
+    const int64_t T = cdiv(a.M, ci.bm) * cdiv(a.N, ci.bn);
+    const int64_t G = (int64_t)num_cus * resident_wgs(cfg);
+    if (G % 8 != 0 || T % G == 0) return sk;
+    const int64_t waves = T / G;
+    const int64_t dp = waves >= 1 ? (waves - 1) * G : 0;
+    const int64_t S = T - dp;
+    const int64_t ipt = a.K / ci.bk;
+    if (S * ipt < 2 * G || T > INT32_MAX) return sk;
+    const size_t need = (size_t)G * ci.bm * ci.bn * sizeof(float);
+    if (a.workspace_bytes < need) return sk;
+    sk.dp = (int)dp;
+    sk.tiles = (int)S;
+    sk.ipt = (int)ipt;
+    sk.grid = (int)G;
+    sk.ws = need;
+    return sk;
+}
+
+}  // namespace
+
 int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* launch) {
     int rc = validate_shape(a);
     if (rc != MI_OK) return rc;
     if (num_cus <= 0) num_cus = 256;
 
     int best_cfg = kCfg128, best_split = 1;
+    SkChoice best_sk;
+    // plan_override bit 4: take stream-K on the override config where it
+    // applies; bit 5: never take stream-K
+    const bool force_sk = (a.plan_override & 0x10) != 0;
+    const bool no_sk = (a.plan_override & 0x20) != 0;
     const int override_cfg = a.plan_override & 0xF;
     const int override_split = (a.plan_override >> 8) & 0xFFF;
     const int override_group = (a.plan_override >> 20) & 0x7FF;
@@ -149,6 +210,10 @@ int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
     } else if (override_ok) {
         best_cfg = override_cfg;
         best_split = is_panel_cfg(override_cfg) ? 1 : std::max(1, override_split);
+        if (force_sk && !no_sk) {
+            best_sk = plan_stream_k(a, override_cfg, num_cus);
+            if (best_sk.tiles > 0) best_split = 1;
+        }
     } else if (a.K <= 64 && a.M % 128 == 0 && a.M % 256 != 0 && a.M < 2048 &&
                cdiv(a.M, 128) * cdiv(a.N, 128) * std::max<int64_t>(1, a.batch) >=
                    2 * (int64_t)num_cus) {
@@ -209,6 +274,26 @@ int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
                     best_t = t;
                     best_cfg = m.id;
                     best_split = s;
+                    best_sk = SkChoice{};
+                }
+            }
+            // Stream-K on this config: the same MFMA work spread evenly over the
+            // workgroups (no wave quantisation), plus one extra partial-tile
+            // store per workgroup and the fixup pass (read the partials, read
+            // and write the split tiles of C; one more launch).
+            const SkChoice sk = no_sk ? SkChoice{} : plan_stream_k(a, m.id, num_cus);
+            if (sk.tiles > 0) {
+                const double tile_bytes = 4.0 * ci.bm * ci.bn;
+                const double t_mfma = (double)tiles * 2.0 * ci.bm * ci.bn * (double)a.K /
+                                      num_cus / (eff * kSkEfficiency * kPeakFlopsPerCuNs);
+                const double t_store = (out_bytes + sk.grid * tile_bytes) / kWriteBytesPerNs;
+                double t = std::max(t_mfma, t_store) + (1.0 - m.overlap) * std::min(t_mfma, t_store);
+                t += 3.0 * sk.grid * tile_bytes / kHbmBytesPerNs + kSkFixupNs;
+                if (t < best_t * 0.999) {
+                    best_t = t;
+                    best_cfg = m.id;
+                    best_split = 1;
+                    best_sk = sk;
                 }
             }
         }
@@ -246,6 +331,9 @@ int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
         col_splits = std::min<int64_t>(tiles_n, std::max<int64_t>(1, cdiv(slots, tiles_m * batch)));
         grid = std::min<int64_t>(tiles_m * col_splits, std::max<int64_t>(1, slots / batch));
     }
+    // Stream-K: every resident workgroup takes part (its K-slice range),
+    // whatever the tile count.
+    if (best_sk.tiles > 0) grid = best_sk.grid;
 
     out.plan_id = best_cfg;
     out.block_m = ci.bm;
@@ -260,7 +348,9 @@ int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
     out.num_tiles = num_tiles;
     out.grid = grid;
     out.workspace_bytes =
-        best_split > 1 ? (size_t)best_split * batch * a.M * a.N * sizeof(float) : 0;
+        best_split > 1 ? (size_t)best_split * batch * a.M * a.N * sizeof(float) : best_sk.ws;
+    out.stream_k = best_sk.tiles > 0 ? 1 : 0;
+    out.sk_tiles = best_sk.tiles;
 
     if (launch) {
         GemmLaunch& g = *launch;
@@ -293,6 +383,9 @@ int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
         g.col_splits = (int)col_splits;
         g.grid_x = (int)grid;
         g.tri_cap = tri_cap;
+        g.sk_dp = best_sk.dp;
+        g.sk_tiles = best_sk.tiles;
+        g.sk_ipt = best_sk.ipt;
     }
     return MI_OK;
 }

@@ -346,6 +346,71 @@ hipError_t launch_splitk_reduce(const float* ws, float* C, int M, int N, int bat
     return hipGetLastError();
 }
 
+// Stream-K fixup: one workgroup per (stream-K tile, band of rows).  The tile's
+// head segment (k from 0) is already in C; the partials of the workgroups
+// whose K-slice ranges start inside the tile sit in their workspace slots
+// (tile-local, bm x bn) and are added in slot order, i.e. in k order -- a
+// fixed order, so the result is the same on every call.  A slot whose
+// workgroup had an empty range holds nothing and is skipped.
+template <bool VEC>
+__global__ void __launch_bounds__(256)
+    sk_fixup_kernel(float* __restrict__ C, const float* __restrict__ ws, int64_t ldc, int M, int N,
+                    int bm, int bn, int tiles_m, int tiles_n, int group_m, int n_dp, int S, int ipt,
+                    int G, int band_rows) {
+    const int t = blockIdx.x;
+    int64_t first, count;
+    sk_fixup_slots(t, S, ipt, G, first, count);
+    if (count == 0) return;
+    const int64_t iters = (int64_t)S * ipt;
+    int tm, tn;
+    raster(n_dp + t, tiles_m, tiles_n, group_m, tm, tn);
+    constexpr int W = VEC ? 4 : 1;
+    const int per_row = bn / W;
+    const int r0 = (int)blockIdx.y * band_rows;
+    const int64_t slot_elems = (int64_t)bm * bn;
+    for (int e = threadIdx.x; e < band_rows * per_row; e += 256) {
+        const int r = r0 + e / per_row, c = (e % per_row) * W;
+        const int row = tm * bm + r, col = tn * bn + c;
+        if (row >= M || col >= N) continue;
+        float* const dst = C + (int64_t)row * ldc + col;
+        const float* const src = ws + (int64_t)r * bn + c;
+        if constexpr (VEC) {
+            f4 v = *reinterpret_cast<const f4*>(dst);
+            for (int64_t q = 0; q < count; ++q) {
+                const int64_t lg = first + q;
+                if (sk_begin(lg + 1, iters, G) == sk_begin(lg, iters, G)) continue;
+                v += *reinterpret_cast<const f4*>(src + lg * slot_elems);
+            }
+            *reinterpret_cast<f4*>(dst) = v;
+        } else {
+            float v = *dst;
+            for (int64_t q = 0; q < count; ++q) {
+                const int64_t lg = first + q;
+                if (sk_begin(lg + 1, iters, G) == sk_begin(lg, iters, G)) continue;
+                v += src[lg * slot_elems];
+            }
+            *dst = v;
+        }
+    }
+}
+
+hipError_t launch_sk_fixup(const GemmLaunch& g, hipStream_t s) {
+    const CfgInfo ci = cfg_info(g.cfg);
+    const int band_rows = 4096 / ci.bn;  // 4096 floats of C per workgroup
+    const dim3 grid((unsigned)g.sk_tiles, (unsigned)(ci.bm / band_rows));
+    const bool vec = g.N % 4 == 0 && g.ldc % 4 == 0 && ((uintptr_t)g.C & 15u) == 0 &&
+                     ((uintptr_t)g.ws & 15u) == 0;
+    if (vec)
+        hipLaunchKernelGGL(sk_fixup_kernel<true>, grid, dim3(256), 0, s, g.C, g.ws, g.ldc, g.M, g.N,
+                           ci.bm, ci.bn, g.tiles_m, g.tiles_n, g.group_m, g.sk_dp, g.sk_tiles,
+                           g.sk_ipt, g.grid_x, band_rows);
+    else
+        hipLaunchKernelGGL(sk_fixup_kernel<false>, grid, dim3(256), 0, s, g.C, g.ws, g.ldc, g.M, g.N,
+                           ci.bm, ci.bn, g.tiles_m, g.tiles_n, g.group_m, g.sk_dp, g.sk_tiles,
+                           g.sk_ipt, g.grid_x, band_rows);
+    return hipGetLastError();
+}
+
 __global__ void fill_zero_kernel(float* __restrict__ C, int64_t rows, int64_t cols, int64_t ld,
                                  int64_t batch_stride, const float* __restrict__ bias) {
     const int64_t per = rows * cols;

@@ -105,9 +105,26 @@ typedef struct {
     int32_t group_m;        /* tile rows per raster group */
     int64_t num_tiles;      /* output tiles per (split, batch) */
     int64_t grid;           /* workgroups launched per (split, batch); each walks tiles
-                               wg, wg + grid, ... (persistent) */
-    size_t workspace_bytes; /* split-K partial tiles */
+                               wg, wg + grid, ... (persistent; stream-K plans: see
+                               mi_gemm_work_item) */
+    size_t workspace_bytes; /* split-K partial tiles, or one stream-K partial tile per
+                               workgroup */
+    int32_t stream_k;       /* 1: stream-K schedule -- the last sk_tiles tiles' K-slices
+                               are dealt out evenly over the grid workgroups (the
+                               first num_tiles - sk_tiles tiles stay whole), partial
+                               tiles are added in by a fixed-order fixup pass */
+    int64_t sk_tiles;
 } mi_plan;
+
+/* One work item of a workgroup under a plan (host introspection). */
+typedef struct {
+    int32_t tile_m, tile_n; /* output tile */
+    int64_t k_begin, k_end; /* K range it reduces */
+    int32_t dest;           /* 0: written to C (a whole tile, or the k = 0 head of a
+                               stream-K tile); 1: written to workspace slot `slot`
+                               (a split-K split, or a stream-K partial tile) */
+    int32_t slot;
+} mi_work_item;
 
 MI_API int mi_gemm_f32(const mi_gemm_args* args, void* stream);
 MI_API size_t mi_gemm_workspace_bytes(const mi_gemm_args* args);
@@ -147,6 +164,26 @@ MI_API int mi_gemm_plan(const mi_gemm_args* args, int32_t num_cus, mi_plan* out)
  * negative mi_status on error. */
 MI_API int mi_gemm_tile_of(const mi_gemm_args* args, int32_t num_cus, int64_t item, int32_t split,
                            int32_t* tile_m, int32_t* tile_n, int64_t* k_begin, int64_t* k_end);
+
+/* Scheduler introspection for dense persistent plans, stream-K included (no
+ * reference counterpart; for tests and tuning): work item `item` (0, 1, ...
+ * in the order it runs) of workgroup wg (0 <= wg < mi_plan.grid) of split
+ * `split`.  Returns 1 and fills *out, 0 when the workgroup has no such item,
+ * MI_ERR_BAD_LAYOUT for triangular and A-panel plans (mi_gemm_tile_of covers
+ * those), another negative mi_status on error. */
+MI_API int mi_gemm_work_item(const mi_gemm_args* args, int32_t num_cus, int64_t wg, int32_t split,
+                             int64_t item, mi_work_item* out);
+
+/* Stream-K fixup (no reference counterpart; for tests and tuning): stream-K
+ * tile t (0 <= t < mi_plan.sk_tiles) is output tile (tile_m, tile_n); the
+ * fixup pass adds workspace slots first_slot, first_slot + 1, ...,
+ * first_slot + n_slots - 1 into it, in that order (n_slots = 0: one
+ * workgroup reduced the whole tile).  A slot whose workgroup got no K-slices
+ * holds nothing and is skipped.  Returns 1, or a negative mi_status (also for
+ * a plan that is not stream-K). */
+MI_API int mi_gemm_sk_fixup_of(const mi_gemm_args* args, int32_t num_cus, int64_t t,
+                               int32_t* tile_m, int32_t* tile_n, int64_t* first_slot,
+                               int64_t* n_slots);
 
 /* ---- one entry point per reference operator ------------------------------ */
 

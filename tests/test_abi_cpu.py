@@ -33,6 +33,7 @@ def test_every_named_entry_point_cites_a_reference_file():
         parts = txt[:txt.index(n + "(")].rsplit(");", 2)
         block = parts[-1] if "/*" in parts[-1] else parts[-2] + parts[-1]  # shared comment
         if n in ("mi_gemm_f32", "mi_gemm_workspace_bytes", "mi_gemm_plan", "mi_gemm_tile_of",
+                 "mi_gemm_work_item", "mi_gemm_sk_fixup_of",
                  "mi_fill_uniform_f32", "mi_status_string", "mi_version"):
             continue
         if n == "mi_gemm_f32_noalloc":   # says it has none, and whom it is for
@@ -100,12 +101,17 @@ def test_plan_is_sane(ck, M, N, K, batch):
     assert p.tiles_n * p.block_n >= N > (p.tiles_n - 1) * p.block_n
     assert p.num_tiles == p.tiles_m * p.tiles_n
     # persistent grid: no more workgroups than tiles, a multiple of the 8 XCDs
-    # unless the tiles run out first
-    assert 1 <= p.grid <= p.num_tiles
+    # unless the tiles run out first (stream-K: every resident workgroup)
+    assert 1 <= p.grid <= p.num_tiles or p.stream_k
     if p.plan_id not in (6, 7, 8):  # panel plans size the grid by row panels x column runs
         assert p.grid % 8 == 0 or p.grid == p.num_tiles
     assert p.k_chunk % p.block_k == 0
     assert p.k_chunk * p.split_k >= K > p.k_chunk * (p.split_k - 1)
+    if p.stream_k:
+        # every resident workgroup takes a K-slice range; one partial tile each
+        assert p.split_k == 1 and p.grid % 8 == 0 and 0 < p.sk_tiles <= p.num_tiles
+        assert p.workspace_bytes == p.grid * p.block_m * p.block_n * 4
+        return
     want_ws = p.split_k * batch * M * N * 4 if p.split_k > 1 else 0
     assert p.workspace_bytes == want_ws
     # without a workspace the scheduler never plans a split
@@ -158,7 +164,7 @@ def test_plan_shallow_k_takes_the_128_tile(ck, M, N, K, want):
 def test_plan_splits_by_per_cu_load(ck, M, N, K, split):
     """Splits are priced by the most loaded CU's share of K, up to twice the
     CUs in items, not stopped at the first split that covers every CU."""
-    rc, p = ck.abi.plan(M, N, K, workspace_bytes=1 << 30)
+    rc, p = ck.abi.plan(M, N, K, workspace_bytes=1 << 30, plan_override=0x20)  # no stream-K
     assert rc == 0 and p.plan_id == 2 and p.split_k == split, (M, N, K, p.plan_id, p.split_k)
 
 
@@ -331,3 +337,150 @@ def test_symmetric_structure_is_the_nn_dense_plan(ck):
     rc2, pd = ck.abi.plan(4096, 4096, 4096)
     assert rc == rc2 == 0
     assert (ps.plan_id, ps.grid, ps.split_k, ps.tiles_m) == (pd.plan_id, pd.grid, pd.split_k, pd.tiles_m)
+
+
+# ---- stream-K -------------------------------------------------------------------
+
+SK_FORCE = 0x10
+SK_NEVER = 0x20
+
+
+def _sk_cover(ck, args, num_cus=256):
+    """Enumerate every workgroup's items under a stream-K plan and check the
+    schedule: each output tile's K range is covered exactly once, in whole
+    slices; the segment that starts at k = 0 is written to C and every other
+    segment to its workgroup's own slot (one per workgroup); the data-parallel
+    tiles come whole; the fixup adds exactly a tile's slot segments, in k order."""
+    rc, p = ck.abi.plan(args.M, args.N, args.K, num_cus=num_cus, op_a=args.op_a, op_b=args.op_b,
+                        workspace_bytes=args.workspace_bytes, plan_override=args.plan_override)
+    assert rc == 0 and p.stream_k == 1 and p.split_k == 1
+    K, bk = args.K, p.block_k
+    segs = {}
+    slots_used = {}
+    for wg in range(p.grid):
+        items = ck.abi.work_items(args, wg, 0, num_cus)
+        n_ws = 0
+        for tm, tn, kb, ke, dest, slot in items:
+            assert 0 <= tm < p.tiles_m and 0 <= tn < p.tiles_n
+            assert 0 <= kb < ke <= K and kb % bk == 0 and ke % bk == 0
+            assert dest == (1 if kb > 0 else 0), "k = 0 heads go to C, the rest to the workspace"
+            if dest:
+                n_ws += 1
+                assert slot not in slots_used, "one partial tile per workspace slot"
+                slots_used[slot] = (tm, tn, kb, ke)
+                assert 0 <= slot < p.grid
+            segs.setdefault((tm, tn), []).append((kb, ke, dest, slot))
+        assert n_ws <= 1, "a workgroup's range starts inside a tile at most once"
+    assert set(segs) == {(i, j) for i in range(p.tiles_m) for j in range(p.tiles_n)}
+    for tile, parts in segs.items():
+        parts.sort()
+        pos = 0
+        for kb, ke, _, _ in parts:      # exact partition of [0, K)
+            assert kb == pos
+            pos = ke
+        assert pos == K, (tile, parts)
+    # the fixup pass: each stream-K tile's slots, in k order, and nothing else
+    fixed = set()
+    for t in range(p.sk_tiles):
+        rc, tm, tn, first, n = ck.abi.sk_fixup_of(args, t, num_cus)
+        assert rc == 1
+        fixed.add((tm, tn))
+        want = [slot for kb, ke, dest, slot in segs[(tm, tn)] if dest == 1]
+        assert want == list(range(first, first + n)), ((tm, tn), want, first, n)
+    split_tiles = {tile for tile, parts in segs.items() if len(parts) > 1}
+    assert split_tiles <= fixed
+    # data-parallel tiles are whole: the first num_tiles - sk_tiles of the raster
+    assert len(fixed) == p.sk_tiles
+    whole = [tile for tile, parts in segs.items() if tile not in fixed]
+    assert len(whole) == p.num_tiles - p.sk_tiles
+    assert all(segs[t] == [(0, K, 0, 0)] for t in whole)
+    return p, segs
+
+
+@pytest.mark.parametrize("M,N,K,cfg,ops", [
+    (5120, 5120, 8192, 3, (0, 0)),    # 400 tiles on 256 workgroups
+    (3584, 3584, 3584, 3, (1, 0)),    # 196 tiles < 256: every tile stream-K
+    (3072, 3072, 3072, 2, (0, 1)),    # 128 tile, 576 tiles on 768 workgroups
+    (6400, 4608, 2048, 2, (1, 1)),    # 1800 tiles: one data-parallel wave, then 1032 stream-K
+    (1024, 1024, 1024, 2, (0, 0)),    # 64 tiles over 768 workgroups: many segments per tile
+    (1000, 1000, 4096, 3, (0, 1)),    # ragged edges
+    (33000, 1000, 1024, 2, (0, 0)),   # 2072 tiles
+])
+def test_stream_k_schedule_covers_every_tile_once(ck, M, N, K, cfg, ops):
+    args = ck.abi.make_args(M, N, K, op_a=ops[0], op_b=ops[1], workspace_bytes=1 << 40,
+                            plan_override=cfg | SK_FORCE)
+    p, segs = _sk_cover(ck, args)
+    T, G = p.num_tiles, p.grid
+    waves = T // G
+    assert p.sk_tiles == (T - (waves - 1) * G if waves >= 1 else T)
+    # balance: every workgroup reduces the same number of K-slices, +-1
+    per_wg = []
+    for wg in range(G):
+        per_wg.append(sum(ke - kb for _, _, kb, ke, _, _ in ck.abi.work_items(args, wg)) // p.block_k)
+    assert max(per_wg) - min(per_wg) <= 1
+
+
+def test_stream_k_applies_only_where_it_can(ck):
+    # whole waves (1024 tiles of 256 on 256 CUs), a batch, a bias, operands the
+    # direct kernel cannot stage, no workspace: no stream-K even when asked
+    for kw in [dict(M=8192, N=8192, K=8192), dict(M=2560, N=2560, K=2560, batch=2),
+               dict(M=2560, N=2560, K=2562), dict(M=2561, N=2561, K=2560)]:
+        rc, p = ck.abi.plan(workspace_bytes=1 << 40, plan_override=3 | SK_FORCE, **kw)
+        assert rc == 0 and p.stream_k == 0, kw
+    rc, p = ck.abi.plan(2560, 2560, 2560, workspace_bytes=0, plan_override=3 | SK_FORCE)
+    assert rc == 0 and p.stream_k == 0
+    # bit 5 keeps the cost model off stream-K
+    rc, p = ck.abi.plan(5120, 5120, 8192, workspace_bytes=1 << 40, plan_override=SK_NEVER)
+    assert rc == 0 and p.stream_k == 0
+    # the per-workgroup introspection refuses plans it does not describe
+    args = ck.abi.make_args(4096, 4096, 4096, structure=1)
+    w = ck.abi.WorkItem()
+    assert ck.abi.lib().mi_gemm_work_item(ctypes.byref(args), 256, 0, 0, 0, ctypes.byref(w)) == \
+        ck.abi.MI_ERR_BAD_LAYOUT
+
+
+@pytest.mark.parametrize("M,N,K", [(1000, 700, 300), (4096, 256, 100000), (8192, 8192, 8192)])
+def test_work_items_of_persistent_plans_cover_every_tile(ck, M, N, K):
+    """mi_gemm_work_item on data-parallel and split-K plans: workgroup w runs
+    tiles w, w + grid, ...; together they cover every (tile, split) once."""
+    args = ck.abi.make_args(M, N, K, workspace_bytes=1 << 40, plan_override=SK_NEVER)
+    rc, p = ck.abi.plan(M, N, K, workspace_bytes=1 << 40, plan_override=SK_NEVER)
+    assert rc == 0 and not p.stream_k
+    seen = {}
+    for s in range(p.split_k):
+        for wg in range(p.grid):
+            for tm, tn, kb, ke, dest, slot in ck.abi.work_items(args, wg, s):
+                assert dest == (1 if p.split_k > 1 else 0) and slot == (s if dest else 0)
+                seen.setdefault((tm, tn), []).append((kb, ke))
+    assert len(seen) == p.tiles_m * p.tiles_n
+    for parts in seen.values():
+        assert len(parts) == p.split_k
+        assert sum(min(ke, K) - kb for kb, ke in parts if kb < K) == K
+
+
+@pytest.mark.parametrize("M,N,K,want", [
+    # measured on MI355X (TFLOP/s, best plan first): stream-K where whole waves
+    # of tiles quantise badly ...
+    (3072, 3072, 8192, (3, 1)),    # SK 256 140.6 / split 4 106.9
+    (5120, 5120, 8192, (3, 1)),    # SK 256 143.7 / data-parallel 128 130.0
+    (4608, 4608, 4608, (3, 1)),    # SK 256 140.6 / split 2 117.4
+    (3584, 3584, 3584, (3, 1)),    # SK 256 135.5 / data-parallel 256 113.9
+    (7168, 7168, 4096, (3, 1)),    # SK 256 143.8 / data-parallel 128 138.1
+    (1280, 1280, 8192, (None, 1)),  # SK 128 121.5, SK 256 116.8 / split 8 107.0
+    # ... and not where the data-parallel or split-K plan is faster
+    (6144, 6144, 6144, (2, 0)),    # data-parallel 128 (3 exact waves) 147.1 / SK 256 144.7
+    (5376, 5376, 5376, (2, 0)),    # data-parallel 128 145.6 / SK 256 142.9
+    (2048, 2048, 2048, (2, 0)),    # 123.8 / SK 128 120.3
+    (1024, 1024, 1024, (2, 0)),    # split 4 68.9 / SK 128 43.8
+    (1000, 1000, 8192, (2, 0)),    # split 4 112.6 / SK 128 107.5
+    (65536, 512, 256, (2, 0)),     # 129.3 / SK 128 106.7
+    (16384, 768, 2048, (2, 0)),    # 144.0 / SK 256 129.5
+    (4096, 4096, 1024, (3, 0)),    # 138.4 / SK 128 123.2
+    (2048, 8192, 4096, (3, 0)),    # one exact wave: 148.6
+    (8192, 8192, 8192, (3, 0)),
+])
+def test_plan_takes_stream_k_where_it_measured_faster(ck, M, N, K, want):
+    rc, p = ck.abi.plan(M, N, K, workspace_bytes=1 << 30)
+    cfg, sk = want
+    assert rc == 0 and p.stream_k == sk and (cfg is None or p.plan_id == cfg), \
+        (M, N, K, p.plan_id, p.split_k, p.stream_k)

@@ -1,0 +1,111 @@
+"""Stream-K schedule on the GPU, through the C ABI: parity with the fp64 oracle
+in every layout on both direct-staged tiles, tiles split over many workgroups
+and ragged edges, a data-parallel wave ahead of the stream-K tiles, bitwise
+repeatability (the fixup adds partials in a fixed order), and agreement with
+the data-parallel plan of the same problem.
+
+Bar: normalised max error <= 1e-4 against fp64; bitwise equality across runs.
+"""
+import numpy as np
+import pytest
+import torch
+
+import freivalds as fv
+from gpu_util import assert_close, gemm_args, run_gemm, to_dev, to_host, workspace
+
+pytestmark = pytest.mark.gpu
+
+SK_FORCE, SK_NEVER = 0x10, 0x20
+LAYOUTS = [(0, 0), (1, 0), (0, 1), (1, 1)]
+
+
+def _operands(orc, M, N, K, op_a, op_b, seed):
+    a_st = orc.uniform((K, M) if op_a else (M, K), seed)
+    b_st = orc.uniform((N, K) if op_b else (K, N), seed + 1)
+    return a_st, b_st, (a_st.T if op_a else a_st), (b_st.T if op_b else b_st)
+
+
+def _run(ck, A, B, M, N, K, op_a, op_b, override, fill=float("nan")):
+    C = torch.full((M, N), fill, device="cuda")
+    args = gemm_args(ck, A, B, C, M, N, K, op_a, op_b, override=override)
+    ws = workspace(ck, args)
+    args = gemm_args(ck, A, B, C, M, N, K, op_a, op_b, override=override, ws=ws)
+    ck.abi.check(run_gemm(ck, args), "mi_gemm_f32")
+    return C
+
+
+def _plan(ck, M, N, K, op_a, op_b, override):
+    rc, p = ck.abi.plan(M, N, K, op_a=op_a, op_b=op_b, workspace_bytes=1 << 40,
+                        plan_override=override)
+    assert rc == 0
+    return p
+
+
+@pytest.mark.parametrize("op_a,op_b", LAYOUTS)
+@pytest.mark.parametrize("M,N,K,cfg", [
+    (1280, 1280, 2048, 3),   # 25 tiles of 256 over 256 workgroups: ~10 segments per tile
+    (1000, 1000, 4096, 3),   # ragged edges on the 256 tile
+    (640, 640, 2048, 2),     # 25 tiles of 128 over 768 workgroups
+    (1000, 1100, 1024, 2),   # ragged edges on the 128 tile
+])
+def test_stream_k_parity(ck, orc, dev, op_a, op_b, M, N, K, cfg):
+    p = _plan(ck, M, N, K, op_a, op_b, cfg | SK_FORCE)
+    assert p.stream_k == 1 and p.plan_id == cfg
+    a_st, b_st, a, b = _operands(orc, M, N, K, op_a, op_b, seed=4100 + cfg)
+    A, B = to_dev(a_st), to_dev(b_st)
+    C = _run(ck, A, B, M, N, K, op_a, op_b, cfg | SK_FORCE)
+    assert_close(orc, to_host(C), orc.gemm(a, b), K, what=f"stream-K {op_a}{op_b} {M}x{N}x{K} cfg{cfg}")
+
+
+@pytest.mark.parametrize("M,N,K,cfg,ops", [
+    (5760, 5120, 256, 2, (0, 0)),    # 1800 tiles: one data-parallel wave (768) + 1032 stream-K
+    (5120, 5120, 2048, 3, (1, 1)),   # 400 tiles of 256: 1.56 tiles per workgroup
+    (3584, 3584, 1024, 3, (0, 1)),   # 196 tiles < 256 workgroups
+])
+def test_stream_k_larger_every_element(ck, orc, dev, M, N, K, cfg, ops):
+    """Bigger stream-K schedules, every element through fp64 row and column
+    checksums, plus exact fp64 rows."""
+    op_a, op_b = ops
+    p = _plan(ck, M, N, K, op_a, op_b, cfg | SK_FORCE)
+    assert p.stream_k == 1 and p.plan_id == cfg
+    a_st, b_st, a, b = _operands(orc, M, N, K, op_a, op_b, seed=4200 + cfg)
+    A, B = to_dev(a_st), to_dev(b_st)
+    Cd = _run(ck, A, B, M, N, K, op_a, op_b, cfg | SK_FORCE)
+    C = to_host(Cd)
+    rows = sorted({0, 1, 255, 256, 257, M // 2, M - 1})
+    assert_close(orc, C[rows], orc.gemm(a, b, rows=rows), K, what="stream-K rows")
+    v, u = fv.signs(N, 9), fv.signs(M, 10)
+    fv.check(orc, *orc.checksums(C, v, u), *fv.reference(orc, a, b, v, u), K, 1.0, 1.0,
+             f"stream-K {M}x{N}x{K} every element")
+
+
+@pytest.mark.parametrize("M,N,K,cfg", [(1280, 1280, 2048, 3), (640, 640, 2048, 2)])
+def test_stream_k_bitwise_repeatable(ck, orc, dev, M, N, K, cfg):
+    """20 runs, bitwise identical: every partial tile is added in slot order."""
+    a_st, b_st, _, _ = _operands(orc, M, N, K, 0, 0, seed=4300)
+    A, B = to_dev(a_st), to_dev(b_st)
+    first = to_host(_run(ck, A, B, M, N, K, 0, 0, cfg | SK_FORCE))
+    for _ in range(19):
+        np.testing.assert_array_equal(to_host(_run(ck, A, B, M, N, K, 0, 0, cfg | SK_FORCE)), first)
+
+
+@pytest.mark.parametrize("M,N,K,cfg", [(1280, 1280, 2048, 3), (640, 640, 2048, 2)])
+def test_stream_k_integer_inputs_exact(ck, orc, dev, M, N, K, cfg):
+    """Integer-valued inputs: every partial sum is an exact integer, so the
+    stream-K result equals the data-parallel one bit for bit."""
+    a = orc.integers((M, K), 4400)
+    b = orc.integers((K, N), 4401)
+    A, B = to_dev(a), to_dev(b)
+    sk = to_host(_run(ck, A, B, M, N, K, 0, 0, cfg | SK_FORCE))
+    dp = to_host(_run(ck, A, B, M, N, K, 0, 0, cfg | SK_NEVER))
+    np.testing.assert_array_equal(sk, dp)
+    np.testing.assert_array_equal(sk, (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float32))
+
+
+def test_stream_k_matches_data_parallel_within_tolerance(ck, orc, dev):
+    M, N, K = 1280, 1280, 2048
+    a_st, b_st, a, b = _operands(orc, M, N, K, 0, 0, seed=4500)
+    A, B = to_dev(a_st), to_dev(b_st)
+    sk = to_host(_run(ck, A, B, M, N, K, 0, 0, 3 | SK_FORCE))
+    dp = to_host(_run(ck, A, B, M, N, K, 0, 0, 3 | SK_NEVER))
+    assert orc.norm_err(sk, dp.astype(np.float64), K, 1.0, 1.0) <= 2 * orc.TOL

@@ -41,18 +41,22 @@ def _pair(ck, orc, M, N, K, op_a, op_b, seed):
     ((256, 256, 1 << 18, 0, 0), (128, 192, 1 << 16, 0, 0)),   # split-K both times
     ((1024, 1024, 1024, 0, 0), (520, 264, 1000, 1, 1)),      # small split-K, then odd T/T
     ((2048, 2048, 2048, 0, 1), (64, 64, 4096, 1, 0)),        # unsplit, then split-K
+    ((1280, 1280, 8192, 0, 0), (1024, 1024, 1024, 1, 0)),    # stream-K, then split-K
 ])
 def test_noalloc_matches_workspace_entry_point(ck, orc, dev, first, second):
     used = [_pair(ck, orc, *first, seed=1200), _pair(ck, orc, *second, seed=1300)]
     if first[2] >= 1 << 16:
         assert used[0], "the first case is meant to take split-K"
+    if first[:3] == (1280, 1280, 8192):
+        rc, p = ck.abi.plan(*first[:3], workspace_bytes=1 << 40)
+        assert rc == 0 and p.stream_k == 1 and used[0]
 
 
 def test_noalloc_rejects_problems_beyond_its_scratch(ck, dev):
     L = ck.abi.lib()
-    M = N = 3072                       # split 4 of 36 MiB partials: 144 MiB
+    M = N = 2048                       # split 8 of 16 MiB partials: 128 MiB
     K = 1 << 20
-    args = ck.abi.make_args(M, N, K)
+    args = ck.abi.make_args(M, N, K, plan_override=3 | (8 << 8))
     need = L.mi_gemm_workspace_bytes(ctypes.byref(args))
     assert need > ck.abi.NOALLOC_SCRATCH_BYTES
     # nothing is launched: the operands are never touched
