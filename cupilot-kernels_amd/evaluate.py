@@ -22,6 +22,8 @@ or a stated synthetic shape.  Inputs are uniform[-1, 1) from the library's
 counter-based generator, resident in HBM before timing; latency is the mean
 of ``--reps`` calls between HIP events on the current stream after
 ``--warmup`` calls, output allocation included (as KernelBench times a call).
+With ``--cpu`` the host torch operator is timed on the same inputs (best of 3
+calls after one warm-up call, all host threads) after every GPU timing.
 """
 from __future__ import annotations
 
@@ -198,8 +200,8 @@ def _norm_diff(got, ref, inputs, k: int) -> float:
     return d / (math.sqrt(max(k, 1)) * scale)
 
 
-def run(pids: Optional[Sequence[int]] = None, preset: str = "baseline", warmup: int = 2,
-        reps: int = 5, cpu: bool = False, log=print) -> List[Dict[str, object]]:
+def run(pids: Optional[Sequence[int]] = None, preset: str = "baseline", warmup: int = 3,
+        reps: int = 10, cpu: bool = False, log=print) -> List[Dict[str, object]]:
     """Measure every problem (or ``pids``); returns one row dict per problem."""
     import ctypes
     import torch
@@ -219,9 +221,8 @@ def run(pids: Optional[Sequence[int]] = None, preset: str = "baseline", warmup: 
         return t
 
     rows = []
-    for p in _problems(ck, preset):
-        if pids and p.pid not in pids:
-            continue
+    todo = [p for p in _problems(ck, preset) if not pids or p.pid in pids]
+    for p in todo:
         inputs = p.make(u)
         torch.cuda.synchronize()
         t_ref = _time_gpu(p.torch_ref, inputs, warmup, reps)
@@ -234,28 +235,37 @@ def run(pids: Optional[Sequence[int]] = None, preset: str = "baseline", warmup: 
             thr, unit = p.nbytes / (t_ours * 1e-3) / 1e9, "GB/s"
         else:
             thr, unit = p.flops / (t_ours * 1e-3) / 1e12, "TFLOP/s"
-        t_cpu, threads = None, None
-        if cpu:
-            threads = os.cpu_count() or 1
-            torch.set_num_threads(threads)
-            host = [t.cpu() if isinstance(t, torch.Tensor) else t for t in inputs]
-            p.torch_ref(*host)
-            t0 = time.perf_counter()
-            p.torch_ref(*host)
-            t_cpu = (time.perf_counter() - t0) * 1e3
-            del host
         row = {
             "Problem_ID": p.pid, "Kernels": KERNELS_LABEL,
             "Target_PyTorch_Latency(ms)": t_ref, "Generated_Kernel_Latency(ms)": t_ours,
             "Ratio_to_Target": t_ref / t_ours if t_ours > 0 else float("nan"),
             "Shape": p.shape, "Work": p.note, "Generated_Throughput": thr, "Unit": unit,
-            "Max_Norm_Diff_vs_Torch": diff, "CPU_Torch_Latency(ms)": t_cpu, "CPU_Threads": threads,
+            "Max_Norm_Diff_vs_Torch": diff, "CPU_Torch_Latency(ms)": None, "CPU_Threads": None,
         }
         rows.append(row)
         log(f"[eval] PID {p.pid:3d} {p.shape:>24s}: torch {t_ref:9.4f} ms  ours {t_ours:9.4f} ms  "
             f"ratio {row['Ratio_to_Target']:6.2f}  {thr:8.1f} {unit}  diff {diff:.2e}")
         del inputs
         torch.cuda.empty_cache()
+    if cpu:
+        # host legs after every GPU timing: the host BLAS leaves its threads
+        # spinning on every core for a while, which delays GPU launches
+        threads = os.cpu_count() or 1
+        torch.set_num_threads(threads)
+        for p, row in zip(todo, rows):
+            inputs = p.make(u)
+            host = [t.cpu() if isinstance(t, torch.Tensor) else t for t in inputs]
+            del inputs
+            torch.cuda.empty_cache()
+            p.torch_ref(*host)                      # one warm-up call, then the best of 3
+            best = float("inf")
+            for _ in range(3):
+                t0 = time.perf_counter()
+                p.torch_ref(*host)
+                best = min(best, time.perf_counter() - t0)
+            row["CPU_Torch_Latency(ms)"], row["CPU_Threads"] = best * 1e3, threads
+            log(f"[eval] PID {p.pid:3d} host torch {best * 1e3:9.2f} ms on {threads} threads")
+            del host
     return rows
 
 
@@ -288,8 +298,8 @@ def main(argv=None) -> int:
                     help="reference-schema CSV; the extended table goes next to it (*_ext.csv)")
     ap.add_argument("--pids", default="", help="comma-separated problem ids (default: all)")
     ap.add_argument("--preset", choices=["baseline", "small"], default="baseline")
-    ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--reps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--reps", type=int, default=10)
     ap.add_argument("--cpu", action="store_true", help="also time the torch operator on the host")
     a = ap.parse_args(argv)
     pids = [int(x) for x in a.pids.split(",") if x.strip()]
