@@ -438,15 +438,25 @@ def summary_header(cfg, timed, warmup, root):
               f"  rocprofv3 --pmc FETCH_SIZE --output-format csv -d {root}/copy/f -o c -- python3 bench.py --mode copy",
               f"  rocprofv3 --pmc WRITE_SIZE --output-format csv -d {root}/copy/w -o c -- python3 bench.py --mode copy",
               f"  python3 bench.py --summarize {d}/trace {d}/pmc1 {d}/pmc2 {d}/pmc3 --calib {root}/copy "
-              f"--mode {cfg.name} --steps {timed}", ""]
+              f"--mode {cfg.name} --steps {timed} --warmup {warmup}", ""]
     return lines
 
 
-def summarize(dirs, calib, timed, cfg=None):
+def _per_call(n_dispatch, timed, warmup):
+    """Dispatches of a kernel per operator call in a --mode run of
+    warmup + timed calls (1 when the count does not divide evenly)."""
+    calls = timed + (warmup or 0)
+    if warmup is not None and n_dispatch >= calls and n_dispatch % calls == 0:
+        return n_dispatch // calls
+    return 1
+
+
+def summarize(dirs, calib, timed, cfg=None, warmup=None):
     """Text summary of rocprofv3 --output-format csv runs: per kernel, the
-    mean over its last `timed` dispatches (the timed calls of a --mode run);
-    with cfg, the operator's time (its kernels' timed means added) against
-    its algorithmic work and roofline."""
+    mean over the dispatches of the last `timed` calls of a --mode run of
+    warmup + timed calls; with cfg, the operator's time per call (its
+    kernels' timed means times their dispatches per call, added) against its
+    algorithmic work and roofline."""
     out = []
     means = {}   # kernel -> timed mean (ns), for ordering and picking the main kernel
     trace = _csv_rows(dirs, "_kernel_trace.csv")
@@ -454,19 +464,22 @@ def summarize(dirs, calib, timed, cfg=None):
         by = {}
         for r in trace:
             by.setdefault(r["Kernel_Name"], []).append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
-        out.append(f"kernel durations (us): all dispatches, and the mean of the last {timed} "
-                   f"(the timed calls)")
-        out.append(f"  {'calls':>5} {'timed mean':>11} {'min':>9} {'max':>9}  kernel")
+        out.append(f"kernel durations (us): all dispatches, and the mean over the dispatches of the "
+                   f"last {timed} calls (the timed calls)")
+        out.append(f"  {'disp':>5} {'per call':>8} {'timed mean':>11} {'min':>9} {'max':>9}  kernel")
         op_us = 0.0
         for k, v in sorted(by.items(), key=lambda kv: -sum(kv[1])):
-            last = v[-timed:] if len(v) >= timed else v
+            per_call = _per_call(len(v), timed, warmup)
+            last = v[-timed * per_call:] if len(v) >= timed * per_call else v
             mean = sum(last) / len(last) / 1e3
-            means[k] = mean
-            out.append(f"  {len(v):5d} {mean:11.2f} {min(v) / 1e3:9.2f} {max(v) / 1e3:9.2f}  {_short(k)}")
+            means[k] = mean * per_call
+            out.append(f"  {len(v):5d} {per_call:8d} {mean:11.2f} {min(v) / 1e3:9.2f} {max(v) / 1e3:9.2f}  "
+                       f"{_short(k)}")
             if len(v) >= timed and not any(x in k for x in SETUP_KERNELS):
-                op_us += mean
+                op_us += mean * per_call
         if cfg is not None and op_us > 0:
-            out.append(f"operator time (timed means of its kernels added): {op_us:.2f} us")
+            out.append(f"operator time per call (timed means x dispatches per call, added over its kernels): "
+                       f"{op_us:.2f} us")
             if cfg.flops is not None:
                 tf = cfg.flops / (op_us * 1e-6) / 1e12
                 out.append(f"  algorithmic {cfg.flops:.6g} flop -> {tf:.2f} TFLOP/s = {tf / cfg.peak:.3f} of "
@@ -494,7 +507,7 @@ def summarize(dirs, calib, timed, cfg=None):
             d = per.setdefault(r["Kernel_Name"], {}).setdefault(int(r["Dispatch_Id"]), {})
             d[r["Counter_Name"]] = float(r["Counter_Value"])
             d["ns"] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
-        out.append(f"counters per dispatch (mean of the last {timed} dispatches of each kernel):")
+        out.append(f"counters per dispatch (mean over the dispatches of the last {timed} calls):")
         traffic = None
         main = max((k for k in per if not any(x in k for x in SETUP_KERNELS)),
                    key=lambda k: means.get(k, 0.0), default=None)
@@ -503,11 +516,12 @@ def summarize(dirs, calib, timed, cfg=None):
                 continue
             # one dict per dispatch, merged over the counter passes in dispatch order
             vals = list(ds.values())
+            per_call = _per_call(len(vals), timed, warmup)
             cnames = sorted({c for v in vals for c in v if c != "ns"})
             last = {}
             for c in cnames:
                 xs = [v[c] for v in vals if c in v]
-                xs = xs[-timed:] if len(xs) >= timed else xs
+                xs = xs[-timed * per_call:] if len(xs) >= timed * per_call else xs
                 last[c] = sum(xs) / len(xs)
             out.append(f"  {_short(k)}")
             line = []
@@ -518,7 +532,7 @@ def summarize(dirs, calib, timed, cfg=None):
                     line.append(f"MFMA busy {100 * busy / (cyc * NUM_SIMD):.1f} % "
                                 f"(SQ_VALU_MFMA_BUSY_CYCLES / (1024 SIMDs x GRBM_GUI_ACTIVE / 8 XCDs))")
                 ns = [v["ns"] for v in vals if "GRBM_GUI_ACTIVE" in v]
-                ns = ns[-timed:] if len(ns) >= timed else ns
+                ns = ns[-timed * per_call:] if len(ns) >= timed * per_call else ns
                 if sum(ns) / len(ns) > 2e5:   # (shorter dispatches: GRBM counts beyond them)
                     line.append(f"engine clock {cyc / (sum(ns) / len(ns)):.2f} GHz (GRBM_GUI_ACTIVE / "
                                 f"8 XCDs over the dispatch)")
@@ -559,7 +573,8 @@ def main() -> int:
             sys.path.insert(0, REPO)
             import __graft_entry__
             cfg = {c.name: c for c in configs(__graft_entry__.load_package())}.get(args.mode)
-        text = summarize(args.summarize, args.calib, args.steps, cfg)
+        text = summarize(args.summarize, args.calib, args.steps, cfg,
+                         args.warmup if cfg is not None else None)
         if cfg is not None:
             root = os.path.dirname(os.path.normpath(args.summarize[0]))
             root = os.path.relpath(os.path.dirname(root), REPO) if os.path.isabs(root) else os.path.dirname(root)
