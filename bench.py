@@ -3,6 +3,9 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-configs]
     python bench.py --mode NAME [--steps K] [--warmup W]     one config alone (profiling)
     python bench.py --mode list                              the config names
+    python bench.py --mode gemm:MxNxK[:TN|NT|TT][@BITS][,...] [--override BITS]
+                                                    dense products through the C ABI, with a
+                                                    plan override (stream-K / tile / split)
     python bench.py --summarize DIR [DIR ...] [--calib DIR]  rocprofv3 CSV output -> text summary
 
 One step = the BASELINE configs[1] workload: an fp32 8192^3 GEMM in each of the
@@ -70,6 +73,9 @@ def parse_args():
                         "table only), copy (a plain 1 GiB device copy: PMC calibration), list, or "
                         "one config name")
     p.add_argument("--no-configs", action="store_true", help="skip the per-config table")
+    p.add_argument("--override", type=lambda x: int(x, 0), default=0,
+                   help="with --mode gemm:MxNxK[:TN|NT|TT]: mi_gemm_args.plan_override (bits 0-3 tile "
+                        "config, 4 take stream-K, 5 no stream-K, 8-19 split count)")
     p.add_argument("--summarize", nargs="+", metavar="DIR",
                    help="summarise rocprofv3 CSV output under DIR(s) and exit")
     p.add_argument("--calib", metavar="DIR", default=None,
@@ -221,6 +227,40 @@ def configs(ck):
         cpu_note="F.scaled_dot_product_attention in fp32", cpu_scale=32.0,
         cpu_sample="batch 0 of 32 (32 heads), time x 32", baseline=False)
     return C
+
+
+def adhoc_gemm(ck, mode, override):
+    """--mode gemm:MxNxK[:TN|NT|TT]: one dense product through the C ABI
+    (mi_gemm_f32) with a plan override and a workspace from the plan."""
+    import ctypes
+
+    import torch
+    parts = mode.split(":")
+    M, N_, K = (int(x) for x in parts[1].split("x"))
+    lay = parts[2] if len(parts) > 2 else "NN"
+    op_a, op_b = int(lay[0] == "T"), int(lay[1] == "T")
+    L = ck.abi.lib()
+    state = {}
+
+    def make(u):
+        a = u((K, M) if op_a else (M, K), 1)
+        b = u((N_, K) if op_b else (K, N_), 2)
+        c = torch.empty((M, N_), device=a.device)
+        args = ck.abi.make_args(M, N_, K, op_a=op_a, op_b=op_b, plan_override=override,
+                                workspace_bytes=1 << 40)
+        need = L.mi_gemm_workspace_bytes(ctypes.byref(args))
+        ws = torch.empty(max(need, 1), dtype=torch.uint8, device=a.device)
+        args.A, args.B, args.C = a.data_ptr(), b.data_ptr(), c.data_ptr()
+        args.workspace, args.workspace_bytes = ws.data_ptr(), need
+        state["keep"] = (a, b, c, ws)
+        return (args,)
+
+    def op(args):
+        ck.abi.check(L.mi_gemm_f32(ctypes.byref(args),
+                                   ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), "mi_gemm_f32")
+    c = Cfg(mode, make, op, None, flops=2.0 * M * N_ * K, baseline=False)
+    c.M, c.N, c.K, c.op_a, c.op_b = M, N_, K, op_a, op_b
+    return c
 
 
 def make_filler(ck, dev, stream):
@@ -610,6 +650,20 @@ def main() -> int:
             dst.copy_(src)
         torch.cuda.synchronize()
         log("copy: 1 GiB read + 1 GiB write x3")
+        return 0
+    if args.mode.startswith("gemm:"):
+        # a comma-separated list of gemm:MxNxK[:LAYOUT][@OVERRIDE]; --override
+        # applies where a spec names none
+        for spec in args.mode.split(","):
+            spec, _, ov = spec.partition("@")
+            override = int(ov, 0) if ov else args.override
+            c = adhoc_gemm(ck, spec, override)
+            rc, plan = ck.abi.plan(c.M, c.N, c.K, op_a=c.op_a, op_b=c.op_b, workspace_bytes=1 << 40,
+                                   plan_override=override)
+            ck.abi.check(rc, "mi_gemm_plan")
+            r = run_config(c, u, stream, reps=args.steps, warmup=args.warmup, exact_warmup=True)
+            print(json.dumps({"config": spec, "override": hex(override), "plan": plan.plan_id,
+                              "split_k": plan.split_k, "stream_k": plan.stream_k, **r}), flush=True)
         return 0
     if args.mode in by_name:
         c = by_name[args.mode]

@@ -97,9 +97,16 @@ __global__ void __launch_bounds__(T::NT) gemm_f32_panel_kernel(const GemmParams 
             return tn_begin + (q >= run ? q - run : q);
         };
 
-        // every wave is past the previous item's last barrier: LDS is free
-        la.load(A, p.lda, m0, p.M, 0, p.K, tid);
-        la.store(sA, tid);
+        // every wave is past the previous item's last barrier: LDS is free.
+        // (lda and the thread index are made opaque per item: otherwise the
+        // panel load's per-slot rows and addresses, invariant across items,
+        // are hoisted out of the item loop and kept live through it -- with A
+        // stored K x M more than the 64-deep 256-row panel's 256 VGPRs hold.)
+        int64_t lda_item = p.lda;
+        int tid_a = tid;
+        asm volatile("" : "+s"(lda_item), "+v"(tid_a));
+        la.load(A, lda_item, m0, p.M, 0, p.K, tid_a);
+        la.store(sA, tid_a);
         if (run > 0) {
             lb.load(B, p.ldb, col_tile(0) * T::BN, p.N, 0, p.K, tid);
             lb.store(sB[0], tid);
@@ -209,13 +216,21 @@ __global__ void __launch_bounds__(T::NT) gemm_f32_panel_kernel(const GemmParams 
             };
             // one step: prefetch the next B tile, compute (and store the
             // previous tile), then put the prefetched tile in the other buffer
+            // The 64-deep 256-row panel with A stored K x M runs at the 256-VGPR
+            // limit: there the B loader's addresses are recomputed each step
+            // from an opaque copy of the thread index instead of being kept
+            // live (and spilled) across the column walk.
+            constexpr bool TIGHT = AT && T::KMAX == 64 && T::BM == 256;
             auto step_fn = [&](int step, f16v (&acc_c)[T::TM][T::TN],
                                const f16v (&acc_s)[T::TM][T::TN], bool store) {
                 const int buf = step & 1;
                 const int tn_next = col_tile(step + 1 < run ? step + 1 : step);
-                lb.load(B, p.ldb, tn_next * T::BN, p.N, 0, p.K, tid);
+                int tid_b = tid;
+                if constexpr (TIGHT) asm volatile("" : "+v"(tid_b));
+                lb.load(B, p.ldb, tn_next * T::BN, p.N, 0, p.K, tid_b);
                 tile_step(acc_c, sB[buf], acc_s, store ? col_tile(step - 1) : 0, store);
-                lb.store(sB[buf ^ 1], tid);
+                if constexpr (TIGHT) asm volatile("" : "+v"(tid_b));
+                lb.store(sB[buf ^ 1], tid_b);
                 __syncthreads();
             };
 
