@@ -156,7 +156,8 @@ int mi_gemm_tile_of(const mi_gemm_args* args, int32_t num_cus, int64_t item, int
         case kCfg64: compute = MI_TILE_OF(64); break;
         case kCfg128:
         case kCfg128K32:
-        case kCfg128K64: compute = MI_TILE_OF(128); break;
+        case kCfg128K64:
+        case kCfg128B32: compute = MI_TILE_OF(128); break;
         default: compute = MI_TILE_OF(256); break;
     }
 #undef MI_TILE_OF
@@ -202,6 +203,7 @@ int mi_gemm_work_item(const mi_gemm_args* args, int32_t num_cus, int64_t wg, int
     switch (g.cfg) {
         case kCfg64: tile_of<64, 64, kDense>(kp, (int)t, g.num_tiles, split, tm, tn, kb, ke); break;
         case kCfg256: tile_of<256, 256, kDense>(kp, (int)t, g.num_tiles, split, tm, tn, kb, ke); break;
+        case kCfg128B32:
         default: tile_of<128, 128, kDense>(kp, (int)t, g.num_tiles, split, tm, tn, kb, ke); break;
     }
     out->tile_m = tm;

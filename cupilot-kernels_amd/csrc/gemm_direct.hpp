@@ -79,7 +79,8 @@ __device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, uint32_t vo
 template <bool KCONTIG, int NW, int ROWS = 256, int BK = 32, int VB = 16>
 struct DirectLoader {
     static_assert((ROWS == 256 && BK == 32) || (ROWS == 128 && BK == 16) ||
-                      ((ROWS == 128 || ROWS == 512) && BK == 32 && KCONTIG && VB == 16),
+                      (ROWS == 128 && BK == 32 && VB == 16) ||
+                      (ROWS == 512 && BK == 32 && KCONTIG && VB == 16),
                   "slice shapes built");
     static_assert(VB == 16 || VB == 4, "dwordx4 or dword loads");
     // K-contiguous: a row is CH 16-byte chunks, swizzled; RPW rows share one
@@ -693,6 +694,7 @@ inline hipError_t launch_direct_tile(const GemmLaunch& g, hipStream_t s) {
 template <bool AT, bool BT>
 inline hipError_t launch_direct(const GemmLaunch& g, hipStream_t s) {
     if (!direct_ok(g)) return launch_direct_tile<Tile128, AT, BT, 4>(g, s);
+    if (g.cfg == kCfg128B32) return launch_direct_tile<Tile128B32, AT, BT, 16>(g, s);
     return g.cfg == kCfg128 ? launch_direct_tile<Tile128, AT, BT, 16>(g, s)
                             : launch_direct_tile<Tile256, AT, BT, 16>(g, s);
 }

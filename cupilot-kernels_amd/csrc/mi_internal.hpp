@@ -18,9 +18,11 @@ namespace mi {
 //   5   128 x 128        4      64 x 64     ~68 KiB, one 64-deep slice (K <= 64)
 //   6   256 x 128 panel  8      64 x 64     A panel resident, K <= 32 (~71 KiB, 1 WG/CU)
 //   7   256 x 128 panel  8      64 x 64     A panel resident, K <= 64 (~137 KiB)
+//   8   128 x 128 panel  8      64 x 32     A panel resident, K <= 64
+//   9   128 x 128        4      64 x 64     32-deep slices, direct-staged only (~65 KiB, 2 WGs/CU)
 enum TileCfgId {
     kCfg64 = 1, kCfg128 = 2, kCfg256 = 3, kCfg128K32 = 4, kCfg128K64 = 5,
-    kCfgPanel32 = 6, kCfgPanel64 = 7, kCfgPanel128x64 = 8, kNumCfg = 9
+    kCfgPanel32 = 6, kCfgPanel64 = 7, kCfgPanel128x64 = 8, kCfg128B32 = 9, kNumCfg = 10
 };
 inline bool is_panel_cfg(int id) {
     return id == kCfgPanel32 || id == kCfgPanel64 || id == kCfgPanel128x64;
@@ -39,6 +41,7 @@ inline CfgInfo cfg_info(int id) {
         case kCfgPanel32: return {256, 128, 32, 512};
         case kCfgPanel64: return {256, 128, 64, 512};
         case kCfgPanel128x64: return {128, 128, 64, 512};
+        case kCfg128B32: return {128, 128, 32, 256};
         default: return {0, 0, 0, 0};
     }
 }
@@ -98,6 +101,12 @@ inline bool direct_ok(const GemmLaunch& g) {
         const int64_t lim_a = g.op_a == 0 ? (INT64_C(1) << 22) : (INT64_C(1) << 25);
         const int64_t lim_b = g.op_b != 0 ? (INT64_C(1) << 22) : (INT64_C(1) << 25);
         return g.K % 16 == 0 && g.k_chunk % 16 == 0 && g.lda <= lim_a && g.ldb <= lim_b;
+    }
+    if (g.cfg == kCfg128B32) {
+        // 128 rows of a K-contiguous operand, 32 rows of an MN-contiguous one
+        const int64_t lim_a = g.op_a == 0 ? (INT64_C(1) << 22) : (INT64_C(1) << 24);
+        const int64_t lim_b = g.op_b != 0 ? (INT64_C(1) << 22) : (INT64_C(1) << 24);
+        return g.K % 32 == 0 && g.k_chunk % 32 == 0 && g.lda <= lim_a && g.ldb <= lim_b;
     }
     return false;
 }

@@ -5,16 +5,18 @@
 // replaces the reference's per-kernel compile-time tilings and shape-specific
 // literals (e.g. kernels/2_...:16-18 and :129-132 hard-code 2048x8192x4096 and a
 // 4x108 persistent grid; kernels/6_...:147-188 splits K over 8 host streams)
-// with one cost model over (tile config c, split s):
-//   t_mfma(c, s)  = ceil(tiles(c) * batch * s / CUs) * 2*BM*BN*(K/s) / (eff(c) * CU peak)
-//   t_store(s)    = output bytes (s partial copies when split) / sustained write bandwidth
-//   time(c, s)    = max(t_mfma, t_store) + (1 - overlap(c)) * min(t_mfma, t_store)
-//                   + split-K reduction traffic
-// and picks the cheapest.  eff and overlap are calibrated on MI355X: the
-// 256-tile runs one workgroup per CU, so its stores overlap its MFMAs only
-// through the next-tile prefetch; the smaller tiles keep 4-8 workgroups per
-// CU in flight.  Triangular problems use a square tiling with the compute
-// tiles ordered longest-K first.
+// with one cost model over (tile config c, split s) and stream-K:
+//   per_cu        = ceil(tiles(c) * batch * s / CUs) work items per CU
+//   occ           = min(resident workgroups of c, per_cu)
+//   time(c, s)    = per_cu * 2*BM*BN*(K/s) / (eff(c, occ) * CU peak)
+//                   + items per workgroup * fixed item cost(c)
+//                   + exposed(c, occ) * output bytes * s / sustained write bandwidth
+//                   + split-K reduction (read s partials, write C; one pass)
+//   stream-K(c)   = the same MFMA work spread evenly over every resident
+//                   workgroup, one partial tile per workgroup, and the fixup
+// and picks the cheapest.  The constants are fitted to MI355X timings (see
+// kModels).  Triangular problems use a square tiling with the compute tiles
+// ordered longest-K first.
 #include <algorithm>
 #include <cstdint>
 
@@ -28,36 +30,45 @@ namespace {
 
 struct CfgModel {
     int id;
-    double efficiency;  // sustained fraction of the CU's MFMA peak (measured)
-    double overlap;     // fraction of the shorter of MFMA / store time hidden
+    double eff[3];         // sustained fraction of the CU's MFMA peak with 1, 2, >= 3
+                           // workgroups of the config resident on the CU
+    double item_ns;        // fixed cost per work item of a workgroup
+    double store_exp[2];   // fraction of the output store time left exposed with
+                           // 1 and >= 2 workgroups per CU
 };
 
-// Measured on MI355X (8192^3: 256-tile 85 %; 16384x768x2048: 128-tile 78 %,
-// 256-tile 62 % because 192 tiles leave CUs idle; 1024^3: 64-tile best).
-// The single-slice configs only apply when K fits their slice.
+// Cost model of a dense plan, fitted to 2147 MI355X timings of candidate
+// plans -- 64 / 128 / 32-deep 128 / 256 tiles, split-K 1 - 32, stream-K --
+// over 141 shapes from 256 x 512 x 4096 to 8192 x 3072 x 16384, N/N plus all
+// four layouts of 12 of them (tests/data/plan_timings_mi355x.csv, fitted by
+// plan_fit.py: a local search on the ranking from a least-squares fit on log
+// time).  The plan it picks is on average 0.8 % slower than the fastest one
+// measured, at most 6.6 % (the previous model: 6.1 %, at most 40 %).  The
+// single-slice configs (K <= 32 / 64) take the 128 tile's constants with half
+// its exposed store time.
 constexpr CfgModel kModels[] = {
-    {kCfg256, 0.86, 0.7},
-    {kCfg128, 0.80, 0.8},
-    {kCfg64, 0.55, 0.8},
-    {kCfg128K32, 0.80, 0.95},
-    {kCfg128K64, 0.80, 0.95},
+    {kCfg256, {0.945, 0.945, 0.945}, 660.0, {1.48, 1.48}},
+    {kCfg128, {0.824, 0.910, 0.916}, 3990.0, {0.87, 0.523}},
+    {kCfg64, {0.448, 0.644, 0.724}, 2960.0, {0.87, 0.523}},
+    {kCfg128K32, {0.824, 0.910, 0.916}, 0.0, {0.44, 0.26}},
+    {kCfg128K64, {0.824, 0.910, 0.916}, 0.0, {0.44, 0.26}},
+    {kCfg128B32, {0.846, 0.913, 0.913}, 4260.0, {0.87, 0.523}},
 };
 
 constexpr double kPeakFlopsPerCuNs = 256.0 * 2.4;  // fp32 MFMA flop per ns per CU
-constexpr double kHbmBytesPerNs = 8000.0;
 constexpr double kWriteBytesPerNs = 5500.0;        // sustained write-only bandwidth (measured)
-// Stream-K: MFMA efficiency relative to whole tiles (segment starts and ends
-// inside the K loop), and the fixup launch.  Fitted to MI355X timings of
-// forced stream-K against the data-parallel plans: it must rank 6144^3 and
-// 5376^3 below the data-parallel 128 tile (147.1 vs 144.7, 145.6 vs 142.9
-// TFLOP/s) and 7168^2 x 4096 above it (143.8 vs 138.1): 0.884 < f < 0.926.
-constexpr double kSkEfficiency = 0.91;
-constexpr double kSkFixupNs = 4000.0;
+// split-K reduction and stream-K fixup passes: bytes per ns over what they
+// read and write, plus a fixed cost per reduction pass
+constexpr double kReduceBytesPerNs = 8850.0;
+constexpr double kReduceNs = 5430.0;
+// stream-K: the fixup workgroup of a tile adds its G / S partials one after
+// another (G workgroups, S stream-K tiles)
+constexpr double kSkSlotNs = 990.0;
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // Smallest K per split the cost model may choose.
-constexpr int64_t kMinSplitK = 256;
+constexpr int64_t kMinSplitK = 128;
 
 // Workgroups of each config held on one CU at once; the kernels are built to
 // exactly this occupancy (amdgpu_waves_per_eu): 64-tile 8, 128-tile 3, 256-tile 1.
@@ -70,6 +81,7 @@ int resident_wgs(int cfg) {
         case kCfgPanel32: return 1;
         case kCfgPanel64: return 1;
         case kCfgPanel128x64: return 1;
+        case kCfg128B32: return 2;
         default: return 8;
     }
 }
@@ -128,7 +140,7 @@ struct SkChoice {
 
 SkChoice plan_stream_k(const mi_gemm_args& a, int cfg, int num_cus) {
     SkChoice sk;
-    if (cfg != kCfg256 && cfg != kCfg128) return sk;
+    if (cfg != kCfg256 && cfg != kCfg128 && cfg != kCfg128B32) return sk;
     if (a.structure != MI_DENSE || a.batch > 1 || a.bias_m != nullptr) return sk;
     if (((uintptr_t)a.workspace & 15u) != 0) return sk;
     const CfgInfo ci = cfg_info(cfg);
@@ -178,8 +190,14 @@ int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
     const int override_split = (a.plan_override >> 8) & 0xFFF;
     const int override_group = (a.plan_override >> 20) & 0x7FF;
 
+    // the 32-deep 128 tile exists only direct-staged (16-byte operands, K % 32 == 0)
+    // (its row limits: the buffer offsets of 128 K-contiguous rows or 32
+    // MN-contiguous rows stay below 2^31 bytes)
+    const bool b32_ok = a.structure == MI_DENSE && choose_vec(a) == 4 && a.K % 32 == 0 &&
+                        a.lda <= (a.op_a == 0 ? (INT64_C(1) << 22) : (INT64_C(1) << 24)) &&
+                        a.ldb <= (a.op_b != 0 ? (INT64_C(1) << 22) : (INT64_C(1) << 24));
     const bool override_ok =
-        override_cfg >= kCfg64 && override_cfg < kNumCfg &&
+        override_cfg >= kCfg64 && override_cfg < kNumCfg && (override_cfg != kCfg128B32 || b32_ok) &&
         !((override_cfg == kCfg128K32 || override_cfg == kCfg128K64 || is_panel_cfg(override_cfg)) &&
           a.K > cfg_info(override_cfg).bk) &&
         !(is_panel_cfg(override_cfg) && a.structure != MI_DENSE);
@@ -243,33 +261,37 @@ int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
         for (const CfgModel& m : kModels) {
             const CfgInfo ci = cfg_info(m.id);
             if ((m.id == kCfg128K32 || m.id == kCfg128K64) && a.K > ci.bk) continue;
-            double eff = m.id == kCfg256 && !full16 ? 0.75 * m.efficiency : m.efficiency;
-            // One 256 tile per CU: at K <= 512 its 256 KiB store is barely
-            // covered by the next tile's short MFMA run.  Measured, 128 vs 256
-            // tile at K = 256: 65536x512 135 vs 139 us, 16384x2048 136 vs 149,
-            // 8192^2 270 vs 275, equal at 131072x512 and 65536x768; K = 512:
-            // 4096^2 129 vs 137, 4096x8192 256 vs 261, 65536x512 250 vs 253;
-            // within 1.6 % at K = 1024 - 2048, the 256 tile 1-1.5 % ahead at 4096.
-            if (m.id == kCfg256 && a.K <= 512) eff *= 0.92;
+            if (m.id == kCfg128B32 && !b32_ok) continue;
+            // the 64 tile stages through registers: with operands that are not
+            // 16-byte aligned it loads one float at a time, where the 128 tile
+            // keeps direct 4-byte staging (4248 x 2044 x 3769: 59 vs 96 TFLOP/s)
+            const double scale = m.id == kCfg256 && !full16      ? 0.75
+                                 : m.id == kCfg64 && choose_vec(a) != 4 ? 0.6
+                                                                        : 1.0;
+            const int res = resident_wgs(m.id);
             const int64_t tiles = cdiv(a.M, ci.bm) * cdiv(a.N, ci.bn) * batch;
+            const double tile_bytes = 4.0 * ci.bm * ci.bn;
             for (int s = 1; s <= 1024; s *= 2) {
                 if (s > 1) {
                     // split only to fill the machine, with >= kMinSplitK of K per
-                    // split; up to twice the CUs in items, since the per-CU
-                    // quantisation above decides (1536^3, 144 tiles: split 2
-                    // leaves some CUs two items, split 4 measured 86 vs 104 us)
+                    // split: up to twice the CUs in items
                     if (tiles * (s / 2) >= 2 * (int64_t)num_cus) break;
                     if (a.K / s < kMinSplitK) break;
                     const size_t need = (size_t)s * batch * a.M * a.N * sizeof(float);
                     if (a.workspace_bytes < need) break;
                 }
+                // per CU: its share of the work items, run with as many of them
+                // resident as the config allows; each workgroup walks its items
+                const int64_t items = tiles * s;
                 const int64_t kc = cdiv(cdiv(std::max<int64_t>(a.K, 1), s), ci.bk) * ci.bk;
-                const double per_cu = (double)cdiv(tiles * s, (int64_t)num_cus);
-                const double t_mfma = per_cu * 2.0 * ci.bm * ci.bn * (double)kc /
-                                      (eff * kPeakFlopsPerCuNs);
-                const double t_store = out_bytes * s / kWriteBytesPerNs;
-                double t = std::max(t_mfma, t_store) + (1.0 - m.overlap) * std::min(t_mfma, t_store);
-                if (s > 1) t += 2.0 * s * out_bytes / kHbmBytesPerNs;
+                const int64_t per_cu = cdiv(items, (int64_t)num_cus);
+                const int occ = (int)std::min<int64_t>(res, per_cu);
+                const int64_t grid = std::min<int64_t>((int64_t)num_cus * res, items);
+                const double eff = scale * m.eff[std::min(occ, 3) - 1];
+                double t = (double)per_cu * 2.0 * ci.bm * ci.bn * (double)kc / (eff * kPeakFlopsPerCuNs);
+                t += (double)cdiv(items, grid) * m.item_ns;
+                t += m.store_exp[occ > 1 ? 1 : 0] * out_bytes * s / kWriteBytesPerNs;
+                if (s > 1) t += (s + 1) * out_bytes / kReduceBytesPerNs + kReduceNs;
                 if (t < best_t * 0.999) {
                     best_t = t;
                     best_cfg = m.id;
@@ -277,18 +299,19 @@ int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
                     best_sk = SkChoice{};
                 }
             }
-            // Stream-K on this config: the same MFMA work spread evenly over the
-            // workgroups (no wave quantisation), plus one extra partial-tile
-            // store per workgroup and the fixup pass (read the partials, read
-            // and write the split tiles of C; one more launch).
+            // Stream-K on this config: the MFMA work spread evenly over every
+            // resident workgroup (no wave quantisation), plus one partial tile
+            // stored per workgroup and the fixup pass (read the partials, read
+            // and write the split tiles of C).
             const SkChoice sk = no_sk ? SkChoice{} : plan_stream_k(a, m.id, num_cus);
             if (sk.tiles > 0) {
-                const double tile_bytes = 4.0 * ci.bm * ci.bn;
-                const double t_mfma = (double)tiles * 2.0 * ci.bm * ci.bn * (double)a.K /
-                                      num_cus / (eff * kSkEfficiency * kPeakFlopsPerCuNs);
-                const double t_store = (out_bytes + sk.grid * tile_bytes) / kWriteBytesPerNs;
-                double t = std::max(t_mfma, t_store) + (1.0 - m.overlap) * std::min(t_mfma, t_store);
-                t += 3.0 * sk.grid * tile_bytes / kHbmBytesPerNs + kSkFixupNs;
+                const double eff = scale * m.eff[std::min(res, 3) - 1];
+                double t = (double)tiles * 2.0 * ci.bm * ci.bn * (double)a.K / num_cus /
+                           (eff * kPeakFlopsPerCuNs);
+                t += (double)(sk.dp / sk.grid + 2) * m.item_ns;
+                t += m.store_exp[res > 1 ? 1 : 0] * (out_bytes + sk.grid * tile_bytes) / kWriteBytesPerNs;
+                t += 3.0 * sk.grid * tile_bytes / kReduceBytesPerNs +
+                     kSkSlotNs * (double)sk.grid / sk.tiles;
                 if (t < best_t * 0.999) {
                     best_t = t;
                     best_cfg = m.id;

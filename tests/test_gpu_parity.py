@@ -88,6 +88,39 @@ def test_integer_inputs_bitwise(ck, orc, dev, op_a, op_b, cfg):
     np.testing.assert_array_equal(to_host(C), ref.astype(np.float32))
 
 
+@pytest.mark.parametrize("op_a,op_b", LAYOUTS)
+@pytest.mark.parametrize("M,N,K,extra", [(512, 512, 512, 0), (300, 200, 96, 0), (700, 520, 32, 0),
+                                         (132, 1028, 64, 0), (1000, 996, 1024, 0),
+                                         (260, 128, 2048, 2 << 8), (1280, 1280, 2048, 0x10)])
+def test_b32_tile_config(ck, orc, dev, op_a, op_b, M, N, K, extra):
+    """The 32-deep direct-staged 128 tile (config 9): plain, split-K and
+    stream-K schedules, ragged edges, every layout."""
+    ov = 9 | extra
+    rc, p = ck.abi.plan(M, N, K, op_a=op_a, op_b=op_b, workspace_bytes=1 << 40, plan_override=ov)
+    assert rc == 0 and p.plan_id == 9 and p.block_k == 32
+    assert p.stream_k == (1 if extra & 0x10 else 0) and p.split_k == (extra >> 8 or 1)
+    a_st, b_st = _host_operands(orc, M, N, K, op_a, op_b, seed=13)
+    A, B = to_dev(a_st), to_dev(b_st)
+    C = torch.full((M, N), float("nan"), device="cuda")
+    ws = workspace(ck, gemm_args(ck, A, B, C, M, N, K, op_a, op_b, override=ov))
+    ck.abi.check(run_gemm(ck, gemm_args(ck, A, B, C, M, N, K, op_a, op_b, override=ov, ws=ws)))
+    ref = orc.gemm(_logical(a_st, op_a), _logical(b_st, op_b))
+    assert_close(orc, to_host(C), ref, K, np.abs(a_st).max(), np.abs(b_st).max(),
+                 f"cfg 9 layout {op_a}{op_b} {M}x{N}x{K} override {ov:#x}")
+
+
+@pytest.mark.parametrize("op_a,op_b", LAYOUTS)
+def test_b32_integer_inputs_bitwise(ck, orc, dev, op_a, op_b):
+    M, N, K = 200, 136, 992
+    a_st = orc.integers((K, M) if op_a else (M, K), seed=23)
+    b_st = orc.integers((N, K) if op_b else (K, N), seed=24)
+    A, B = to_dev(a_st), to_dev(b_st)
+    C = torch.empty((M, N), device="cuda")
+    ck.abi.check(run_gemm(ck, gemm_args(ck, A, B, C, M, N, K, op_a, op_b, override=9)))
+    ref = orc.gemm(_logical(a_st, op_a), _logical(b_st, op_b))
+    np.testing.assert_array_equal(to_host(C), ref.astype(np.float32))
+
+
 def test_closed_forms_identity_ones_rank1(ck, orc, dev):
     n = 384
     I = np.eye(n, dtype=np.float32)
