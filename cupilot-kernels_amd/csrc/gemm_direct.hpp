@@ -231,7 +231,7 @@ __device__ __forceinline__ void store_tile_direct(const GemmParams& p, float* C,
                                                   bool c_vec, const TileWork& w,
                                                   const f16v (&acc)[T::TM][T::TN], int wm, int wn,
                                                   int lane) {
-    static_assert(!B_IL || T::TN == 2, "one interleaved pair of column blocks per wave");
+    static_assert(!B_IL || T::TN % 2 == 0, "column blocks interleave in pairs");
     static_assert(!A_IL || T::TM % 2 == 0, "row blocks pair up");
     const bool to_mirror = MODE != kDense && w.mirror;
     const bool tri_mask = MODE != kDense && !w.mirror;
@@ -266,17 +266,20 @@ __device__ __forceinline__ void store_tile_direct(const GemmParams& p, float* C,
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             if (B_IL) {
-                f4 lo, hi;
 #pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                    lo[2 * e] = acc[i][0][4 * q + e];
-                    lo[2 * e + 1] = acc[i][1][4 * q + e];
-                    hi[2 * e] = acc[i][0][4 * q + 2 + e];
-                    hi[2 * e + 1] = acc[i][1][4 * q + 2 + e];
+                for (int u = 0; u < T::TN / 2; ++u) {  // block pair u: columns 64 u ..
+                    f4 lo, hi;
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        lo[2 * e] = acc[i][2 * u][4 * q + e];
+                        lo[2 * e + 1] = acc[i][2 * u + 1][4 * q + e];
+                        hi[2 * e] = acc[i][2 * u][4 * q + 2 + e];
+                        hi[2 * e + 1] = acc[i][2 * u + 1][4 * q + 2 + e];
+                    }
+                    const int col = cw + 64 * u + 16 * q + (lane >> 5) * 4;  // 16 q + 8 h
+                    put(col, lo);
+                    put(col + 4, hi);
                 }
-                const int col = cw + 16 * q + (lane >> 5) * 4;  // 16 q + 8 h
-                put(col, lo);
-                put(col + 4, hi);
             } else {
 #pragma unroll
                 for (int j = 0; j < T::TN; ++j) {
@@ -434,7 +437,9 @@ __global__ void __launch_bounds__(T::NT)
 #pragma unroll
             for (int j = 0; j < T::TN; ++j) LB::frag(Bs, wn * T::WN + j * 32, kb, lane, fb[kb & 1][j]);
         } else {
-            LB::frag_pair(Bs, wn * T::WN, kb, lane, fb[kb & 1]);
+#pragma unroll
+            for (int u = 0; u < T::TN / 2; ++u)
+                LB::frag_pair(Bs, wn * T::WN + u * 64, kb, lane, fb[kb & 1] + 2 * u);
         }
         if constexpr (VB == 4) {
             if (kv < T::BK) {
@@ -639,6 +644,16 @@ __global__ void __launch_bounds__(T::NT)
     }
 }
 
+// 256 x 256 tiles on 4 waves of 128 x 128 (one wave per SIMD, the 256
+// accumulators of a lane in AGPRs), one tile per workgroup: dense products
+// whose slices are all full 16-byte direct loads (direct_ok).  The K loop is
+// a single body (the LDS buffer is picked by the slice's parity) so the
+// compiler keeps every accumulator in the same AGPRs across iterations; an
+// unrolled-by-two body made it split them between AGPRs and VGPRs, with
+// copies and spills.  Per slice: issue the next slice's loads into the other
+// buffer, run this slice's MFMAs (the next k-block's fragments read ahead of
+// each k-block), barrier, read the next slice's first fragments behind the
+// last k-block's held-back MFMAs.
 // Triangular N/N products on the chunked work list (the scheduler plans it
 // when N is a multiple of 256 and the direct path's operand conditions hold),
 // then the pass that folds the mirror partials in and zeroes the rest of the
