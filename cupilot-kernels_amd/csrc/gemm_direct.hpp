@@ -209,6 +209,22 @@ struct DirectLoader {
         out[3] = t[3];
     }
 
+    // MN-contiguous operand, four blocks at once: values for the 4 MFMA steps
+    // of k-block kb in the four interleaved blocks of the 128 columns at c0
+    // (block t, lane i: column c0 + 4 i + t), one 16-byte read per step.
+    __device__ __forceinline__ static void frag_quad(const float* lds, int c0, int kb, int lane,
+                                                     float out[4][4]) {
+        static_assert(!KCONTIG, "K-contiguous fragments are read one block at a time");
+        const int g = 2 * kb + (lane >> 5);  // k = 4 g + s
+        const int col = c0 + 4 * (lane & 31);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const f4 t = *reinterpret_cast<const f4*>(lds + row_base(s * (BK / 4) + g) + col);
+#pragma unroll
+            for (int b = 0; b < 4; ++b) out[b][s] = t[b];
+        }
+    }
+
     // MN-contiguous operand: values for the 4 MFMA steps of k-block kb in the
     // two interleaved blocks of the 64 columns at c0 (block t, lane i: column
     // c0 + 2 i + t).
@@ -229,6 +245,8 @@ struct DirectLoader {
 // Epilogue.  An MN-contiguous operand's 32-wide blocks are interleaved in
 // pairs (frag_pair), which moves its rows / columns:
 //   A (rows):    block i = 2 u + t, lane l -> row 64 u + 2 (l % 32) + t;
+//                with four row blocks per wave (frag_quad) block i = 4 u + t,
+//                lane l -> row 128 u + 4 (l % 32) + t;
 //                K-contiguous A: block i, lane l -> row 32 i + l % 32.
 //   B (columns): register r of the swapped-operand MFMA is block column
 //                i' = 8 (r / 4) + 4 (l / 32) + r % 4; interleaved B puts it at
@@ -249,6 +267,7 @@ __device__ __forceinline__ void store_tile_direct(const GemmParams& p, float* C,
                                                   int lane) {
     static_assert(!B_IL || T::TN % 2 == 0, "column blocks interleave in pairs");
     static_assert(!A_IL || T::TM % 2 == 0, "row blocks pair up");
+    constexpr bool A_QUAD = A_IL && T::TM % 4 == 0;  // frag_quad's interleave
     const bool to_mirror = MODE != kDense && w.mirror;
     const bool tri_mask = MODE != kDense && !w.mirror;
     const int r0 = (to_mirror ? w.tn : w.tm) * T::BM;
@@ -258,7 +277,9 @@ __device__ __forceinline__ void store_tile_direct(const GemmParams& p, float* C,
     const bool add_bias = BIAS && p.split_k == 1;
 #pragma unroll
     for (int i = 0; i < T::TM; ++i) {
-        const int row = r0 + wm * T::WM + (A_IL ? 64 * (i / 2) + 2 * l32 + (i & 1) : 32 * i + l32);
+        const int row = r0 + wm * T::WM +
+                        (A_QUAD ? 128 * (i / 4) + 4 * l32 + (i & 3)
+                                : A_IL ? 64 * (i / 2) + 2 * l32 + (i & 1) : 32 * i + l32);
         if (row >= p.M) continue;
         const float bv = add_bias ? p.bias[row] : 0.f;
         float* const crow = LOCAL ? C + (int64_t)(row - r0) * ldc : C + (int64_t)row * ldc;
@@ -444,6 +465,10 @@ __global__ void __launch_bounds__(T::NT)
         if constexpr (A_KC) {
 #pragma unroll
             for (int i = 0; i < T::TM; ++i) LA::frag(As, wm * T::WM + i * 32, kb, lane, fa[kb & 1][i]);
+        } else if constexpr (T::TM % 4 == 0) {  // four row blocks per 16-byte read
+#pragma unroll
+            for (int u = 0; u < T::TM / 4; ++u)
+                LA::frag_quad(As, wm * T::WM + u * 128, kb, lane, fa[kb & 1] + 4 * u);
         } else {
 #pragma unroll
             for (int u = 0; u < T::TM / 2; ++u)
