@@ -521,10 +521,11 @@ __global__ void __launch_bounds__(T::NT)
     // Per slice: the next slice's loads, then for each k-block the next
     // k-block's fragment reads ahead of this k-block's MFMAs (scheduling
     // barriers keep that order).  With full 16-byte slices the loads are
-    // spread: part(-1) before the first k-block, part(s) after its MFMA step
-    // s (see the caller), so a wave does not stall on the address unit with
-    // all of them at once while its SIMD's MFMA pipe drains (8192^3 N/N
-    // +0.5 %, N/T +1.2 %).  The last k-block's s = 2, 3 MFMAs are held
+    // spread: part(s) after MFMA step s of the first k-block, so a wave does
+    // not stall on the address unit with all of them at once while its
+    // SIMD's MFMA pipe drains (8192^3 N/N +0.5 %, N/T +1.2 %, T/N and T/T
+    // +0.3 % once MN-contiguous A takes frag_quad; before that, spreading
+    // A's loads cost those two layouts 0.5 %).  The last k-block's s = 2, 3 MFMAs are held
     // back until after the slice barrier (tail), where they cover the latency
     // of the next slice's first fragment reads, issued right after the
     // barrier; so the slice's first k-block fragments are already in
@@ -532,10 +533,7 @@ __global__ void __launch_bounds__(T::NT)
     constexpr int NKB = T::BK / 8;
     constexpr bool SPREAD = VB == 16 && NKB >= 2;
     auto compute = [&](const float* As, const float* Bs, auto&& loads, auto&& part) __attribute__((always_inline)) {
-        if constexpr (SPREAD)
-            part(-1);
-        else
-            loads();
+        if constexpr (!SPREAD) loads();
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb) {
@@ -669,16 +667,7 @@ __global__ void __launch_bounds__(T::NT)
         static_assert(!SPREAD || (LA::PER_WAVE <= 4 && LB::PER_WAVE <= 4), "parts 0..3 cover every load");
         compute(curA, curB, [&]() __attribute__((always_inline)) { issue(nw, nit, nxtA, nxtB); },
                 [&](int q) __attribute__((always_inline)) {
-                    // MN-contiguous A (T/N, T/T) keeps its loads up front:
-                    // spread, those layouts measured 0.5 % slower
-                    if constexpr (AT) {
-                        if (q < 0) {
-#pragma unroll
-                            for (int i = 0; i < LA::PER_WAVE; ++i) LA::load_one(ra, voA, nxtA, wave, i);
-                        }
-                    } else {
-                        if (q >= 0 && q < LA::PER_WAVE) LA::load_one(ra, voA, nxtA, wave, q);
-                    }
+                    if (q >= 0 && q < LA::PER_WAVE) LA::load_one(ra, voA, nxtA, wave, q);
                     if (q >= 0 && q < LB::PER_WAVE) LB::load_one(rb, voB, nxtB, wave, q);
                 });
         __syncthreads();
