@@ -137,9 +137,10 @@ def test_operators_replay_in_a_hip_graph(ck, dev):
     sequence of them can be captured in a HIP graph: captured once, replayed
     three times with eager work and synchronisations between the replays,
     every replay bitwise equal to the eager results.  Covers the direct-staged
-    256 and 128 tiles, split-K with its reduction (workspace), the chunked
-    triangular list with its finishing pass, GEMV, diag, pointwise conv and
-    attention."""
+    256 and 128 tiles, split-K with its reduction (workspace), stream-K with
+    its fixup on the 256 and 32-deep 128 tiles, the 32-deep tile data-parallel
+    and split, the chunked triangular list with its finishing pass, GEMV,
+    diag, pointwise conv and attention."""
     g = torch.Generator(device="cuda")
     g.manual_seed(97)
     u = lambda *shape: torch.rand(*shape, device="cuda", generator=g) * 2 - 1
@@ -151,9 +152,21 @@ def test_operators_replay_in_a_hip_graph(ck, dev):
     dv, dm = u(2048), u(2048, 2048)
     cx, cw, cb = u(2, 64, 64, 64), u(128, 64), u(128)
     q, k, v = (u(1, 2, 128, 1024).half() for _ in range(3))
+    # plans: stream-K on the 256 tile, stream-K / data-parallel / split-K on
+    # the 32-deep 128 tile (asserted below)
+    sk3a, sk3b = u(3072, 8192), u(8192, 3072)
+    sk9a, sk9b = u(1280, 8192), u(8192, 1280)
+    d9a, d9b = u(2048, 2048), u(2048, 4096)
+    s9a, s9b = u(1024, 1024), u(1024, 1024)
+    for (m, kk, n), want in [((3072, 8192, 3072), (3, 1)), ((1280, 8192, 1280), (9, 1)),
+                             ((2048, 2048, 4096), (9, 0)), ((1024, 1024, 1024), (9, 0))]:
+        rc, p = ck.abi.plan(m, n, kk, workspace_bytes=1 << 40)
+        assert rc == 0 and (p.plan_id, p.stream_k) == want, (m, kk, n, p.plan_id, p.stream_k)
 
     def ops():
-        return [ck.p01.matmul_cuda(a4, b4), ck.p02.matmul_cuda(a2, b2), ck.p06.matmul_cuda(lka, lkb),
+        return [ck.p02.matmul_cuda(sk3a, sk3b), ck.p02.matmul_cuda(sk9a, sk9b), ck.p02.matmul_cuda(d9a, d9b),
+                ck.p01.matmul_cuda(s9a, s9b),
+                ck.p01.matmul_cuda(a4, b4), ck.p02.matmul_cuda(a2, b2), ck.p06.matmul_cuda(lka, lkb),
                 ck.p15.lower_tri_mul_cuda(ta, tb), ck.p04.gemv_cuda(ga, gx), ck.p12.diag_mult_cuda(dv, dm),
                 ck.p87.pointwise_conv_cuda(cx, cw, cb), ck.p97.fused_attention_cuda(q, k, v)]
 
