@@ -4,6 +4,7 @@
     python bench.py --mode NAME [--steps K] [--warmup W]     one config alone (profiling)
     python bench.py --mode list                              the config names
     python bench.py --mode gemm:MxNxK[:TN|NT|TT][@BITS][,...] [--override BITS]
+    python bench.py --mode torch:MxNxK[:TN|NT|TT][,...]     (torch-ROCm's own GEMM, for profiling)
                                                     dense products through the C ABI, with a
                                                     plan override (stream-K / tile / split)
     python bench.py --summarize DIR [DIR ...] [--calib DIR]  rocprofv3 CSV output -> text summary
@@ -261,6 +262,28 @@ def adhoc_gemm(ck, mode, override):
     c = Cfg(mode, make, op, None, flops=2.0 * M * N_ * K, baseline=False)
     c.M, c.N, c.K, c.op_a, c.op_b = M, N_, K, op_a, op_b
     return c
+
+
+def adhoc_torch_gemm(mode):
+    """--mode torch:MxNxK[:TN|NT|TT]: the same product through torch-ROCm's
+    own GEMM (A @ B on the GPU, transposed views for the T layouts), for
+    profiling the library kernel this path is measured against."""
+    import torch
+    parts = mode.split(":")
+    M, N_, K = (int(x) for x in parts[1].split("x"))
+    lay = parts[2] if len(parts) > 2 else "NN"
+    op_a, op_b = lay[0] == "T", lay[1] == "T"
+    state = {}
+
+    def make(u):
+        a = u((K, M) if op_a else (M, K), 1)
+        b = u((N_, K) if op_b else (K, N_), 2)
+        state["keep"] = (a, b)
+        return (a.t() if op_a else a, b.t() if op_b else b)
+
+    def op(a, b):
+        state["out"] = a @ b
+    return Cfg(mode, make, op, None, flops=2.0 * M * N_ * K, baseline=False)
 
 
 def make_filler(ck, dev, stream):
@@ -609,7 +632,9 @@ def main() -> int:
     args = parse_args()
     if args.summarize:
         cfg = None
-        if args.mode not in ("full", "gemm", "configs", "copy", "list"):
+        if args.mode.startswith("torch:") and "," not in args.mode:
+            cfg = adhoc_torch_gemm(args.mode)
+        elif args.mode not in ("full", "gemm", "configs", "copy", "list"):
             sys.path.insert(0, REPO)
             import __graft_entry__
             cfg = {c.name: c for c in configs(__graft_entry__.load_package())}.get(args.mode)
@@ -664,6 +689,12 @@ def main() -> int:
             r = run_config(c, u, stream, reps=args.steps, warmup=args.warmup, exact_warmup=True)
             print(json.dumps({"config": spec, "override": hex(override), "plan": plan.plan_id,
                               "split_k": plan.split_k, "stream_k": plan.stream_k, **r}), flush=True)
+        return 0
+    if args.mode.startswith("torch:"):
+        for spec in args.mode.split(","):
+            c = adhoc_torch_gemm(spec)
+            r = run_config(c, u, stream, reps=args.steps, warmup=args.warmup, exact_warmup=True)
+            print(json.dumps({"config": spec, "operator": "torch A @ B", **r}), flush=True)
         return 0
     if args.mode in by_name:
         c = by_name[args.mode]
