@@ -123,7 +123,11 @@ int mi_gemm_tile_of(const mi_gemm_args* args, int32_t num_cus, int64_t item, int
     GemmLaunch g{};
     rc = plan_gemm(ca, num_cus, p, &g);
     if (rc != MI_OK) return rc;
-    if (item < 0 || item >= g.num_tiles || split < 0 || split >= g.split_k) return MI_ERR_BAD_SIZE;
+    // the chunked triangular list (dynamic order) continues past its compute
+    // items with the zero tiles its workgroups write
+    const int64_t n_items =
+        g.num_tiles + (g.tri_cap >= 2 ? tri_zero_items(g.tiles_m, g.tri_cap) : 0);
+    if (item < 0 || item >= n_items || split < 0 || split >= g.split_k) return MI_ERR_BAD_SIZE;
     if (g.sk_tiles > 0) return MI_ERR_BAD_LAYOUT;  // stream-K: mi_gemm_work_item
     const GemmParams kp = make_params(g);
     int tm = 0, tn = 0, kb = 0, ke = 0;
@@ -138,7 +142,16 @@ int mi_gemm_tile_of(const mi_gemm_args* args, int32_t num_cus, int64_t item, int
     }
     if (g.tri_cap > 0) {
         // chunked triangular list: 2 marks a chunk whose partial sum is
-        // stored in the mirror tile (tile_n, tile_m) and added in afterwards
+        // stored in the mirror tile (tile_n, tile_m) and added in afterwards;
+        // 3 a zero-triangle tile the workgroup writes with +0.0 (no K range)
+        if (item >= g.num_tiles) {
+            tri_zero_tile((int)(item - g.num_tiles), g.tiles_m, g.structure == kLower, tm, tn);
+            *tile_m = tm;
+            *tile_n = tn;
+            *k_begin = 0;
+            *k_end = 0;
+            return 3;
+        }
         int u0, u1, mirror;
         tri_item((int)item, g.tiles_m, g.tri_cap, g.structure == kLower, tm, tn, u0, u1, mirror);
         *tile_m = tm;

@@ -611,11 +611,44 @@ __global__ void __launch_bounds__(T::NT)
     __shared__ int s_item;
     int* const ctr = MODE == kLower ? reinterpret_cast<int*>(p.C + 256)
                                     : reinterpret_cast<int*>(p.C + 256 * p.ldc);
+    // Past the compute items the counter hands out the zero-triangle tiles
+    // of tri_zero_tile (tiles with no parked partial): a workgroup writes
+    // +0.0 over each it claims, so the tail of the list, when CUs run out of
+    // compute items, does the stores the finishing pass would do after the
+    // kernel.
+    auto zero_items = [&](int z) __attribute__((always_inline)) {
+        if constexpr (MODE != kDense) {
+            const int total = p.num_tiles + tri_zero_items(p.tiles_m, p.tri_cap);
+            while (z < total) {
+                int zm, zn;
+                tri_zero_tile(z - p.num_tiles, p.tiles_m, MODE == kLower, zm, zn);
+                float* const z0 = C + (int64_t)zm * T::BM * ldc + (int64_t)zn * T::BN;
+#pragma unroll 4
+                for (int e = tid; e < T::BM * (T::BN / 4); e += T::NT) {
+                    float* const d = z0 + (int64_t)(e / (T::BN / 4)) * ldc + (e % (T::BN / 4)) * 4;
+                    if (c_vec) {
+                        *reinterpret_cast<f4*>(d) = f4{0.f, 0.f, 0.f, 0.f};
+                    } else {
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) d[q] = 0.f;
+                    }
+                }
+                __syncthreads();  // every wave has read s_item
+                if (tid == 0) s_item = atomicAdd(ctr, 1);
+                __syncthreads();
+                z = s_item;
+            }
+        }
+    };
     int t = SK ? 0 : blockIdx.x;
     if (dyn) {
         if (tid == 0) s_item = atomicAdd(ctr, 1);
         __syncthreads();
         t = s_item;
+        if (t >= p.num_tiles) {
+            zero_items(t);
+            return;
+        }
     }
     if (!SK && t >= p.num_tiles) return;
     TileWork cur = decode(t);
@@ -654,6 +687,7 @@ __global__ void __launch_bounds__(T::NT)
             } else {
                 nt = dyn ? s_item : t + gridDim.x;
                 has_next = nt < p.num_tiles;
+                if (dyn && !has_next) t = nt;  // handed on to zero_items
                 if (has_next) nw = decode(nt);
             }
             nit = has_next ? 0 : it;
@@ -706,18 +740,9 @@ __global__ void __launch_bounds__(T::NT)
         if (slice(std::integral_constant<int, 0>{})) break;
         if (slice(std::integral_constant<int, 1>{})) break;
     }
+    if (dyn) zero_items(t);  // t: the claim that ended the compute items
 }
 
-// 256 x 256 tiles on 4 waves of 128 x 128 (one wave per SIMD, the 256
-// accumulators of a lane in AGPRs), one tile per workgroup: dense products
-// whose slices are all full 16-byte direct loads (direct_ok).  The K loop is
-// a single body (the LDS buffer is picked by the slice's parity) so the
-// compiler keeps every accumulator in the same AGPRs across iterations; an
-// unrolled-by-two body made it split them between AGPRs and VGPRs, with
-// copies and spills.  Per slice: issue the next slice's loads into the other
-// buffer, run this slice's MFMAs (the next k-block's fragments read ahead of
-// each k-block), barrier, read the next slice's first fragments behind the
-// last k-block's held-back MFMAs.
 // Triangular N/N products on the chunked work list (the scheduler plans it
 // when N is a multiple of 256 and the direct path's operand conditions hold),
 // then the pass that folds the mirror partials in and zeroes the rest of the
@@ -740,7 +765,7 @@ inline hipError_t launch_direct_tri(const GemmLaunch& g, hipStream_t s) {
                            dim3(Tile256::NT), 0, s, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    return launch_tri_finish(g.C, g.ldc, g.tiles_m, g.tri_cap, g.structure == kLower, s);
+    return launch_tri_finish(g.C, g.ldc, g.tiles_m, g.tri_cap, g.structure == kLower, g.tri_cap >= 2, s);
 }
 
 template <class T, bool AT, bool BT, int VB>

@@ -128,6 +128,27 @@ __host__ __device__ __forceinline__ void tri_item(int pid, int nt, int cap, bool
     u1 = u0 + len;
 }
 
+// Zero-triangle tiles the chunked list's workgroups write with +0.0 once
+// the compute items run out (dynamic order, cap >= 2): those at diagonal
+// distance 1 .. cap - 1, i.e. every zero tile except the mirror tiles
+// (distance >= cap, which park second-chunk partials for the finishing pass)
+// and the tile holding the item counter ((0, 1) lower, (1, 0) upper, which
+// the finishing pass zeroes).  Item z of them, by distance, then row.
+__host__ __device__ __forceinline__ int tri_zero_items(int nt, int cap) {
+    if (cap < 2 || nt < 2) return 0;
+    const int dmax = cap - 1 < nt - 1 ? cap - 1 : nt - 1;
+    return dmax * nt - dmax * (dmax + 1) / 2 - 1;
+}
+__host__ __device__ __forceinline__ void tri_zero_tile(int z, int nt, bool lower, int& tm, int& tn) {
+    int rem = z + 1, d = 1;  // + 1: skip the counter tile, distance 1 row 0
+    while (rem >= nt - d) {
+        rem -= nt - d;
+        ++d;
+    }
+    tm = lower ? rem : rem + d;
+    tn = lower ? rem + d : rem;
+}
+
 // Stream-K schedule (dense products on a persistent grid of G workgroups).
 // The T output tiles of one product, in raster order, are split into n_dp
 // data-parallel tiles (a multiple of G: whole waves, each tile reduced by one

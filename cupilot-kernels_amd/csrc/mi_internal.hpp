@@ -157,7 +157,10 @@ hipError_t launch_splitk_reduce(const float* ws, float* C, int M, int N, int bat
 // triangle, add it into its mirror compute tile when that tile was cut in two
 // (it holds the second chunk's partial sum), then write it with +0.0.  C is
 // nt*256 square.
-hipError_t launch_tri_finish(float* C, int64_t ldc, int nt, int cap, bool lower, hipStream_t s);
+// zeroed: the dynamic-order kernel already wrote the zero tiles that hold no
+// partial (tri_zero_tile), so only the mirrors and the counter's tile remain.
+hipError_t launch_tri_finish(float* C, int64_t ldc, int nt, int cap, bool lower, bool zeroed,
+                             hipStream_t s);
 // Writes integer 0 to one 4-byte word (a kernel, so it can be graph-captured).
 hipError_t launch_zero_word(void* w, hipStream_t s);
 // C[b][r][c] = bias ? bias[r] : 0 (a contraction with K = 0)

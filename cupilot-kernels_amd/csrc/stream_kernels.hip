@@ -439,10 +439,13 @@ hipError_t launch_fill_zero_2d(float* C, int64_t rows, int64_t cols, int64_t ld,
 // the first chunk's result (one fixed-order fp32 add).
 template <bool VEC>
 __global__ void __launch_bounds__(256)
-    tri_finish_kernel(float* __restrict__ C, int64_t ldc, int nt, int cap, int lower) {
+    tri_finish_kernel(float* __restrict__ C, int64_t ldc, int nt, int cap, int lower, int zeroed) {
     int a, b;
     tri_tile(nt * (nt + 1) / 2 + (int)blockIdx.x, nt, lower != 0, a, b);
     const bool add = (a > b ? a - b : b - a) + 1 > cap;
+    // zeroed: the main kernel wrote every zero tile but the mirrors and the
+    // item counter's tile (zero-triangle tile 0, (0, 1) / (1, 0))
+    if (zeroed && !add && blockIdx.x != 0) return;
     const int64_t row0 = (int64_t)blockIdx.y * 64;
     float* const z0 = C + ((int64_t)a * 256 + row0) * ldc + (int64_t)b * 256;
     float* const d0 = C + ((int64_t)b * 256 + row0) * ldc + (int64_t)a * 256;
@@ -463,14 +466,17 @@ __global__ void __launch_bounds__(256)
     }
 }
 
-hipError_t launch_tri_finish(float* C, int64_t ldc, int nt, int cap, bool lower, hipStream_t s) {
+hipError_t launch_tri_finish(float* C, int64_t ldc, int nt, int cap, bool lower, bool zeroed,
+                             hipStream_t s) {
     const int zero_tiles = nt * (nt - 1) / 2;
     if (zero_tiles == 0) return hipSuccess;
     const dim3 grid((unsigned)zero_tiles, 4);
     if (ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(C) & 15u) == 0)
-        hipLaunchKernelGGL(tri_finish_kernel<true>, grid, dim3(256), 0, s, C, ldc, nt, cap, (int)lower);
+        hipLaunchKernelGGL(tri_finish_kernel<true>, grid, dim3(256), 0, s, C, ldc, nt, cap, (int)lower,
+                           (int)zeroed);
     else
-        hipLaunchKernelGGL(tri_finish_kernel<false>, grid, dim3(256), 0, s, C, ldc, nt, cap, (int)lower);
+        hipLaunchKernelGGL(tri_finish_kernel<false>, grid, dim3(256), 0, s, C, ldc, nt, cap, (int)lower,
+                           (int)zeroed);
     return hipGetLastError();
 }
 

@@ -160,8 +160,11 @@ MI_API int mi_gemm_plan(const mi_gemm_args* args, int32_t num_cus, mi_plan* out)
  * (tile_n, tile_m) of the zero triangle and added in by a finishing pass
  * (the chunked work list of triangular products with N % 256 == 0; its items
  * run longest first, claimed in list order by persistent workgroups as they
- * free up, so which workgroup runs an item is decided at run time), a
- * negative mi_status on error. */
+ * free up, so which workgroup runs an item is decided at run time), 3 for a
+ * zero-triangle tile that list's workgroups write with +0.0 once its compute
+ * items are claimed (items num_tiles, num_tiles + 1, ...: every zero tile
+ * that parks no partial, except the one holding the item counter; the
+ * finishing pass writes the rest), a negative mi_status on error. */
 MI_API int mi_gemm_tile_of(const mi_gemm_args* args, int32_t num_cus, int64_t item, int32_t split,
                            int32_t* tile_m, int32_t* tile_n, int64_t* k_begin, int64_t* k_end);
 

@@ -262,6 +262,22 @@ def test_triangular_chunked_work_list(ck, structure, n, override, cap):
         rc, tm, tn, kb, ke = ck.abi.tile_of(args, wg)
         lengths.append(ke - kb)
     assert all(x >= y for x, y in zip(lengths, lengths[1:])), "items must run longest first"
+    # past the compute items: the zero tiles the workgroups write (rc 3) --
+    # every zero-triangle tile that parks no partial (distance < cap), once,
+    # except the counter's tile (0, 1) / (1, 0), which the finishing pass
+    # zeroes with the mirrors
+    zeros, i = [], p.num_tiles
+    while True:
+        rc, tm, tn, kb, ke = ck.abi.tile_of(args, i)
+        if rc < 0:
+            break
+        assert rc == 3 and kb == ke == 0
+        zeros.append((tm, tn))
+        i += 1
+    counter = (0, 1) if structure == 1 else (1, 0)
+    want_z = [(i, j) for i in range(T) for j in range(T)
+              if (i < j if structure == 1 else i > j) and abs(i - j) < cap and (i, j) != counter]
+    assert sorted(zeros) == sorted(want_z) and len(set(zeros)) == len(zeros)
 
 
 def test_triangular_chunked_plan_needs_direct_operands(ck):
