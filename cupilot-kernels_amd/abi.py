@@ -28,8 +28,8 @@ NOALLOC_SCRATCH_BYTES = 64 << 20
 
 MI_OP_N, MI_OP_T = 0, 1
 MI_DENSE, MI_LOWER, MI_UPPER, MI_SYMMETRIC = 0, 1, 2, 3
-CFG64, CFG128, CFG256, CFG128K32, CFG128K64, CFG_PANEL32, CFG_PANEL64, CFG_PANEL128, CFG128B32 = (
-    1, 2, 3, 4, 5, 6, 7, 8, 9)
+(CFG64, CFG128, CFG256, CFG128K32, CFG128K64, CFG_PANEL32, CFG_PANEL64, CFG_PANEL128, CFG128B32,
+ CFG64W) = (1, 2, 3, 4, 5, 6, 7, 8, 9, 10)
 
 _i64 = ctypes.c_int64
 _vp = ctypes.c_void_p

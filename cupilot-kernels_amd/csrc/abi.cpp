@@ -166,7 +166,8 @@ int mi_gemm_tile_of(const mi_gemm_args* args, int32_t num_cus, int64_t item, int
      : g.structure == kUpper ? tile_of<BMN, BMN, kUpper>(kp, bid, nb, split, tm, tn, kb, ke) \
                              : tile_of<BMN, BMN, kDense>(kp, bid, nb, split, tm, tn, kb, ke))
     switch (g.cfg) {
-        case kCfg64: compute = MI_TILE_OF(64); break;
+        case kCfg64:
+        case kCfg64W: compute = MI_TILE_OF(64); break;
         case kCfg128:
         case kCfg128K32:
         case kCfg128K64:
@@ -214,7 +215,8 @@ int mi_gemm_work_item(const mi_gemm_args* args, int32_t num_cus, int64_t wg, int
     const GemmParams kp = make_params(g);
     int tm = 0, tn = 0, kb = 0, ke = 0;
     switch (g.cfg) {
-        case kCfg64: tile_of<64, 64, kDense>(kp, (int)t, g.num_tiles, split, tm, tn, kb, ke); break;
+        case kCfg64:
+        case kCfg64W: tile_of<64, 64, kDense>(kp, (int)t, g.num_tiles, split, tm, tn, kb, ke); break;
         case kCfg256: tile_of<256, 256, kDense>(kp, (int)t, g.num_tiles, split, tm, tn, kb, ke); break;
         case kCfg128B32:
         default: tile_of<128, 128, kDense>(kp, (int)t, g.num_tiles, split, tm, tn, kb, ke); break;

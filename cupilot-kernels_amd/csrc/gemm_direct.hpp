@@ -80,6 +80,7 @@ template <bool KCONTIG, int NW, int ROWS = 256, int BK = 32, int VB = 16>
 struct DirectLoader {
     static_assert((ROWS == 256 && BK == 32) || (ROWS == 128 && BK == 16) ||
                       (ROWS == 128 && BK == 32 && VB == 16) ||
+                      (ROWS == 64 && BK == 64 && VB == 16) ||
                       (ROWS == 512 && BK == 32 && KCONTIG && VB == 16),
                   "slice shapes built");
     static_assert(VB == 16 || VB == 4, "dwordx4 or dword loads");

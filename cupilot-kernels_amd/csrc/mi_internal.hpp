@@ -20,9 +20,12 @@ namespace mi {
 //   7   256 x 128 panel  8      64 x 64     A panel resident, K <= 64 (~137 KiB)
 //   8   128 x 128 panel  8      64 x 32     A panel resident, K <= 64
 //   9   128 x 128        4      64 x 64     32-deep slices, direct-staged only (~65 KiB, 2 WGs/CU)
+//   10  64 x 64          8      64 x 64     each wave one 8-deep k-block of every 64-deep
+//                                           slice, 4-stage direct ring (~130 KiB, 1 WG/CU)
 enum TileCfgId {
     kCfg64 = 1, kCfg128 = 2, kCfg256 = 3, kCfg128K32 = 4, kCfg128K64 = 5,
-    kCfgPanel32 = 6, kCfgPanel64 = 7, kCfgPanel128x64 = 8, kCfg128B32 = 9, kNumCfg = 10
+    kCfgPanel32 = 6, kCfgPanel64 = 7, kCfgPanel128x64 = 8, kCfg128B32 = 9, kCfg64W = 10,
+    kNumCfg = 11
 };
 inline bool is_panel_cfg(int id) {
     return id == kCfgPanel32 || id == kCfgPanel64 || id == kCfgPanel128x64;
@@ -42,6 +45,7 @@ inline CfgInfo cfg_info(int id) {
         case kCfgPanel64: return {256, 128, 64, 512};
         case kCfgPanel128x64: return {128, 128, 64, 512};
         case kCfg128B32: return {128, 128, 32, 256};
+        case kCfg64W: return {64, 64, 64, 512};
         default: return {0, 0, 0, 0};
     }
 }
@@ -109,6 +113,14 @@ inline bool direct_ok(const GemmLaunch& g) {
         return g.K % 32 == 0 && g.k_chunk % 32 == 0 && g.lda <= lim_a && g.ldb <= lim_b;
     }
     return false;
+}
+
+// The 64 x 64 k-split tile (gemm_small.hpp) stages 16-byte slices only:
+// dense, K and the split chunk multiples of 64, and the byte offsets within a
+// slice (64 rows of either operand layout) below 2^31.
+inline bool ksplit_ok(int structure, int vec, int64_t K, int64_t k_chunk, int64_t lda, int64_t ldb) {
+    return structure == 0 && vec == 4 && K % 64 == 0 && k_chunk % 64 == 0 &&
+           lda <= (INT64_C(1) << 23) && ldb <= (INT64_C(1) << 23);
 }
 
 // Dense 128-tile launches the 16-byte path cannot take (operands not 16-byte

@@ -82,6 +82,7 @@ int resident_wgs(int cfg) {
         case kCfgPanel64: return 1;
         case kCfgPanel128x64: return 1;
         case kCfg128B32: return 2;
+        case kCfg64W: return 1;
         default: return 8;
     }
 }
@@ -196,8 +197,11 @@ int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
     const bool b32_ok = a.structure == MI_DENSE && choose_vec(a) == 4 && a.K % 32 == 0 &&
                         a.lda <= (a.op_a == 0 ? (INT64_C(1) << 22) : (INT64_C(1) << 24)) &&
                         a.ldb <= (a.op_b != 0 ? (INT64_C(1) << 22) : (INT64_C(1) << 24));
+    // the 64-tile k-split config: 16-byte operands, K a multiple of 64
+    const bool w64_ok = ksplit_ok(a.structure, choose_vec(a), a.K, 64, a.lda, a.ldb) && a.K > 0;
     const bool override_ok =
         override_cfg >= kCfg64 && override_cfg < kNumCfg && (override_cfg != kCfg128B32 || b32_ok) &&
+        (override_cfg != kCfg64W || w64_ok) &&
         !((override_cfg == kCfg128K32 || override_cfg == kCfg128K64 || is_panel_cfg(override_cfg)) &&
           a.K > cfg_info(override_cfg).bk) &&
         !(is_panel_cfg(override_cfg) && a.structure != MI_DENSE);

@@ -121,6 +121,74 @@ def test_b32_integer_inputs_bitwise(ck, orc, dev, op_a, op_b):
     np.testing.assert_array_equal(to_host(C), ref.astype(np.float32))
 
 
+@pytest.mark.parametrize("op_a,op_b", LAYOUTS)
+@pytest.mark.parametrize("M,N,K,batch,pad,split", [(1024, 1024, 1024, 1, 0, 1), (300, 520, 1088, 1, 0, 1),
+                                                   (260, 252, 2048, 1, 4, 1), (516, 260, 1024, 3, 0, 1),
+                                                   (264, 300, 512, 2, 4, 1), (64, 64, 64, 1, 0, 1),
+                                                   (20, 36, 192, 1, 0, 1), (132, 68, 128, 1, 4, 1),
+                                                   (256, 192, 4096, 1, 0, 4), (200, 136, 640, 2, 0, 2)])
+def test_ksplit_tile_config(ck, orc, dev, op_a, op_b, M, N, K, batch, pad, split):
+    """The 64 x 64 tile whose eight waves split each 64-deep slice (config 10):
+    every layout, edge rows and columns (loaded from the last valid row /
+    column, never stored), padded leading dimensions, batched, split-K, row
+    bias (N/N only); a 1-, 2- or 3-slice K range runs the ring's first steps
+    only."""
+    a_st = orc.uniform((batch,) + ((K, M) if op_a else (M, K)), 141)
+    b_st = orc.uniform((batch,) + ((N, K) if op_b else (K, N)), 142)
+    bias = orc.uniform((M,), 143)
+    lda, ldb, ldc = (M if op_a else K) + pad, (K if op_b else N) + pad, N + pad
+    a_pad = np.zeros((batch, a_st.shape[1], lda), np.float32)
+    a_pad[:, :, :a_st.shape[2]] = a_st
+    b_pad = np.zeros((batch, b_st.shape[1], ldb), np.float32)
+    b_pad[:, :, :b_st.shape[2]] = b_st
+    A, B, Bi = to_dev(a_pad), to_dev(b_pad), to_dev(bias)
+    la = np.swapaxes(a_st, 1, 2) if op_a else a_st
+    lb = np.swapaxes(b_st, 1, 2) if op_b else b_st
+    ov = 10 | (split << 8)
+    rc, p = ck.abi.plan(M, N, K, batch=batch, op_a=op_a, op_b=op_b, workspace_bytes=1 << 40,
+                        plan_override=ov)
+    assert rc == 0 and p.plan_id == 10 and p.block_k == 64 and p.split_k == split
+    for with_bias in ((False, True) if (op_a, op_b) == (0, 0) else (False,)):
+        C = torch.full((batch, M, ldc), float("nan"), device="cuda")
+        args = gemm_args(ck, A, B, C, M, N, K, op_a, op_b, batch=batch, lda=lda, ldb=ldb, ldc=ldc,
+                         sa=a_pad[0].size, sb=b_pad[0].size, sc=M * ldc, override=ov)
+        ws = workspace(ck, args)
+        args = gemm_args(ck, A, B, C, M, N, K, op_a, op_b, batch=batch, lda=lda, ldb=ldb, ldc=ldc,
+                         sa=a_pad[0].size, sb=b_pad[0].size, sc=M * ldc, override=ov, ws=ws)
+        if with_bias:
+            args.bias_m = Bi.data_ptr()
+        ck.abi.check(run_gemm(ck, args))
+        ref = orc.gemm(la, lb) + (bias.astype(np.float64)[None, :, None] if with_bias else 0.0)
+        got = to_host(C)
+        assert_close(orc, got[:, :, :N], ref, K,
+                     what=f"cfg 10 {op_a}{op_b} {M}x{N}x{K}x{batch} pad={pad} split={split} bias={with_bias}")
+        if pad:
+            assert np.isnan(got[:, :, N:]).all(), "a store landed in the ldc padding"
+
+
+@pytest.mark.parametrize("op_a,op_b", LAYOUTS)
+def test_ksplit_integer_inputs_bitwise_and_repeatable(ck, orc, dev, op_a, op_b):
+    """Config 10 on small-integer operands is exact, and its fixed-order
+    reduction of the eight waves' partial tiles repeats bit for bit on
+    uniform inputs."""
+    M, N, K = 200, 136, 1024
+    a_st = orc.integers((K, M) if op_a else (M, K), seed=25)
+    b_st = orc.integers((N, K) if op_b else (K, N), seed=26)
+    C = torch.empty((M, N), device="cuda")
+    ck.abi.check(run_gemm(ck, gemm_args(ck, to_dev(a_st), to_dev(b_st), C, M, N, K, op_a, op_b,
+                                        override=10)))
+    ref = orc.gemm(_logical(a_st, op_a), _logical(b_st, op_b))
+    np.testing.assert_array_equal(to_host(C), ref.astype(np.float32))
+    a_st, b_st = _host_operands(orc, M, N, K, op_a, op_b, seed=27)
+    A, B = to_dev(a_st), to_dev(b_st)
+    outs = []
+    for _ in range(3):
+        C = torch.full((M, N), float("nan"), device="cuda")
+        ck.abi.check(run_gemm(ck, gemm_args(ck, A, B, C, M, N, K, op_a, op_b, override=10)))
+        outs.append(to_host(C))
+    assert all(np.array_equal(outs[0], o) for o in outs[1:])
+
+
 def test_closed_forms_identity_ones_rank1(ck, orc, dev):
     n = 384
     I = np.eye(n, dtype=np.float32)
