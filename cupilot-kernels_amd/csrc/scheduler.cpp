@@ -37,33 +37,34 @@ struct CfgModel {
                            // 1 and >= 2 workgroups per CU
 };
 
-// Cost model of a dense plan, fitted to 2147 MI355X timings of candidate
-// plans -- 64 / 128 / 32-deep 128 / 256 tiles, split-K 1 - 32, stream-K --
-// over 141 shapes from 256 x 512 x 4096 to 8192 x 3072 x 16384, N/N plus all
-// four layouts of 12 of them (tests/data/plan_timings_mi355x.csv, fitted by
-// plan_fit.py: a local search on the ranking from a least-squares fit on log
-// time).  The plan it picks is on average 0.8 % slower than the fastest one
-// measured, at most 6.6 % (the previous model: 6.1 %, at most 40 %).  The
+// Cost model of a dense plan, fitted to 2814 MI355X timings of candidate
+// plans -- 64 / 128 / 32-deep 128 / 256 tiles, the 64-tile k-split config,
+// split-K 1 - 32, stream-K -- over 141 shapes from 256 x 512 x 4096 to
+// 8192 x 3072 x 16384, N/N plus all four layouts of 12 of them
+// (tests/data/plan_timings_mi355x.csv, fitted by plan_fit.py: a local search
+// on the ranking from the previous constants).  The plan it picks is on
+// average 0.8 % slower than the fastest one measured, at most 10.5 %.  The
 // single-slice configs (K <= 32 / 64) take the 128 tile's constants with half
 // its exposed store time.
 constexpr CfgModel kModels[] = {
-    {kCfg256, {0.945, 0.945, 0.945}, 660.0, {1.48, 1.48}},
-    {kCfg128, {0.824, 0.910, 0.916}, 3990.0, {0.87, 0.523}},
-    {kCfg64, {0.448, 0.644, 0.724}, 2960.0, {0.87, 0.523}},
-    {kCfg128K32, {0.824, 0.910, 0.916}, 0.0, {0.44, 0.26}},
-    {kCfg128K64, {0.824, 0.910, 0.916}, 0.0, {0.44, 0.26}},
-    {kCfg128B32, {0.846, 0.913, 0.913}, 4260.0, {0.87, 0.523}},
+    {kCfg256, {0.950, 0.950, 0.950}, 559.0, {1.495, 1.495}},
+    {kCfg128, {0.823, 0.910, 0.918}, 3838.0, {0.873, 0.517}},
+    {kCfg64, {0.430, 0.638, 0.707}, 2691.0, {0.873, 0.517}},
+    {kCfg128K32, {0.823, 0.910, 0.918}, 0.0, {0.44, 0.26}},
+    {kCfg128K64, {0.823, 0.910, 0.918}, 0.0, {0.44, 0.26}},
+    {kCfg128B32, {0.849, 0.913, 0.913}, 4233.0, {0.873, 0.517}},
+    {kCfg64W, {0.859, 0.859, 0.859}, 2893.0, {0.874, 0.874}},
 };
 
 constexpr double kPeakFlopsPerCuNs = 256.0 * 2.4;  // fp32 MFMA flop per ns per CU
 constexpr double kWriteBytesPerNs = 5500.0;        // sustained write-only bandwidth (measured)
 // split-K reduction and stream-K fixup passes: bytes per ns over what they
 // read and write, plus a fixed cost per reduction pass
-constexpr double kReduceBytesPerNs = 8850.0;
-constexpr double kReduceNs = 5430.0;
+constexpr double kReduceBytesPerNs = 8296.0;
+constexpr double kReduceNs = 5467.0;
 // stream-K: the fixup workgroup of a tile adds its G / S partials one after
 // another (G workgroups, S stream-K tiles)
-constexpr double kSkSlotNs = 990.0;
+constexpr double kSkSlotNs = 953.0;
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
@@ -266,6 +267,7 @@ int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
             const CfgInfo ci = cfg_info(m.id);
             if ((m.id == kCfg128K32 || m.id == kCfg128K64) && a.K > ci.bk) continue;
             if (m.id == kCfg128B32 && !b32_ok) continue;
+            if (m.id == kCfg64W && !w64_ok) continue;
             // the 64 tile stages through registers: with operands that are not
             // 16-byte aligned it loads one float at a time, where the 128 tile
             // keeps direct 4-byte staging (4248 x 2044 x 3769: 59 vs 96 TFLOP/s)

@@ -30,16 +30,17 @@ from scipy.optimize import least_squares
 NC = 256
 PEAK = 256 * 2.4  # fp32 MFMA flop per ns per CU
 WRITE = 5500.0
-BM = {1: 64, 2: 128, 3: 256, 9: 128}
-BK = {1: 16, 2: 16, 3: 32, 9: 32}
-RES = {1: 8, 2: 3, 3: 1, 9: 2}
+BM = {1: 64, 2: 128, 3: 256, 9: 128, 10: 64}
+BK = {1: 16, 2: 16, 3: 32, 9: 32, 10: 64}
+RES = {1: 8, 2: 3, 3: 1, 9: 2, 10: 1}
 NAMES = ["e1_1", "e1_2", "e1_3", "e2_1", "e2_2", "e2_3", "e3", "e9_1", "e9_2",
-         "o1", "o2", "o3", "o9", "x3", "x_occ1", "x_occ2", "reduce_bw", "reduce_ns", "sk_slot_ns"]
+         "o1", "o2", "o3", "o9", "x3", "x_occ1", "x_occ2", "reduce_bw", "reduce_ns", "sk_slot_ns",
+         "e10", "o10", "x10"]
 # the constants csrc/scheduler.cpp carries (the starting point of the search)
-X0 = [0.448, 0.644, 0.724, 0.824, 0.910, 0.916, 0.945, 0.846, 0.913, 2960, 3990, 660, 4260, 1.48, 0.87, 0.523,
-      8850, 5430, 990]
-LO = [0.2] * 9 + [0.0] * 4 + [0.0, 0.0, 0.0, 1000, 0, 0]
-HI = [1.2] * 9 + [5e4] * 4 + [1.5, 1.5, 1.5, 2e4, 5e4, 5e4]
+X0 = [0.430, 0.638, 0.707, 0.823, 0.910, 0.918, 0.950, 0.849, 0.913, 2691, 3838, 559, 4233, 1.495, 0.873,
+      0.517, 8296, 5467, 953, 0.859, 2893, 0.874]
+LO = [0.2] * 9 + [0.0] * 4 + [0.0, 0.0, 0.0, 1000, 0, 0] + [0.2, 0.0, 0.0]
+HI = [1.2] * 9 + [5e4] * 4 + [1.5, 1.5, 1.5, 2e4, 5e4, 5e4] + [1.2, 5e4, 1.5]
 
 
 def cdiv(a, b):
@@ -54,8 +55,9 @@ def model(r, x):
     out = 4.0 * M * N * B
     scale = 0.75 if (c == 3 and K % 32) else 1.0
     eff = {1: [P["e1_1"], P["e1_2"], P["e1_3"]], 2: [P["e2_1"], P["e2_2"], P["e2_3"]],
-           3: [P["e3"]] * 3, 9: [P["e9_1"], P["e9_2"], P["e9_2"]]}[c]
-    xs = [P["x3"], P["x3"]] if c == 3 else [P["x_occ1"], P["x_occ2"]]
+           3: [P["e3"]] * 3, 9: [P["e9_1"], P["e9_2"], P["e9_2"]], 10: [P["e10"]] * 3}[c]
+    xs = ([P["x3"], P["x3"]] if c == 3 else [P["x10"], P["x10"]] if c == 10
+          else [P["x_occ1"], P["x_occ2"]])
     o = P["o%d" % c]
     if sk:
         G = NC * RES[c]

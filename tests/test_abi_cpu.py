@@ -157,7 +157,6 @@ def test_plan_shallow_k_takes_the_128_tile(ck, M, N, K, want):
 
 
 @pytest.mark.parametrize("M,N,K,at_least,at_most", [
-    (1024, 1024, 1024, 4, 4),       # 64 tiles of 128: split 4 70.0 / no split 31.0 TFLOP/s
     (512, 512, 32768, 16, 64),      # 16 tiles: split 16 118 / stream-K 93
     (1024, 2048, 8192, 4, 8),       # split 4 136 / split 2 124
     (2048, 2048, 2048, 1, 1),       # 256 tiles of 128 fill the CUs: 125 / split 2 120
@@ -168,6 +167,33 @@ def test_plan_splits_only_where_tiles_are_few(ck, M, N, K, at_least, at_most):
     MI355X), not where the tiles already fill them."""
     rc, p = ck.abi.plan(M, N, K, workspace_bytes=1 << 40, plan_override=0x20)  # no stream-K
     assert rc == 0 and at_least <= p.split_k <= at_most, (M, N, K, p.plan_id, p.split_k)
+
+
+@pytest.mark.parametrize("M,N,K,want,split", [
+    # measured on MI355X (TFLOP/s): the 64-tile k-split config against the
+    # best other plan (tests/data/plan_timings_mi355x.csv)
+    (1024, 1024, 1024, 10, 1),   # 94 / 68 (the 128 tile split 4)
+    (512, 1536, 1024, 10, 1),
+    (256, 4096, 1536, 10, 1),
+    (1024, 1024, 2048, 10, 1),
+    (8192, 8192, 8192, 3, 1),    # many tiles: the 256 tile (150 / 135)
+    (2048, 2048, 1024, 9, 1),    # 118 / 113
+])
+def test_plan_small_problems_take_the_k_split_tile(ck, M, N, K, want, split):
+    """Where the 128 / 256 tiles fill the CUs only through split-K, the
+    64 x 64 tile whose waves split each K slice reduces the whole K range in
+    one launch, with no partial tiles; not where the larger tiles fill the
+    machine by themselves."""
+    rc, p = ck.abi.plan(M, N, K, workspace_bytes=1 << 40)
+    assert rc == 0 and (p.plan_id, p.split_k) == (want, split), (M, N, K, p.plan_id, p.split_k)
+
+
+def test_k_split_tile_needs_sixteen_byte_operands_and_k_multiple_of_64(ck):
+    rc, p = ck.abi.plan(1024, 1024, 1024, plan_override=10)
+    assert rc == 0 and p.plan_id == 10 and p.block_k == 64 and p.grid == 256
+    for kw in (dict(M=1024, N=1024, K=1000), dict(M=1024, N=1022, K=1024), dict(M=1024, N=1024, K=1056)):
+        rc, p = ck.abi.plan(workspace_bytes=1 << 40, plan_override=10, **kw)
+        assert rc == 0 and p.plan_id != 10, kw  # the override is ignored, the planner picks
 
 
 def _cover(ck, args, num_cus=256):

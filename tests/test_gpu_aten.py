@@ -115,14 +115,17 @@ def test_runs_on_current_stream(ck, orc, dev):
     assert_close(orc, C.cpu().numpy(), orc.gemm(a, b), 256, what="side stream")
 
 
-@pytest.mark.parametrize("M,K,N", [(300, 5000, 300), (512, 2048, 512), (1024, 1024, 1024), (256, 4096, 256),
-                                   (768, 3072, 768)])
-def test_small_deep_products_split_by_default(ck, orc, dev, M, K, N):
-    """Problems whose tiles leave most CUs idle are split along K by default
-    (down to 256 of K per split) with the workspace from the caching
-    allocator; the fixed-order reduction keeps repeated calls bitwise equal."""
+@pytest.mark.parametrize("M,K,N,cfg,split", [(300, 5000, 300, 1, 32), (512, 2048, 512, 10, 4),
+                                             (1024, 1024, 1024, 10, 1), (256, 4096, 256, 10, 16),
+                                             (768, 3072, 768, 10, 1)])
+def test_small_deep_products_split_by_default(ck, orc, dev, M, K, N, cfg, split):
+    """Problems whose 128 / 256 tiles would leave most CUs idle take small
+    tiles by default -- the 64-tile k-split config where K is a multiple of
+    64 -- split along K where those still do not fill the CUs, with the
+    workspace from the caching allocator; the fixed-order reductions (the
+    waves' partial tiles, the splits) keep repeated calls bitwise equal."""
     rc, p = ck.abi.plan(M, N, K, workspace_bytes=1 << 40)
-    assert rc == 0 and p.split_k > 1, (M, N, K, p.split_k)
+    assert rc == 0 and (p.plan_id, p.split_k) == (cfg, split), (M, N, K, p.plan_id, p.split_k)
     a, b = _u(orc, (M, K), 91), _u(orc, (K, N), 92)
     A, B = to_dev(a), to_dev(b)
     C1 = ck.p02.matmul_cuda(A, B)
@@ -139,7 +142,8 @@ def test_operators_replay_in_a_hip_graph(ck, dev):
     every replay bitwise equal to the eager results.  Covers the direct-staged
     256 and 128 tiles, split-K with its reduction (workspace), stream-K with
     its fixup on the 256 and 32-deep 128 tiles, the 32-deep tile data-parallel
-    and split, the chunked triangular list with its finishing pass, GEMV,
+    and split, the 64-tile k-split config alone and split, the chunked
+    triangular list with its finishing pass, GEMV,
     diag, pointwise conv and attention."""
     g = torch.Generator(device="cuda")
     g.manual_seed(97)
@@ -157,15 +161,20 @@ def test_operators_replay_in_a_hip_graph(ck, dev):
     sk3a, sk3b = u(3072, 8192), u(8192, 3072)
     sk9a, sk9b = u(1280, 8192), u(8192, 1280)
     d9a, d9b = u(2048, 2048), u(2048, 4096)
-    s9a, s9b = u(1024, 1024), u(1024, 1024)
-    for (m, kk, n), want in [((3072, 8192, 3072), (3, 1)), ((1280, 8192, 1280), (9, 1)),
-                             ((2048, 2048, 4096), (9, 0)), ((1024, 1024, 1024), (9, 0))]:
+    s9a, s9b = u(1024, 8192), u(8192, 2048)
+    # ... and the 64-tile k-split config, alone and split
+    k10a, k10b = u(1024, 1024), u(1024, 1024)
+    k10sa, k10sb = u(512, 8192), u(8192, 512)
+    for (m, kk, n), want in [((3072, 8192, 3072), (3, 1, 1)), ((1280, 8192, 1280), (9, 1, 1)),
+                             ((2048, 2048, 4096), (9, 0, 1)), ((1024, 8192, 2048), (9, 0, 4)),
+                             ((1024, 1024, 1024), (10, 0, 1)), ((512, 8192, 512), (10, 0, 4))]:
         rc, p = ck.abi.plan(m, n, kk, workspace_bytes=1 << 40)
-        assert rc == 0 and (p.plan_id, p.stream_k) == want, (m, kk, n, p.plan_id, p.stream_k)
+        assert rc == 0 and (p.plan_id, p.stream_k, p.split_k) == want, (m, kk, n, p.plan_id, p.stream_k,
+                                                                         p.split_k)
 
     def ops():
         return [ck.p02.matmul_cuda(sk3a, sk3b), ck.p02.matmul_cuda(sk9a, sk9b), ck.p02.matmul_cuda(d9a, d9b),
-                ck.p01.matmul_cuda(s9a, s9b),
+                ck.p02.matmul_cuda(s9a, s9b), ck.p01.matmul_cuda(k10a, k10b), ck.p02.matmul_cuda(k10sa, k10sb),
                 ck.p01.matmul_cuda(a4, b4), ck.p02.matmul_cuda(a2, b2), ck.p06.matmul_cuda(lka, lkb),
                 ck.p15.lower_tri_mul_cuda(ta, tb), ck.p04.gemv_cuda(ga, gx), ck.p12.diag_mult_cuda(dv, dm),
                 ck.p87.pointwise_conv_cuda(cx, cw, cb), ck.p97.fused_attention_cuda(q, k, v)]

@@ -39,9 +39,9 @@ def _pair(ck, orc, M, N, K, op_a, op_b, seed):
 
 @pytest.mark.parametrize("first,second", [
     ((256, 256, 1 << 18, 0, 0), (128, 192, 1 << 16, 0, 0)),   # split-K both times
-    ((1024, 1024, 1024, 0, 0), (520, 264, 1000, 1, 1)),      # small split-K, then odd T/T
+    ((512, 512, 8192, 0, 0), (520, 264, 1000, 1, 1)),        # k-split tile split 4, then odd T/T
     ((2048, 2048, 2048, 0, 1), (64, 64, 4096, 1, 0)),        # unsplit, then split-K
-    ((1280, 1280, 8192, 0, 0), (1024, 1024, 1024, 1, 0)),    # stream-K, then split-K
+    ((1280, 1280, 8192, 0, 0), (1024, 2048, 8192, 1, 0)),    # stream-K, then split-K
 ])
 def test_noalloc_matches_workspace_entry_point(ck, orc, dev, first, second):
     used = [_pair(ck, orc, *first, seed=1200), _pair(ck, orc, *second, seed=1300)]
