@@ -87,7 +87,9 @@ typedef struct {
     int32_t op_a, op_b;       /* mi_op */
     int32_t structure;        /* mi_structure; square, batch 1, N/N layouts */
     int32_t plan_override;    /* 0 = scheduler's choice; else (tests, tuning) bits 0-3 tile
-                                 config id, bits 8-19 split count, bits 20-30 raster group rows */
+                                 config id (mi_plan.plan_id), bit 4 stream-K where it applies,
+                                 bit 5 never stream-K, bits 8-19 split count, bits 20-30 raster
+                                 group rows; a config the problem cannot take is ignored */
     void* workspace;
     size_t workspace_bytes;
     const float* bias_m;      /* NULL, or M floats: C[b][i][j] = (sum over k) + bias_m[i],
