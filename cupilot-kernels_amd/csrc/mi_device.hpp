@@ -72,10 +72,14 @@ __host__ __device__ __forceinline__ bool tri_tile(int pid, int nt, bool lower, i
 // -- which lies in the zero triangle, so C itself holds the partial sum until
 // the finishing pass adds it in and zeroes the mirror.  Items run longest
 // first, so workgroups dispatched in order as CUs free up balance the load:
-// for l = cap, cap - 1, ..., 1 come the whole tiles of length l (distance
-// l - 1 from the diagonal), then (l == cap only) the first chunks of every
-// long tile, longest tile first, then the second chunks of length l.
-// Requires 2 cap >= nt (every second chunk is at most cap long).
+// for l = cap, cap - 1, ..., 1 come (l == cap only) the first chunks of
+// every long tile, longest tile first, then the second chunks of length l,
+// then the whole tiles of length l (distance l - 1 from the diagonal).  At
+// equal length a whole tile runs shorter -- the diagonal masks empty part
+// of both its first and last unit, a chunk's only one of them -- so the
+// list ends with the diagonal tiles (measured on 8192: 0.5-0.7 % faster
+// than whole tiles before chunks).  Requires 2 cap >= nt (every second
+// chunk is at most cap long).
 __host__ __device__ __forceinline__ int tri_items(int nt, int cap) {
     const int nl = nt > cap ? nt - cap : 0;
     return nt * (nt + 1) / 2 + nl * (nl + 1) / 2;
@@ -88,13 +92,6 @@ __host__ __device__ __forceinline__ void tri_item(int pid, int nt, int cap, bool
     int rem = pid, d = 0, r = 0, first = 0, len = 0;
     mirror = 0;
     for (int l = cap; l >= 1; --l) {
-        if (rem < nt - (l - 1)) {  // whole tiles of length l
-            d = l - 1;
-            r = rem;
-            len = l;
-            break;
-        }
-        rem -= nt - (l - 1);
         if (l == cap) {  // first chunks of the long tiles, L = nt down to cap + 1
             bool found = false;
             for (int L = nt; L > cap; --L) {
@@ -121,6 +118,13 @@ __host__ __device__ __forceinline__ void tri_item(int pid, int nt, int cap, bool
             }
             rem -= nt - L + 1;
         }
+        if (rem < nt - (l - 1)) {  // whole tiles of length l
+            d = l - 1;
+            r = rem;
+            len = l;
+            break;
+        }
+        rem -= nt - (l - 1);
     }
     tm = lower ? r + d : r;
     tn = lower ? r : r + d;

@@ -288,6 +288,15 @@ def test_triangular_chunked_work_list(ck, structure, n, override, cap):
         rc, tm, tn, kb, ke = ck.abi.tile_of(args, wg)
         lengths.append(ke - kb)
     assert all(x >= y for x, y in zip(lengths, lengths[1:])), "items must run longest first"
+    # at equal length the chunks (whose diagonal masks empty part of one unit)
+    # run before the whole tiles (part of two), so the list ends with the T
+    # diagonal tiles
+    kinds = []
+    for wg in range(p.num_tiles):
+        rc, tm, tn, kb, ke = ck.abi.tile_of(args, wg)
+        kinds.append((ke - kb, rc == 1 and ke - kb == (abs(tm - tn) + 1) * 256, tm == tn))
+    assert not any(a[0] == b[0] and a[1] and not b[1] for a, b in zip(kinds, kinds[1:]))
+    assert all(k[2] for k in kinds[-T:])
     # past the compute items: the zero tiles the workgroups write (rc 3) --
     # every zero-triangle tile that parks no partial (distance < cap), once,
     # except the counter's tile (0, 1) / (1, 0), which the finishing pass
