@@ -360,6 +360,19 @@ int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
         col_splits = std::min<int64_t>(tiles_n, std::max<int64_t>(1, cdiv(slots, tiles_m * batch)));
         grid = std::min<int64_t>(tiles_m * col_splits, std::max<int64_t>(1, slots / batch));
     }
+    // The direct-staged 128 tile with at least two waves of work items runs
+    // one tile per workgroup instead: a finished tile's stores then leave
+    // with its waves and do not hold up the next tile's slice waits (gfx9's
+    // vmcnt counts a wave's stores with its loads), while the other two
+    // workgroups on the CU cover the next one's start.  Measured in one
+    // process: 65536 x 512 x 256 129.9 vs 127.0 TFLOP/s, 8192^2 x 512 141.5
+    // vs 137.1, 16384^2 x 256 133.5 vs 127.2, 32768 x 1024 x 192 122.7 vs
+    // 118.9; with about one wave (4096^2 x 512, 16384 x 768 x 512) equal.
+    // (The 256 and 32-deep 128 tiles, one and two workgroups per CU, lose
+    // 2 % that way on 65536 x 512 x 256.)
+    if (best_cfg == kCfg128 && a.structure == MI_DENSE && choose_vec(a) == 4 && a.K % 16 == 0 &&
+        num_tiles * best_split * batch >= 2 * slots)
+        grid = num_tiles;
     // Stream-K: every resident workgroup takes part (its K-slice range),
     // whatever the tile count.
     if (best_sk.tiles > 0) grid = best_sk.grid;
