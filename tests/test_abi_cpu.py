@@ -188,6 +188,21 @@ def test_plan_small_problems_take_the_k_split_tile(ck, M, N, K, want, split):
     assert rc == 0 and (p.plan_id, p.split_k) == (want, split), (M, N, K, p.plan_id, p.split_k)
 
 
+@pytest.mark.parametrize("M,N,K,cfg,grid", [
+    (65536, 512, 256, 2, 2048),      # 2048 tiles of 128: 2.7 waves of 768 -> one tile per workgroup
+    (16384, 16384, 256, 2, 16384),
+    (16384, 768, 2048, 2, 768),      # one wave: the persistent grid (the same 768)
+    (4096, 4096, 512, 2, 768),       # 1.3 waves: persistent
+    (8192, 8192, 8192, 3, 256),      # the 256 tile stays persistent
+])
+def test_many_wave_128_tile_plans_run_one_tile_per_workgroup(ck, M, N, K, cfg, grid):
+    """With two or more waves of 128-tile work items the grid is one
+    workgroup per tile (a tile's stores then leave with its waves; measured
+    faster on MI355X), otherwise the persistent grid of resident workgroups."""
+    rc, p = ck.abi.plan(M, N, K, workspace_bytes=1 << 40)
+    assert rc == 0 and (p.plan_id, p.grid) == (cfg, grid), (M, N, K, p.plan_id, p.grid)
+
+
 def test_k_split_tile_needs_sixteen_byte_operands_and_k_multiple_of_64(ck):
     rc, p = ck.abi.plan(1024, 1024, 1024, plan_override=10)
     assert rc == 0 and p.plan_id == 10 and p.block_k == 64 and p.grid == 256
