@@ -21,7 +21,8 @@
 //   * at the end the eight partial tiles go through LDS (two per stage
 //     buffer, 16-byte chunks XOR-swizzled by row, conflict-free both ways) and are
 //     added in wave order 0 .. 7, a fixed order, so results are deterministic.
-// Persistent: workgroup b walks tiles b, b + grid, ... (XCD-aware raster).
+// Persistent: workgroup b walks tiles b, b + grid, ... (XCD-aware raster),
+// or its stream-K items.
 #pragma once
 
 #include "gemm_direct.hpp"
@@ -36,9 +37,14 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-template <bool AT, bool BT, bool BIAS>
+// SK: the stream-K schedule (sk_work): workgroup b runs its items 0, 1, ...
+// -- whole tiles, then the segments of its K-slice range -- and stores a
+// segment that does not start at k = 0 into its workspace slot
+// (xcd_remap(b, grid), 64 x 64, tile-local) for sk_fixup to add in.
+template <bool AT, bool BT, bool BIAS, bool SK = false>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
     gemm_f32_ksplit_kernel(const GemmParams p) {
+    static_assert(!SK || !BIAS, "stream-K: no bias");
     constexpr int BM = 64, BK = 64, NW = 8;
     constexpr bool A_KC = !AT;  // A row-major (M x K) is contiguous along K
     constexpr bool B_KC = BT;   // B stored N x K is contiguous along K
@@ -84,9 +90,22 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     };
 
     uint32_t voA[LA::PER_WAVE], voB[LB::PER_WAVE];
-    for (int t = blockIdx.x; t < p.num_tiles; t += gridDim.x) {
+    // stream-K: this workgroup's workspace slot
+    float* const sk_slot = SK ? p.ws + (int64_t)xcd_remap(blockIdx.x, gridDim.x) * (BM * BM) : nullptr;
+    for (int t = SK ? 0 : blockIdx.x;; t += SK ? 1 : gridDim.x) {
         int tm, tn, k_begin, k_end;
-        tile_of<BM, BM, kDense>(p, t, p.num_tiles, blockIdx.y, tm, tn, k_begin, k_end);
+        bool to_slot = false;
+        if constexpr (SK) {
+            int lt, s0, s1, to_ws;
+            if (!sk_work(blockIdx.x, t, gridDim.x, p.sk_dp, p.sk_tiles, p.sk_ipt, lt, s0, s1, to_ws)) break;
+            raster(lt, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
+            k_begin = s0 * BK;
+            k_end = s1 * BK;
+            to_slot = to_ws != 0;
+        } else {
+            if (t >= p.num_tiles) break;
+            tile_of<BM, BM, kDense>(p, t, p.num_tiles, blockIdx.y, tm, tn, k_begin, k_end);
+        }
         // (the planner takes this config only with K and the split chunk
         // multiples of 64: every slice is full)
         const int ns = (k_end - k_begin) / BK;
@@ -222,8 +241,10 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
                 if (add_bias) v += bv;
                 const int col = tn * BM + 4 * c;
                 if (row < p.M) {
-                    float* const dst = C + (int64_t)row * ldc + col;
-                    if (c_vec && col + 3 < p.N) {
+                    // (a stream-K segment that does not start at k = 0: its
+                    // slot, tile-local, row stride BM, 16-byte aligned)
+                    float* const dst = to_slot ? sk_slot + r * BM + 4 * c : C + (int64_t)row * ldc + col;
+                    if ((to_slot || c_vec) && col + 3 < p.N) {
                         *reinterpret_cast<f4*>(dst) = v;
                     } else {
 #pragma unroll
@@ -240,6 +261,13 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
 template <bool AT, bool BT>
 inline hipError_t launch_ksplit(const GemmLaunch& g, hipStream_t s) {
     const GemmParams p = make_params(g);
+    if (g.sk_tiles > 0) {  // stream-K (the scheduler plans it for batch 1, split 1, no bias)
+        hipLaunchKernelGGL((gemm_f32_ksplit_kernel<AT, BT, false, true>), dim3((unsigned)g.grid_x),
+                           dim3(512), 0, s, p);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        return launch_sk_fixup(g, s);
+    }
     dim3 grid((unsigned)g.grid_x, (unsigned)g.split_k, (unsigned)g.batch);
     if constexpr (!AT && !BT) {  // the row bias exists for N/N only
         if (g.bias != nullptr && g.split_k == 1) {

@@ -35,36 +35,38 @@ struct CfgModel {
     double item_ns;        // fixed cost per work item of a workgroup
     double store_exp[2];   // fraction of the output store time left exposed with
                            // 1 and >= 2 workgroups per CU
+    double sk_eff;         // stream-K: efficiency relative to eff (each segment restarts
+                           // the k-split tile's four-stage ring)
 };
 
-// Cost model of a dense plan, fitted to 2814 MI355X timings of candidate
+// Cost model of a dense plan, fitted to 2874 MI355X timings of candidate
 // plans -- 64 / 128 / 32-deep 128 / 256 tiles, the 64-tile k-split config,
 // split-K 1 - 32, stream-K -- over 141 shapes from 256 x 512 x 4096 to
 // 8192 x 3072 x 16384, N/N plus all four layouts of 12 of them
 // (tests/data/plan_timings_mi355x.csv, fitted by plan_fit.py: a local search
 // on the ranking from the previous constants).  The plan it picks is on
-// average 0.8 % slower than the fastest one measured, at most 10.5 %.  The
+// average 0.9 % slower than the fastest one measured, at most 11 %.  The
 // single-slice configs (K <= 32 / 64) take the 128 tile's constants with half
 // its exposed store time.
 constexpr CfgModel kModels[] = {
-    {kCfg256, {0.950, 0.950, 0.950}, 559.0, {1.495, 1.495}},
-    {kCfg128, {0.823, 0.910, 0.918}, 3838.0, {0.873, 0.517}},
-    {kCfg64, {0.430, 0.638, 0.707}, 2691.0, {0.873, 0.517}},
-    {kCfg128K32, {0.823, 0.910, 0.918}, 0.0, {0.44, 0.26}},
-    {kCfg128K64, {0.823, 0.910, 0.918}, 0.0, {0.44, 0.26}},
-    {kCfg128B32, {0.849, 0.913, 0.913}, 4233.0, {0.873, 0.517}},
-    {kCfg64W, {0.859, 0.859, 0.859}, 2893.0, {0.874, 0.874}},
+    {kCfg256, {0.947, 0.947, 0.947}, 220.0, {1.38, 1.38}, 1.0},
+    {kCfg128, {0.821, 0.907, 0.915}, 3393.0, {0.935, 0.495}, 1.0},
+    {kCfg64, {0.433, 0.642, 0.718}, 2937.0, {0.935, 0.495}, 1.0},
+    {kCfg128K32, {0.821, 0.907, 0.915}, 0.0, {0.47, 0.25}, 1.0},
+    {kCfg128K64, {0.821, 0.907, 0.915}, 0.0, {0.47, 0.25}, 1.0},
+    {kCfg128B32, {0.850, 0.914, 0.914}, 4286.0, {0.935, 0.495}, 1.0},
+    {kCfg64W, {0.850, 0.850, 0.850}, 2361.0, {0.733, 0.733}, 0.798},
 };
 
 constexpr double kPeakFlopsPerCuNs = 256.0 * 2.4;  // fp32 MFMA flop per ns per CU
 constexpr double kWriteBytesPerNs = 5500.0;        // sustained write-only bandwidth (measured)
 // split-K reduction and stream-K fixup passes: bytes per ns over what they
 // read and write, plus a fixed cost per reduction pass
-constexpr double kReduceBytesPerNs = 8296.0;
-constexpr double kReduceNs = 5467.0;
+constexpr double kReduceBytesPerNs = 7661.0;
+constexpr double kReduceNs = 5354.0;
 // stream-K: the fixup workgroup of a tile adds its G / S partials one after
 // another (G workgroups, S stream-K tiles)
-constexpr double kSkSlotNs = 953.0;
+constexpr double kSkSlotNs = 930.0;
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
@@ -132,7 +134,7 @@ namespace {
 
 // Stream-K schedule of a dense product on config cfg (sk_work in
 // mi_device.hpp), or sk.tiles = 0 where it does not apply: batch 1, no bias,
-// the direct-staged 16-byte kernel (every K-slice full), a tile count that
+// the direct-staged 16-byte kernels (every K-slice full), a tile count that
 // whole waves of the persistent grid do not cover exactly, at least two
 // slices per workgroup, and a workspace for one partial tile per workgroup.
 struct SkChoice {
@@ -142,7 +144,7 @@ struct SkChoice {
 
 SkChoice plan_stream_k(const mi_gemm_args& a, int cfg, int num_cus) {
     SkChoice sk;
-    if (cfg != kCfg256 && cfg != kCfg128 && cfg != kCfg128B32) return sk;
+    if (cfg != kCfg256 && cfg != kCfg128 && cfg != kCfg128B32 && cfg != kCfg64W) return sk;
     if (a.structure != MI_DENSE || a.batch > 1 || a.bias_m != nullptr) return sk;
     if (((uintptr_t)a.workspace & 15u) != 0) return sk;
     const CfgInfo ci = cfg_info(cfg);
@@ -156,7 +158,9 @@ SkChoice plan_stream_k(const mi_gemm_args& a, int cfg, int num_cus) {
     g.op_b = a.op_b;
     g.lda = a.lda;
     g.ldb = a.ldb;
-    if (a.K <= 0 || !direct_ok(g)) return sk;
+    const bool staged = cfg == kCfg64W ? ksplit_ok(a.structure, g.vec, a.K, a.K, a.lda, a.ldb)
+                                       : direct_ok(g);
+    if (a.K <= 0 || !staged) return sk;
     const int64_t T = cdiv(a.M, ci.bm) * cdiv(a.N, ci.bn);
     const int64_t G = (int64_t)num_cus * resident_wgs(cfg);
     if (G % 8 != 0 || T % G == 0) return sk;
@@ -280,8 +284,10 @@ int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
             for (int s = 1; s <= 1024; s *= 2) {
                 if (s > 1) {
                     // split only to fill the machine, with >= kMinSplitK of K per
-                    // split: up to twice the CUs in items
-                    if (tiles * (s / 2) >= 2 * (int64_t)num_cus) break;
+                    // split: while the previous split's items stay below four
+                    // times the CUs (the k-split 64 tile, one workgroup per CU,
+                    // measured fastest at 4.5 items per CU: 3620 x 296 x 6144)
+                    if (tiles * (s / 2) >= 4 * (int64_t)num_cus) break;
                     if (a.K / s < kMinSplitK) break;
                     const size_t need = (size_t)s * batch * a.M * a.N * sizeof(float);
                     if (a.workspace_bytes < need) break;
@@ -311,7 +317,7 @@ int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
             // and write the split tiles of C).
             const SkChoice sk = no_sk ? SkChoice{} : plan_stream_k(a, m.id, num_cus);
             if (sk.tiles > 0) {
-                const double eff = scale * m.eff[std::min(res, 3) - 1];
+                const double eff = scale * m.sk_eff * m.eff[std::min(res, 3) - 1];
                 double t = (double)tiles * 2.0 * ci.bm * ci.bn * (double)a.K / num_cus /
                            (eff * kPeakFlopsPerCuNs);
                 t += (double)(sk.dp / sk.grid + 2) * m.item_ns;

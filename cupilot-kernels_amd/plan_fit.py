@@ -8,7 +8,8 @@ the table):
            + store_exp[cfg][occ > 1] * out_bytes * split / write bandwidth
            + (split > 1) * ((split + 1) * out_bytes / reduce bandwidth + reduce_ns)
   stream-K: the work spread over every resident workgroup, (dp / G + 2) items,
-           partial tiles stored and read back three times, sk_slot_ns * G / S.
+           partial tiles stored and read back three times, sk_slot_ns * G / S; on the
+           k-split 64 tile its own efficiency factor and fixed cost (sk10_eff, sk10_ns).
 Fit: a random local search on the ranking (mean regret of the plan the model
 picks + 0.1 x worst regret + 0.2 x rms log error, plans within 15 % of a
 shape's best weighing 4x in the rms) from the constants scheduler.cpp
@@ -35,12 +36,12 @@ BK = {1: 16, 2: 16, 3: 32, 9: 32, 10: 64}
 RES = {1: 8, 2: 3, 3: 1, 9: 2, 10: 1}
 NAMES = ["e1_1", "e1_2", "e1_3", "e2_1", "e2_2", "e2_3", "e3", "e9_1", "e9_2",
          "o1", "o2", "o3", "o9", "x3", "x_occ1", "x_occ2", "reduce_bw", "reduce_ns", "sk_slot_ns",
-         "e10", "o10", "x10"]
+         "e10", "o10", "x10", "sk10_eff", "sk10_ns"]
 # the constants csrc/scheduler.cpp carries (the starting point of the search)
-X0 = [0.430, 0.638, 0.707, 0.823, 0.910, 0.918, 0.950, 0.849, 0.913, 2691, 3838, 559, 4233, 1.495, 0.873,
-      0.517, 8296, 5467, 953, 0.859, 2893, 0.874]
-LO = [0.2] * 9 + [0.0] * 4 + [0.0, 0.0, 0.0, 1000, 0, 0] + [0.2, 0.0, 0.0]
-HI = [1.2] * 9 + [5e4] * 4 + [1.5, 1.5, 1.5, 2e4, 5e4, 5e4] + [1.2, 5e4, 1.5]
+X0 = [0.433, 0.642, 0.718, 0.821, 0.907, 0.915, 0.947, 0.850, 0.914, 2937, 3393, 220, 4286, 1.38, 0.935,
+      0.495, 7661, 5354, 930, 0.850, 2361, 0.733, 0.798, 0.0]
+LO = [0.2] * 9 + [0.0] * 4 + [0.0, 0.0, 0.0, 1000, 0, 0] + [0.2, 0.0, 0.0, 0.3, 0.0]
+HI = [1.2] * 9 + [5e4] * 4 + [1.5, 1.5, 1.5, 2e4, 5e4, 5e4] + [1.2, 5e4, 1.5, 1.2, 5e4]
 
 
 def cdiv(a, b):
@@ -65,7 +66,9 @@ def model(r, x):
         dp = (waves - 1) * G if waves >= 1 else 0
         S = T - dp
         tile = 4.0 * bm * bm
-        t = T * 2.0 * bm * bm * K / NC / (scale * eff[min(RES[c], 3) - 1] * PEAK)
+        ske = P["sk10_eff"] if c == 10 else 1.0
+        t = T * 2.0 * bm * bm * K / NC / (scale * ske * eff[min(RES[c], 3) - 1] * PEAK)
+        t += P["sk10_ns"] if c == 10 else 0.0
         t += (dp // G + 2) * o
         t += xs[1 if RES[c] > 1 else 0] * (out + G * tile) / WRITE
         t += 3.0 * G * tile / P["reduce_bw"] + P["sk_slot_ns"] * G / S

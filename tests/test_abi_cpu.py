@@ -473,6 +473,8 @@ def _sk_cover(ck, args, num_cus=256):
     (1024, 1024, 1024, 2, (0, 0)),    # 64 tiles over 768 workgroups: many segments per tile
     (1000, 1000, 4096, 3, (0, 1)),    # ragged edges
     (33000, 1000, 1024, 2, (0, 0)),   # 2072 tiles
+    (1536, 1536, 1024, 10, (0, 0)),   # k-split 64 tile: 576 tiles, 256 data-parallel + 320 stream-K
+    (640, 640, 2048, 10, (1, 1)),     # 100 tiles of 64 over 256 workgroups
 ])
 def test_stream_k_schedule_covers_every_tile_once(ck, M, N, K, cfg, ops):
     args = ck.abi.make_args(M, N, K, op_a=ops[0], op_b=ops[1], workspace_bytes=1 << 40,

@@ -1,5 +1,5 @@
 """Stream-K schedule on the GPU, through the C ABI: parity with the fp64 oracle
-in every layout on both direct-staged tiles, tiles split over many workgroups
+in every layout on the direct-staged 256 and 128 tiles and the k-split 64 tile, tiles split over many workgroups
 and ragged edges, a data-parallel wave ahead of the stream-K tiles, bitwise
 repeatability (the fixup adds partials in a fixed order), and agreement with
 the data-parallel plan of the same problem.
@@ -47,6 +47,8 @@ def _plan(ck, M, N, K, op_a, op_b, override):
     (1000, 1000, 4096, 3),   # ragged edges on the 256 tile
     (640, 640, 2048, 2),     # 25 tiles of 128 over 768 workgroups
     (1000, 1100, 1024, 2),   # ragged edges on the 128 tile
+    (640, 640, 2048, 10),    # 100 tiles of 64 over 256 workgroups (the k-split 64 tile)
+    (1000, 1100, 1024, 10),  # ragged edges: 288 tiles, one data-parallel wave + 32 stream-K
 ])
 def test_stream_k_parity(ck, orc, dev, op_a, op_b, M, N, K, cfg):
     p = _plan(ck, M, N, K, op_a, op_b, cfg | SK_FORCE)
@@ -61,6 +63,7 @@ def test_stream_k_parity(ck, orc, dev, op_a, op_b, M, N, K, cfg):
     (5760, 5120, 256, 2, (0, 0)),    # 1800 tiles: one data-parallel wave (768) + 1032 stream-K
     (5120, 5120, 2048, 3, (1, 1)),   # 400 tiles of 256: 1.56 tiles per workgroup
     (3584, 3584, 1024, 3, (0, 1)),   # 196 tiles < 256 workgroups
+    (1536, 1536, 2048, 10, (1, 0)),  # 576 tiles of 64: 256 data-parallel + 320 stream-K
 ])
 def test_stream_k_larger_every_element(ck, orc, dev, M, N, K, cfg, ops):
     """Bigger stream-K schedules, every element through fp64 row and column
@@ -79,7 +82,7 @@ def test_stream_k_larger_every_element(ck, orc, dev, M, N, K, cfg, ops):
              f"stream-K {M}x{N}x{K} every element")
 
 
-@pytest.mark.parametrize("M,N,K,cfg", [(1280, 1280, 2048, 3), (640, 640, 2048, 2)])
+@pytest.mark.parametrize("M,N,K,cfg", [(1280, 1280, 2048, 3), (640, 640, 2048, 2), (640, 640, 2048, 10)])
 def test_stream_k_bitwise_repeatable(ck, orc, dev, M, N, K, cfg):
     """20 runs, bitwise identical: every partial tile is added in slot order."""
     a_st, b_st, _, _ = _operands(orc, M, N, K, 0, 0, seed=4300)
@@ -89,7 +92,7 @@ def test_stream_k_bitwise_repeatable(ck, orc, dev, M, N, K, cfg):
         np.testing.assert_array_equal(to_host(_run(ck, A, B, M, N, K, 0, 0, cfg | SK_FORCE)), first)
 
 
-@pytest.mark.parametrize("M,N,K,cfg", [(1280, 1280, 2048, 3), (640, 640, 2048, 2)])
+@pytest.mark.parametrize("M,N,K,cfg", [(1280, 1280, 2048, 3), (640, 640, 2048, 2), (640, 640, 2048, 10)])
 def test_stream_k_integer_inputs_exact(ck, orc, dev, M, N, K, cfg):
     """Integer-valued inputs: every partial sum is an exact integer, so the
     stream-K result equals the data-parallel one bit for bit."""
