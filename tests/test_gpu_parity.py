@@ -60,6 +60,35 @@ def test_gemm_layouts_auto_plan(ck, orc, dev, op_a, op_b, M, N, K):
                  f"layout {op_a}{op_b} {M}x{N}x{K}")
 
 
+def _random_shapes(n, seed):
+    """Seeded small-to-mid problems whose plans the planner picks freely:
+    16-byte rows, K a multiple of 64 (so the k-split tile, split-K and
+    stream-K all compete), random layouts."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        M, N = (int(4 * rng.integers(16, 250)) for _ in range(2))
+        K = int(64 * rng.integers(1, 48))
+        out.append((M, N, K, int(rng.integers(0, 2)), int(rng.integers(0, 2))))
+    return out
+
+
+@pytest.mark.parametrize("M,N,K,op_a,op_b", _random_shapes(12, 2026))
+def test_random_shapes_auto_plan(ck, orc, dev, M, N, K, op_a, op_b):
+    """Whatever the planner picks for these (data-parallel, split-K or
+    stream-K, on any tile), the result matches the oracle."""
+    rc, p = ck.abi.plan(M, N, K, op_a=op_a, op_b=op_b, workspace_bytes=1 << 40)
+    assert rc == 0
+    a_st, b_st = _host_operands(orc, M, N, K, op_a, op_b, seed=M + N + K)
+    A, B = to_dev(a_st), to_dev(b_st)
+    C = torch.full((M, N), float("nan"), device="cuda")
+    ws = workspace(ck, gemm_args(ck, A, B, C, M, N, K, op_a, op_b))
+    ck.abi.check(run_gemm(ck, gemm_args(ck, A, B, C, M, N, K, op_a, op_b, ws=ws)))
+    ref = orc.gemm(_logical(a_st, op_a), _logical(b_st, op_b))
+    assert_close(orc, to_host(C), ref, K, np.abs(a_st).max(), np.abs(b_st).max(),
+                 f"auto plan {p.plan_id}/{p.split_k}/{p.stream_k} {op_a}{op_b} {M}x{N}x{K}")
+
+
 @pytest.mark.parametrize("op_a,op_b", LAYOUTS)
 @pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5, 6, 7])
 @pytest.mark.parametrize("M,N,K", [(512, 512, 512), (300, 200, 100), (64, 640, 37), (700, 520, 31),
