@@ -7,10 +7,10 @@
 // Structure of one workgroup (8 waves, one workgroup per CU):
 //   * K is walked in 64-deep slices staged straight into LDS (buffer_load
 //     ... lds, DirectLoader's 64-row layouts) through a ring of four stage
-//     buffers per operand: the loads of slice i + 3 are issued while slice i
-//     is computed, so each slice's loads have three slice times (~2.5 us) to
-//     arrive from HBM -- every slice is new data for the whole chip, since all
-//     workgroups walk K in step;
+//     buffers (A's slice, then B's, in each): the loads of slice i + 3 are
+//     issued while slice i is computed, so each slice's loads have three slice
+//     times (~2.5 us) to arrive from HBM -- every slice is new data for the
+//     whole chip, since all workgroups walk K in step;
 //   * wave w takes k-block w (k 8w .. 8w + 7) of every slice and the whole
 //     64 x 64 tile (2 x 2 MFMA blocks, 16 v_mfma_f32_32x32x2_f32 per slice):
 //     four independent accumulators per wave, one 16-byte fragment read per
