@@ -19,9 +19,12 @@ time of the same torch operator.
 Shapes (``--preset baseline``) are BASELINE's configs where one names the
 operator, else the reference's own literal extents (PID 2, kernels/2_...:16-18)
 or a stated synthetic shape.  Inputs are uniform[-1, 1) from the library's
-counter-based generator, resident in HBM before timing; latency is the mean
-of ``--reps`` calls between HIP events on the current stream after
-``--warmup`` calls, output allocation included (as KernelBench times a call).
+counter-based generator, resident in HBM before timing.  Both operators get
+``--warmup`` untimed calls; then ``--rounds`` rounds alternate them, each
+round timing ``--reps`` calls of one and then of the other between HIP events
+on the current stream (the order flips every round, so neither always runs
+first); a latency is the median over the rounds of the mean per call, output
+allocation included (as KernelBench times a call).
 With ``--cpu`` the host torch operator is timed on the same inputs (best of 3
 calls after one warm-up call, all host threads) after every GPU timing.
 """
@@ -174,12 +177,10 @@ def _problems(ck, preset: str) -> List[Problem]:
     return P
 
 
-def _time_gpu(fn, args, warmup: int, reps: int) -> float:
+def _time_reps(fn, args, reps: int) -> float:
+    """Mean ms per call of ``reps`` back-to-back calls between HIP events."""
     import torch
     stream = torch.cuda.current_stream()
-    for _ in range(warmup):
-        fn(*args)
-    torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
     for _ in range(reps):
@@ -187,6 +188,27 @@ def _time_gpu(fn, args, warmup: int, reps: int) -> float:
     e1.record(stream)
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / reps
+
+
+def _time_pair(ref, ours, args, warmup: int, reps: int, rounds: int):
+    """(torch ms, ours ms): warm-up calls of both, then ``rounds`` rounds that
+    time ``reps`` calls of each, alternating which goes first; the median
+    over the rounds of each one's mean per call."""
+    import statistics
+    import torch
+    for fn in (ref, ours):
+        for _ in range(warmup):
+            fn(*args)
+    torch.cuda.synchronize()
+    t_ref, t_ours = [], []
+    for r in range(max(1, rounds)):
+        if r % 2 == 0:
+            t_ref.append(_time_reps(ref, args, reps))
+            t_ours.append(_time_reps(ours, args, reps))
+        else:
+            t_ours.append(_time_reps(ours, args, reps))
+            t_ref.append(_time_reps(ref, args, reps))
+    return statistics.median(t_ref), statistics.median(t_ours)
 
 
 def _norm_diff(got, ref, inputs, k: int) -> float:
@@ -201,7 +223,7 @@ def _norm_diff(got, ref, inputs, k: int) -> float:
 
 
 def run(pids: Optional[Sequence[int]] = None, preset: str = "baseline", warmup: int = 3,
-        reps: int = 10, cpu: bool = False, log=print) -> List[Dict[str, object]]:
+        reps: int = 10, cpu: bool = False, log=print, rounds: int = 5) -> List[Dict[str, object]]:
     """Measure every problem (or ``pids``); returns one row dict per problem."""
     import ctypes
     import torch
@@ -225,8 +247,7 @@ def run(pids: Optional[Sequence[int]] = None, preset: str = "baseline", warmup: 
     for p in todo:
         inputs = p.make(u)
         torch.cuda.synchronize()
-        t_ref = _time_gpu(p.torch_ref, inputs, warmup, reps)
-        t_ours = _time_gpu(p.ours, inputs, warmup, reps)
+        t_ref, t_ours = _time_pair(p.torch_ref, p.ours, inputs, warmup, reps, rounds)
         got, ref = p.ours(*inputs), p.torch_ref(*inputs)
         torch.cuda.synchronize()
         diff = _norm_diff(got, ref, inputs, p.k_norm)
@@ -300,11 +321,13 @@ def main(argv=None) -> int:
     ap.add_argument("--preset", choices=["baseline", "small"], default="baseline")
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--reps", type=int, default=10)
+    ap.add_argument("--rounds", type=int, default=5,
+                    help="alternating timing rounds per operator (median reported)")
     ap.add_argument("--cpu", action="store_true", help="also time the torch operator on the host")
     a = ap.parse_args(argv)
     pids = [int(x) for x in a.pids.split(",") if x.strip()]
     rows = run(pids, a.preset, a.warmup, a.reps, a.cpu,
-               log=lambda m: print(m, file=sys.stderr, flush=True))
+               log=lambda m: print(m, file=sys.stderr, flush=True), rounds=a.rounds)
     write_csv(rows, a.out)
     root, ext = os.path.splitext(a.out)
     write_csv(rows, root + "_ext" + (ext or ".csv"), extended=True)

@@ -51,3 +51,26 @@ def test_refuses_without_device(ev):
         pytest.skip("a device is present")
     with pytest.raises(RuntimeError, match="HIP device"):
         ev.run([1])
+
+
+def test_timing_rounds_alternate_and_report_medians(ev, monkeypatch):
+    """Both operators are warmed up, then timed in rounds whose order flips
+    every round (neither always runs first); each latency is the median of its
+    rounds, so one disturbed round does not move it."""
+    import torch
+    calls, order = [], []
+    ref = lambda: calls.append("ref")
+    ours = lambda: calls.append("ours")
+    samples = {"ref": iter([5.0, 1.0, 2.0, 3.0, 2.5]), "ours": iter([1.0, 1.5, 9.0, 1.2, 1.1])}
+
+    def fake_time(fn, args, reps):
+        name = "ref" if fn is ref else "ours"
+        order.append(name)
+        return next(samples[name])
+
+    monkeypatch.setattr(ev, "_time_reps", fake_time)
+    monkeypatch.setattr(torch.cuda, "synchronize", lambda *a, **k: None)
+    t_ref, t_ours = ev._time_pair(ref, ours, (), warmup=2, reps=10, rounds=5)
+    assert calls == ["ref", "ref", "ours", "ours"]
+    assert order == ["ref", "ours", "ours", "ref", "ref", "ours", "ours", "ref", "ref", "ours"]
+    assert (t_ref, t_ours) == (2.5, 1.2)
