@@ -205,7 +205,7 @@ int mi_gemm_work_item(const mi_gemm_args* args, int32_t num_cus, int64_t wg, int
         out->tile_m = tm;
         out->tile_n = tn;
         out->k_begin = (int64_t)s0 * ci.bk;
-        out->k_end = (int64_t)s1 * ci.bk;
+        out->k_end = std::min<int64_t>((int64_t)s1 * ci.bk, g.K);  // (4-byte staging: last slice partial)
         out->dest = to_ws;
         out->slot = to_ws ? xcd_remap((int)wg, g.grid_x) : 0;
         return 1;

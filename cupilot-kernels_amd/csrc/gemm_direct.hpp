@@ -347,7 +347,9 @@ __device__ __forceinline__ void store_tile_direct(const GemmParams& p, float* C,
 // SK: the stream-K schedule (sk_work): workgroup b runs its items 0, 1, ...
 // -- whole tiles, then the segments of its K-slice range -- and stores a
 // segment that does not start at k = 0 into its workspace slot
-// (xcd_remap(b, grid)), tile-local, for sk_fixup to add in.
+// (xcd_remap(b, grid)), tile-local, for sk_fixup to add in.  With 4-byte
+// staging (128 tile) a tile's last slice may be partial: the segment that
+// holds it ends at K.
 template <class T, bool AT, bool BT, bool BIAS, int MODE = kDense, int VB = 16, bool SK = false>
 __global__ void __launch_bounds__(T::NT)
     __attribute__((amdgpu_waves_per_eu(T::WAVES_PER_SIMD, T::WAVES_PER_SIMD)))
@@ -355,7 +357,8 @@ __global__ void __launch_bounds__(T::NT)
     static_assert(T::STAGES == 2 && T::BM == T::BN, "double-buffered square tiles");
     static_assert(MODE == kDense || (!AT && !BT && T::BM == 256 && VB == 16),
                   "triangular products are N/N on the 256 tile");
-    static_assert(!SK || (MODE == kDense && VB == 16 && !BIAS), "stream-K: dense, 16-byte, no bias");
+    static_assert(!SK || (MODE == kDense && !BIAS && (VB == 16 || T::BM == 128)),
+                  "stream-K: dense, no bias; 4-byte staging on the 128 tile only");
     constexpr bool A_KC = !AT;  // A row-major (M x K) is contiguous along K
     constexpr bool B_KC = BT;   // B stored N x K is contiguous along K
     using LA = DirectLoader<A_KC, T::NW, T::BM, T::BK, VB>;
@@ -430,7 +433,8 @@ __global__ void __launch_bounds__(T::NT)
             if (!w.compute) lt = s0 = s1 = to_ws = 0;
             raster(lt, p.tiles_m, p.tiles_n, p.group_m, w.tm, w.tn);
             w.k_begin = s0 * T::BK;
-            w.k_end = s1 * T::BK;
+            // (4-byte staging: the tile's last slice may end past K)
+            w.k_end = s1 * T::BK < p.K ? s1 * T::BK : p.K;
             w.nk = s1 - s0;
             w.mirror = to_ws;
             return w;
@@ -784,9 +788,9 @@ template <class T, bool AT, bool BT, int VB>
 inline hipError_t launch_direct_tile(const GemmLaunch& g, hipStream_t s) {
     const GemmParams p = make_params(g);
     dim3 grid((unsigned)g.grid_x, (unsigned)g.split_k, (unsigned)g.batch);
-    if constexpr (VB == 16) {
+    if constexpr (VB == 16 || T::BM == 128) {
         if (g.sk_tiles > 0) {  // stream-K (the scheduler plans it for batch 1, split 1, no bias)
-            hipLaunchKernelGGL((gemm_f32_direct_kernel<T, AT, BT, false, kDense, 16, true>),
+            hipLaunchKernelGGL((gemm_f32_direct_kernel<T, AT, BT, false, kDense, VB, true>),
                                dim3((unsigned)g.grid_x), dim3(T::NT), 0, s, p);
             const hipError_t e = hipGetLastError();
             if (e != hipSuccess) return e;

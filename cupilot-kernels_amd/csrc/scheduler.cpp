@@ -39,15 +39,16 @@ struct CfgModel {
                            // the k-split tile's four-stage ring)
 };
 
-// Cost model of a dense plan, fitted to 2874 MI355X timings of candidate
+// Cost model of a dense plan, fitted to 3810 MI355X timings of candidate
 // plans -- 64 / 128 / 32-deep 128 / 256 tiles, the 64-tile k-split config,
-// split-K 1 - 32, stream-K -- over 141 shapes from 256 x 512 x 4096 to
-// 8192 x 3072 x 16384, N/N plus all four layouts of 12 of them
-// (tests/data/plan_timings_mi355x.csv, fitted by plan_fit.py: a local search
-// on the ranking from the previous constants).  The plan it picks is on
-// average 0.9 % slower than the fastest one measured, at most 11 %.  The
-// single-slice configs (K <= 32 / 64) take the 128 tile's constants with half
-// its exposed store time.
+// split-K 1 - 32, stream-K -- over 213 shapes from 256 x 512 x 4096 to
+// 8192 x 3072 x 16384: 141 with 16-byte operand rows, N/N plus all four
+// layouts of 12 of them, and 72 random ones in all four layouts whose rows or
+// K are not multiples of 4 floats (or K of 16) (tests/data/plan_timings_mi355x.csv,
+// fitted by plan_fit.py: a local search on the ranking from the previous
+// constants).  The plan it picks is on average 1.3 % slower than the fastest
+// one measured.  The single-slice configs (K <= 32 / 64) take the 128 tile's
+// constants with half its exposed store time.
 constexpr CfgModel kModels[] = {
     {kCfg256, {0.947, 0.947, 0.947}, 220.0, {1.38, 1.38}, 1.0},
     {kCfg128, {0.821, 0.907, 0.915}, 3393.0, {0.935, 0.495}, 1.0},
@@ -67,6 +68,22 @@ constexpr double kReduceNs = 5354.0;
 // stream-K: the fixup workgroup of a tile adds its G / S partials one after
 // another (G workgroups, S stream-K tiles)
 constexpr double kSkSlotNs = 930.0;
+// Operands the 16-byte loaders cannot stage: efficiency relative to eff of
+// the 128 tile's 4-byte direct staging (data-parallel / split-K, and
+// stream-K) with its extra cost per work item (each sets up its 4-byte load
+// offsets), and of the 64 and 256 tiles, which then load through registers
+// one float at a time.
+constexpr double kFourByteEff = 0.8815;
+constexpr double kFourByteItemNs = 1010.0;
+constexpr double kFourByteSkEff = 1.121;
+constexpr double kFourByteSkItemNs = 5552.0;
+constexpr double kReg64Eff = 0.5706;
+constexpr double kReg256Eff = 0.8389;
+// C rows not 16-byte aligned: the output stores are element-wise (their time
+// x kScalarStoreFactor), and so are the split-K reduction and the stream-K
+// fixup (bandwidth x kScalarReduceEff).
+constexpr double kScalarStoreFactor = 5.497;
+constexpr double kScalarReduceEff = 0.2811;
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
@@ -158,8 +175,14 @@ SkChoice plan_stream_k(const mi_gemm_args& a, int cfg, int num_cus) {
     g.op_b = a.op_b;
     g.lda = a.lda;
     g.ldb = a.ldb;
-    const bool staged = cfg == kCfg64W ? ksplit_ok(a.structure, g.vec, a.K, a.K, a.lda, a.ldb)
-                                       : direct_ok(g);
+    bool staged = cfg == kCfg64W ? ksplit_ok(a.structure, g.vec, a.K, a.K, a.lda, a.ldb)
+                                 : direct_ok(g);
+    if (!staged && cfg == kCfg128 && a.K > 0) {
+        // 4-byte direct staging: one K range per tile, of whole 16-deep
+        // slices but its last, which may end at K
+        g.k_chunk = (int)(cdiv(a.K, ci.bk) * ci.bk);
+        staged = direct4_ok(g);
+    }
     if (a.K <= 0 || !staged) return sk;
     const int64_t T = cdiv(a.M, ci.bm) * cdiv(a.N, ci.bn);
     const int64_t G = (int64_t)num_cus * resident_wgs(cfg);
@@ -167,7 +190,7 @@ SkChoice plan_stream_k(const mi_gemm_args& a, int cfg, int num_cus) {
     const int64_t waves = T / G;
     const int64_t dp = waves >= 1 ? (waves - 1) * G : 0;
     const int64_t S = T - dp;
-    const int64_t ipt = a.K / ci.bk;
+    const int64_t ipt = cdiv(a.K, ci.bk);
     if (S * ipt < 2 * G || T > INT32_MAX) return sk;
     const size_t need = (size_t)G * ci.bm * ci.bn * sizeof(float);
     if (a.workspace_bytes < need) return sk;
@@ -262,6 +285,11 @@ int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
         double best_t = 1e300;
         const int64_t batch = std::max<int64_t>(1, a.batch);
         const double out_bytes = 4.0 * (double)batch * a.M * a.N;
+        // C rows not 16-byte aligned: element-wise stores, reduction and fixup
+        const bool c_vec = a.N % 4 == 0 && a.ldc % 4 == 0 && (a.batch <= 1 || a.stride_c % 4 == 0) &&
+                           (a.C == nullptr || aligned16(a.C));
+        const double st_x = c_vec ? 1.0 : kScalarStoreFactor;
+        const double red_x = c_vec ? 1.0 : 1.0 / kScalarReduceEff;
         // The 256 tile stages through LDS directly only with 16-byte operands
         // and K a multiple of 32; otherwise it loads through registers one
         // float at a time, while the 128 tile keeps direct (4-byte) staging:
@@ -275,8 +303,12 @@ int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
             // the 64 tile stages through registers: with operands that are not
             // 16-byte aligned it loads one float at a time, where the 128 tile
             // keeps direct 4-byte staging (4248 x 2044 x 3769: 59 vs 96 TFLOP/s)
-            const double scale = m.id == kCfg256 && !full16      ? 0.75
-                                 : m.id == kCfg64 && choose_vec(a) != 4 ? 0.6
+            // (the 128 tile's 4-byte direct staging: kFourByteEff for its
+            // data-parallel and split-K plans, kFourByteSkEff for stream-K)
+            const bool four_byte = m.id == kCfg128 && !(choose_vec(a) == 4 && a.K % 16 == 0);
+            const double scale = m.id == kCfg256 && !full16           ? kReg256Eff
+                                 : m.id == kCfg64 && choose_vec(a) != 4 ? kReg64Eff
+                                 : four_byte                            ? kFourByteEff
                                                                         : 1.0;
             const int res = resident_wgs(m.id);
             const int64_t tiles = cdiv(a.M, ci.bm) * cdiv(a.N, ci.bn) * batch;
@@ -301,9 +333,9 @@ int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
                 const int64_t grid = std::min<int64_t>((int64_t)num_cus * res, items);
                 const double eff = scale * m.eff[std::min(occ, 3) - 1];
                 double t = (double)per_cu * 2.0 * ci.bm * ci.bn * (double)kc / (eff * kPeakFlopsPerCuNs);
-                t += (double)cdiv(items, grid) * m.item_ns;
-                t += m.store_exp[occ > 1 ? 1 : 0] * out_bytes * s / kWriteBytesPerNs;
-                if (s > 1) t += (s + 1) * out_bytes / kReduceBytesPerNs + kReduceNs;
+                t += (double)cdiv(items, grid) * (m.item_ns + (four_byte ? kFourByteItemNs : 0.0));
+                t += m.store_exp[occ > 1 ? 1 : 0] * st_x * out_bytes * s / kWriteBytesPerNs;
+                if (s > 1) t += (s + 1) * out_bytes / kReduceBytesPerNs * red_x + kReduceNs;
                 if (t < best_t * 0.999) {
                     best_t = t;
                     best_cfg = m.id;
@@ -316,13 +348,23 @@ int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
             // stored per workgroup and the fixup pass (read the partials, read
             // and write the split tiles of C).
             const SkChoice sk = no_sk ? SkChoice{} : plan_stream_k(a, m.id, num_cus);
-            if (sk.tiles > 0) {
-                const double eff = scale * m.sk_eff * m.eff[std::min(res, 3) - 1];
+            // 4-byte staging: stream-K measured faster only with deep tiles,
+            // enough of them (with fewer than G / 6 each tile splits into many
+            // segments), and a data-parallel plan whose busiest CU has >= 12 %
+            // more tiles than the mean (72 random unaligned shapes, all four
+            // layouts); the cost model is not offered it otherwise
+            const bool sk_offered =
+                !four_byte || (a.K >= 1536 && 6 * tiles >= (int64_t)sk.grid &&
+                               (double)cdiv(tiles, num_cus) * num_cus >= 1.12 * (double)tiles);
+            if (sk.tiles > 0 && sk_offered) {
+                const double eff = (four_byte ? kFourByteSkEff : scale) * m.sk_eff *
+                                   m.eff[std::min(res, 3) - 1];
                 double t = (double)tiles * 2.0 * ci.bm * ci.bn * (double)a.K / num_cus /
                            (eff * kPeakFlopsPerCuNs);
-                t += (double)(sk.dp / sk.grid + 2) * m.item_ns;
-                t += m.store_exp[res > 1 ? 1 : 0] * (out_bytes + sk.grid * tile_bytes) / kWriteBytesPerNs;
-                t += 3.0 * sk.grid * tile_bytes / kReduceBytesPerNs +
+                t += (double)(sk.dp / sk.grid + 2) * (m.item_ns + (four_byte ? kFourByteSkItemNs : 0.0));
+                t += m.store_exp[res > 1 ? 1 : 0] * (st_x * out_bytes + sk.grid * tile_bytes) /
+                     kWriteBytesPerNs;
+                t += 3.0 * sk.grid * tile_bytes / kReduceBytesPerNs * red_x +
                      kSkSlotNs * (double)sk.grid / sk.tiles;
                 if (t < best_t * 0.999) {
                     best_t = t;

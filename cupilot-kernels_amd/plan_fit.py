@@ -1,8 +1,8 @@
 """Fit the constants of the planner's dense cost model (csrc/scheduler.cpp,
 kModels and the reduction / stream-K constants) to measured plan timings.
 
-The model is the one plan_gemm evaluates (N/N, 16-byte operands, batch from
-the table):
+The model is the one plan_gemm evaluates (batch and layout from the table;
+operands contiguous, so a row's leading dimensions are its extents):
   per_cu = ceil(items / CUs), occ = min(resident workgroups, per_cu)
   t      = per_cu * 2 BM BN kc / (eff[cfg][occ] * CU peak) + ceil(items / grid) * item_ns[cfg]
            + store_exp[cfg][occ > 1] * out_bytes * split / write bandwidth
@@ -10,6 +10,13 @@ the table):
   stream-K: the work spread over every resident workgroup, (dp / G + 2) items,
            partial tiles stored and read back three times, sk_slot_ns * G / S; on the
            k-split 64 tile its own efficiency factor and fixed cost (sk10_eff, sk10_ns).
+  Operands the 16-byte loaders cannot stage (a row or K not a multiple of 4 floats,
+  or K off the tile's slice depth) scale the efficiency: the 128 tile's 4-byte
+  direct staging by e2v (data-parallel and split-K, plus o2v per work item) and
+  sk2v (stream-K, plus sk2v_ns per work item), the register-staged 64 and 256 tiles by s1v and s3v;
+  with C rows not 16-byte aligned the reduction and fixup passes, which then
+  run element-wise, reach rv of their bandwidth, and the output stores (also
+  element-wise) take xv times as long.
 Fit: a random local search on the ranking (mean regret of the plan the model
 picks + 0.1 x worst regret + 0.2 x rms log error, plans within 15 % of a
 shape's best weighing 4x in the rms) from the constants scheduler.cpp
@@ -36,16 +43,30 @@ BK = {1: 16, 2: 16, 3: 32, 9: 32, 10: 64}
 RES = {1: 8, 2: 3, 3: 1, 9: 2, 10: 1}
 NAMES = ["e1_1", "e1_2", "e1_3", "e2_1", "e2_2", "e2_3", "e3", "e9_1", "e9_2",
          "o1", "o2", "o3", "o9", "x3", "x_occ1", "x_occ2", "reduce_bw", "reduce_ns", "sk_slot_ns",
-         "e10", "o10", "x10", "sk10_eff", "sk10_ns"]
+         "e10", "o10", "x10", "sk10_eff", "sk10_ns", "s1v", "s3v", "e2v", "sk2v", "sk2v_ns", "rv", "xv", "o2v"]
 # the constants csrc/scheduler.cpp carries (the starting point of the search)
 X0 = [0.433, 0.642, 0.718, 0.821, 0.907, 0.915, 0.947, 0.850, 0.914, 2937, 3393, 220, 4286, 1.38, 0.935,
-      0.495, 7661, 5354, 930, 0.850, 2361, 0.733, 0.798, 0.0]
-LO = [0.2] * 9 + [0.0] * 4 + [0.0, 0.0, 0.0, 1000, 0, 0] + [0.2, 0.0, 0.0, 0.3, 0.0]
-HI = [1.2] * 9 + [5e4] * 4 + [1.5, 1.5, 1.5, 2e4, 5e4, 5e4] + [1.2, 5e4, 1.5, 1.2, 5e4]
+      0.495, 7661, 5354, 930, 0.850, 2361, 0.733, 0.798, 0.0, 0.5706, 0.8389, 0.8815, 1.121, 5552.0, 0.2811, 5.497, 1010.0]
+LO = [0.2] * 9 + [0.0] * 4 + [0.0, 0.0, 0.0, 1000, 0, 0] + [0.2, 0.0, 0.0, 0.3, 0.0] + [0.2] * 4 + [0.0, 0.05, 0.5, 0.0]
+HI = [1.2] * 9 + [5e4] * 4 + [1.5, 1.5, 1.5, 2e4, 5e4, 5e4] + [1.2, 5e4, 1.5, 1.2, 5e4] + [1.2, 1.2, 1.2, 1.5] + [5e4, 1.5, 12.0, 5e4]
 
 
 def cdiv(a, b):
     return -(-a // b)
+
+
+def vec4(r):
+    """16-byte operand rows (choose_vec == 4) for contiguous operands."""
+    M, N, K, lay = r["M"], r["N"], r["K"], r["layout"]
+    return ((K if lay[0] == "N" else M) % 4 == 0) and ((N if lay[1] == "N" else K) % 4 == 0)
+
+
+def sk4_allowed(M, N, K):
+    """The planner's guard on stream-K with 4-byte staging (scheduler.cpp,
+    plan_stream_k): K >= 1536, at least G / 6 tiles, and a data-parallel plan
+    whose per-CU tile count is >= 12 % above the mean."""
+    T, G = cdiv(M, 128) * cdiv(N, 128), NC * RES[2]
+    return K >= 1536 and 6 * T >= G and cdiv(T, NC) * NC >= 1.12 * T
 
 
 def model(r, x):
@@ -54,34 +75,44 @@ def model(r, x):
     bm = BM[c]
     T = cdiv(M, bm) * cdiv(N, bm) * B
     out = 4.0 * M * N * B
-    scale = 0.75 if (c == 3 and K % 32) else 1.0
+    v4 = vec4(r)
+    # C rows not 16-byte aligned: the split-K reduction and the stream-K fixup
+    # run element-wise (bandwidth factor rv)
+    red = 1.0 if N % 4 == 0 else 1.0 / P["rv"]
+    xst = 1.0 if N % 4 == 0 else P["xv"]  # (and the output stores are element-wise)
+    four_byte = c == 2 and not (v4 and K % 16 == 0)
+    scale = (P["s3v"] if c == 3 and not (v4 and K % 32 == 0) else P["s1v"] if c == 1 and not v4
+             else P["e2v"] if four_byte and not sk else 1.0)
     eff = {1: [P["e1_1"], P["e1_2"], P["e1_3"]], 2: [P["e2_1"], P["e2_2"], P["e2_3"]],
            3: [P["e3"]] * 3, 9: [P["e9_1"], P["e9_2"], P["e9_2"]], 10: [P["e10"]] * 3}[c]
     xs = ([P["x3"], P["x3"]] if c == 3 else [P["x10"], P["x10"]] if c == 10
           else [P["x_occ1"], P["x_occ2"]])
     o = P["o%d" % c]
+    if sk and four_byte and not sk4_allowed(M, N, K):
+        return math.inf  # the planner does not offer it
     if sk:
         G = NC * RES[c]
         waves = T // G
         dp = (waves - 1) * G if waves >= 1 else 0
         S = T - dp
         tile = 4.0 * bm * bm
-        ske = P["sk10_eff"] if c == 10 else 1.0
+        ske = P["sk10_eff"] if c == 10 else P["sk2v"] if four_byte else 1.0
         t = T * 2.0 * bm * bm * K / NC / (scale * ske * eff[min(RES[c], 3) - 1] * PEAK)
         t += P["sk10_ns"] if c == 10 else 0.0
-        t += (dp // G + 2) * o
-        t += xs[1 if RES[c] > 1 else 0] * (out + G * tile) / WRITE
-        t += 3.0 * G * tile / P["reduce_bw"] + P["sk_slot_ns"] * G / S
+        t += (dp // G + 2) * (o + (P["sk2v_ns"] if four_byte else 0.0))
+        t += xs[1 if RES[c] > 1 else 0] * (xst * out + G * tile) / WRITE
+        t += 3.0 * G * tile / P["reduce_bw"] * red + P["sk_slot_ns"] * G / S
         return t
     items = T * s
     kc = cdiv(cdiv(K, s), BK[c]) * BK[c]
     per_cu = cdiv(items, NC)
     occ = min(RES[c], per_cu)
     grid = min(NC * RES[c], items)
-    t = per_cu * 2.0 * bm * bm * kc / (scale * eff[min(occ, 3) - 1] * PEAK) + cdiv(items, grid) * o
-    t += xs[1 if occ > 1 else 0] * out * s / WRITE
+    t = (per_cu * 2.0 * bm * bm * kc / (scale * eff[min(occ, 3) - 1] * PEAK)
+         + cdiv(items, grid) * (o + (P["o2v"] if four_byte else 0.0)))
+    t += xs[1 if occ > 1 else 0] * xst * out * s / WRITE
     if s > 1:
-        t += (s + 1) * out / P["reduce_bw"] + P["reduce_ns"]
+        t += (s + 1) * out / P["reduce_bw"] * red + P["reduce_ns"]
     return t
 
 
@@ -98,7 +129,9 @@ def main(argv=None):
     ap.add_argument("table")
     ap.add_argument("--iters", type=int, default=2500)
     ap.add_argument("--lsq", action="store_true")
+    ap.add_argument("--only", default="", help="comma-separated constants to search (default: all)")
     args = ap.parse_args(argv)
+    free = [NAMES.index(n) for n in args.only.split(",") if n] or list(range(len(NAMES)))
     rows = [r for r in load(args.table) if r["cfg"] in BM]
     by = defaultdict(list)
     for r in rows:
@@ -108,10 +141,23 @@ def main(argv=None):
     w = np.array([1.0 if r["ms"] <= 1.15 * best[key(r)] else 0.25 for r in rows])
 
     def resid(x):
-        return w * np.array([math.log(model(r, x) / (r["ms"] * 1e6)) for r in rows])
+        return w * np.array([math.log(model(r, x) / (r["ms"] * 1e6)) if math.isfinite(model(r, x)) else 0.0
+                             for r in rows])
+
+    def pick(v, x):
+        # plan_gemm's order (kModels: 256, 128, 64, ..., then split 1, 2, 4, ...
+        # before stream-K per config) and its rule: a later plan replaces the
+        # best so far only if at least 0.1 % faster
+        order = {3: 0, 2: 1, 1: 2, 9: 5, 10: 6}
+        best_r, best_t = None, math.inf
+        for r in sorted(v, key=lambda r: (order[r["cfg"]], r["stream_k"], r["split"])):
+            t = model(r, x)
+            if t < best_t * 0.999:
+                best_r, best_t = r, t
+        return best_r
 
     def regrets(x):
-        return [min(v, key=lambda r: model(r, x))["ms"] / best[k] - 1 for k, v in by.items()]
+        return [pick(v, x)["ms"] / best[k] - 1 for k, v in by.items()]
 
     def score(x):
         reg = regrets(x)
@@ -121,6 +167,10 @@ def main(argv=None):
         reg = regrets(x)
         print(f"{what}: rms log error {np.sqrt(np.mean((resid(x) / w) ** 2)):.3f}; regret of the picked plan: "
               f"mean {np.mean(reg) * 100:.2f} %, max {max(reg) * 100:.1f} %")
+        for name, sel in (("16-byte rows", True), ("4-byte rows", False)):
+            sub = [g for g, k in zip(reg, by) if vec4(by[k][0]) == sel]
+            if sub:
+                print(f"  {name}: {len(sub)} shapes, mean {np.mean(sub) * 100:.2f} %, max {max(sub) * 100:.1f} %")
 
     print(f"{len(rows)} timings, {len(by)} shapes")
     report(np.array(X0), "scheduler.cpp constants")
@@ -130,7 +180,7 @@ def main(argv=None):
     lo, hi = np.array(LO), np.array(HI)
     for _ in range(args.iters):
         cand = cur.copy()
-        k = rng.integers(len(cand), size=rng.integers(1, 4))
+        k = rng.choice(free, size=min(len(free), int(rng.integers(1, 4))), replace=False)
         cand[k] *= np.exp(rng.normal(0, 0.04, size=len(k)))
         cand = np.clip(cand, lo, hi)
         sc = score(cand)

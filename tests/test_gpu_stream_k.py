@@ -1,5 +1,6 @@
 """Stream-K schedule on the GPU, through the C ABI: parity with the fp64 oracle
-in every layout on the direct-staged 256 and 128 tiles and the k-split 64 tile, tiles split over many workgroups
+in every layout on the direct-staged 256 and 128 tiles (16-byte and, on the
+128 tile, 4-byte staging with a partial last slice) and the k-split 64 tile, tiles split over many workgroups
 and ragged edges, a data-parallel wave ahead of the stream-K tiles, bitwise
 repeatability (the fixup adds partials in a fixed order), and agreement with
 the data-parallel plan of the same problem.
@@ -49,6 +50,8 @@ def _plan(ck, M, N, K, op_a, op_b, override):
     (1000, 1100, 1024, 2),   # ragged edges on the 128 tile
     (640, 640, 2048, 10),    # 100 tiles of 64 over 256 workgroups (the k-split 64 tile)
     (1000, 1100, 1024, 10),  # ragged edges: 288 tiles, one data-parallel wave + 32 stream-K
+    (1000, 1100, 1021, 2),   # 4-byte staging (K % 16 != 0): each tile's last slice partial
+    (640, 643, 2047, 2),     # 4-byte staging, N and K odd
 ])
 def test_stream_k_parity(ck, orc, dev, op_a, op_b, M, N, K, cfg):
     p = _plan(ck, M, N, K, op_a, op_b, cfg | SK_FORCE)
@@ -64,6 +67,8 @@ def test_stream_k_parity(ck, orc, dev, op_a, op_b, M, N, K, cfg):
     (5120, 5120, 2048, 3, (1, 1)),   # 400 tiles of 256: 1.56 tiles per workgroup
     (3584, 3584, 1024, 3, (0, 1)),   # 196 tiles < 256 workgroups
     (1536, 1536, 2048, 10, (1, 0)),  # 576 tiles of 64: 256 data-parallel + 320 stream-K
+    (8205, 2949, 5921, 2, (0, 0)),   # 4-byte staging: one data-parallel wave + 792 stream-K tiles
+    (3001, 3001, 3001, 2, (1, 1)),   # 4-byte staging: 576 tiles, every one stream-K
 ])
 def test_stream_k_larger_every_element(ck, orc, dev, M, N, K, cfg, ops):
     """Bigger stream-K schedules, every element through fp64 row and column
@@ -82,7 +87,8 @@ def test_stream_k_larger_every_element(ck, orc, dev, M, N, K, cfg, ops):
              f"stream-K {M}x{N}x{K} every element")
 
 
-@pytest.mark.parametrize("M,N,K,cfg", [(1280, 1280, 2048, 3), (640, 640, 2048, 2), (640, 640, 2048, 10)])
+@pytest.mark.parametrize("M,N,K,cfg", [(1280, 1280, 2048, 3), (640, 640, 2048, 2), (640, 640, 2048, 10),
+                                       (1000, 1100, 1021, 2)])
 def test_stream_k_bitwise_repeatable(ck, orc, dev, M, N, K, cfg):
     """20 runs, bitwise identical: every partial tile is added in slot order."""
     a_st, b_st, _, _ = _operands(orc, M, N, K, 0, 0, seed=4300)
@@ -92,7 +98,8 @@ def test_stream_k_bitwise_repeatable(ck, orc, dev, M, N, K, cfg):
         np.testing.assert_array_equal(to_host(_run(ck, A, B, M, N, K, 0, 0, cfg | SK_FORCE)), first)
 
 
-@pytest.mark.parametrize("M,N,K,cfg", [(1280, 1280, 2048, 3), (640, 640, 2048, 2), (640, 640, 2048, 10)])
+@pytest.mark.parametrize("M,N,K,cfg", [(1280, 1280, 2048, 3), (640, 640, 2048, 2), (640, 640, 2048, 10),
+                                       (1000, 1100, 1021, 2)])
 def test_stream_k_integer_inputs_exact(ck, orc, dev, M, N, K, cfg):
     """Integer-valued inputs: every partial sum is an exact integer, so the
     stream-K result equals the data-parallel one bit for bit."""
