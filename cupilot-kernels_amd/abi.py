@@ -30,6 +30,7 @@ MI_OP_N, MI_OP_T = 0, 1
 MI_DENSE, MI_LOWER, MI_UPPER, MI_SYMMETRIC = 0, 1, 2, 3
 (CFG64, CFG128, CFG256, CFG128K32, CFG128K64, CFG_PANEL32, CFG_PANEL64, CFG_PANEL128, CFG128B32,
  CFG64W) = (1, 2, 3, 4, 5, 6, 7, 8, 9, 10)
+PLAN_NO_PACK, PLAN_PACK = 0x40, 0x80  # plan_override bits (operand packing)
 
 _i64 = ctypes.c_int64
 _vp = ctypes.c_void_p
@@ -58,6 +59,7 @@ class Plan(ctypes.Structure):
         ("split_k", ctypes.c_int32), ("k_chunk", _i64), ("group_m", ctypes.c_int32),
         ("num_tiles", _i64), ("grid", _i64), ("workspace_bytes", _sz),
         ("stream_k", ctypes.c_int32), ("sk_tiles", _i64),
+        ("packed", ctypes.c_int32), ("packed_k", _i64),
     ]
 
 

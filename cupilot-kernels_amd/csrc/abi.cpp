@@ -16,6 +16,8 @@
 namespace mi {
 int validate_shape(const mi_gemm_args& a);
 int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* launch);
+// the packed N/T problem of a plan with mi_plan.packed (operands in workspace)
+mi_gemm_args packed_problem(const mi_gemm_args& a, void* workspace, size_t workspace_bytes);
 }  // namespace mi
 
 using namespace mi;
@@ -284,6 +286,19 @@ int mi_gemm_f32(const mi_gemm_args* args, void* stream) {
     GemmLaunch g{};
     rc = plan_gemm(a, cus, p, &g);
     if (rc != MI_OK) return rc;
+    if (p.packed) {
+        // copy both operands K-contiguous into the workspace, K zero-padded,
+        // then run the N/T product of the copies (planned without packing)
+        if (!a.workspace || a.workspace_bytes < p.workspace_bytes) return MI_ERR_WORKSPACE;
+        const mi_gemm_args pa = packed_problem(a, a.workspace, a.workspace_bytes);
+        hipError_t e = launch_pack_rows(a.A, a.lda, a.op_a == MI_OP_N, a.M, a.K,
+                                        const_cast<float*>(pa.A), pa.K, s);
+        if (e == hipSuccess)
+            e = launch_pack_rows(a.B, a.ldb, a.op_b == MI_OP_T, a.N, a.K, const_cast<float*>(pa.B),
+                                 pa.K, s);
+        if (e != hipSuccess) return hip_rc(e);
+        return mi_gemm_f32(&pa, stream);
+    }
     if ((g.split_k > 1 || g.sk_tiles > 0) &&
         (!a.workspace || a.workspace_bytes < p.workspace_bytes))
         return MI_ERR_WORKSPACE;

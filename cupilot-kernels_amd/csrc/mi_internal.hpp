@@ -173,6 +173,11 @@ hipError_t launch_splitk_reduce(const float* ws, float* C, int M, int N, int bat
 // partial (tri_zero_tile), so only the mirrors and the counter's tile remain.
 hipError_t launch_tri_finish(float* C, int64_t ldc, int nt, int cap, bool lower, bool zeroed,
                              hipStream_t s);
+// Packs R rows of an operand K-contiguous into dst (row stride kp, a multiple
+// of 32; 16-byte aligned): dst[r][k] = src(r, k) for k < K, 0 up to kp.
+// k_contig: src(r, k) = src[r*ld + k]; else src[k*ld + r] (transposed).
+hipError_t launch_pack_rows(const float* src, int64_t ld, bool k_contig, int64_t R, int64_t K, float* dst,
+                            int64_t kp, hipStream_t s);
 // Writes integer 0 to one 4-byte word (a kernel, so it can be graph-captured).
 hipError_t launch_zero_word(void* w, hipStream_t s);
 // C[b][r][c] = bias ? bias[r] : 0 (a contraction with K = 0)

@@ -1,8 +1,9 @@
 // noalloc.hip -- mi_gemm_f32_noalloc: mi_gemm_f32 for callers that cannot
 // allocate device memory (code under HIP graph capture, tight serving loops,
-// harnesses that forbid hipMalloc).  The only scratch mi_gemm_f32's kernels
-// use is the split-K partial tiles (the caller's workspace); here it is a
-// file-scope device array of fixed size instead, so a call allocates nothing.
+// harnesses that forbid hipMalloc).  The scratch mi_gemm_f32's kernels use
+// (split-K partial tiles, stream-K partial tiles, packed operand copies: the
+// caller's workspace) is here a file-scope device array of fixed size
+// instead, so a call allocates nothing.
 //
 // The array's name is a host-side stand-in, not a device address: its
 // address on the current device comes from hipGetSymbolAddress, looked up
@@ -66,7 +67,13 @@ int mi_gemm_f32_noalloc(const mi_gemm_args* args, void* stream) {
     // The plan mi_gemm_f32 uses with a workspace of mi_gemm_workspace_bytes:
     // the same kernels, split and reduction order, so the same result bit
     // for bit.  (0 for an invalid problem: mi_gemm_f32 reports it below.)
-    const size_t need = mi_gemm_workspace_bytes(&a);
+    size_t need = mi_gemm_workspace_bytes(&a);
+    if (need > kScratchBytes && (a.plan_override & MI_PLAN_NO_PACK) == 0) {
+        // a plan that packs the operands (mostly their copies) past the
+        // scratch: the unpacked plan instead
+        a.plan_override |= MI_PLAN_NO_PACK;
+        need = mi_gemm_workspace_bytes(&a);
+    }
     if (need > kScratchBytes) return MI_ERR_SCRATCH_LIMIT;
     void* ws = nullptr;
     const int rc = scratch_on_current_device(&ws);

@@ -84,6 +84,16 @@ constexpr double kReg256Eff = 0.8389;
 // fixup (bandwidth x kScalarReduceEff).
 constexpr double kScalarStoreFactor = 5.497;
 constexpr double kScalarReduceEff = 0.2811;
+// packing pass (plan_gemm): bytes per ns over what it reads and writes and
+// a fixed cost per pack launch (measured: 8205 x 5921 x 2949 in the four
+// layouts 58-87 us for 335 MB, 4095^3 63 us, 1021^3 15 us); the gain a
+// packed plan must promise, and the smallest K it is offered for (40 random
+// unaligned shapes timed packed and unpacked: below K = 1536 the model's
+// choice lost up to 9 %, from it on at most 0.6 %)
+constexpr double kPackBytesPerNs = 5000.0;
+constexpr double kPackLaunchNs = 5000.0;
+constexpr double kPackMargin = 0.97;
+constexpr int64_t kPackMinK = 1536;
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
@@ -202,12 +212,15 @@ SkChoice plan_stream_k(const mi_gemm_args& a, int cfg, int num_cus) {
     return sk;
 }
 
-}  // namespace
-
-int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* launch) {
+// The planner proper (plan_gemm below adds the choice of packing the
+// operands).  cost: the cost model's time of the chosen plan in ns, or -1
+// when the plan does not come from the cost model (structured products,
+// panel configs, overrides).
+int plan_core(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* launch, double* cost) {
     int rc = validate_shape(a);
     if (rc != MI_OK) return rc;
     if (num_cus <= 0) num_cus = 256;
+    double model_t = -1.0;
 
     int best_cfg = kCfg128, best_split = 1;
     SkChoice best_sk;
@@ -374,6 +387,7 @@ int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
                 }
             }
         }
+        model_t = best_t;
     }
 
     const CfgInfo ci = cfg_info(best_cfg);
@@ -477,6 +491,91 @@ int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
         g.sk_tiles = best_sk.tiles;
         g.sk_ipt = best_sk.ipt;
     }
+    out.packed = 0;
+    out.packed_k = 0;
+    if (cost) *cost = model_t;
+    return MI_OK;
+}
+
+// Packing: operands the 16-byte loaders cannot stage (rows or K not a
+// multiple of 4 floats, or K not of 32 -- the 256 tile's slice depth) are
+// first copied into the workspace K-contiguous, with K zero-padded to a
+// multiple of 32 (launch_pack_rows: a copy for K-contiguous sources, a
+// transpose through LDS for MN-contiguous ones), and the product runs as
+// the N/T problem A'[M][Kp] x B'[N][Kp]^T on the 16-byte kernels; the zero
+// padding adds exact zeros.  Dense products only, batch 1, no row bias.
+bool pack_eligible(const mi_gemm_args& a) {
+    if (a.structure != MI_DENSE || a.batch > 1 || a.bias_m != nullptr) return false;
+    if (a.M <= 0 || a.N <= 0 || a.K <= 0) return false;
+    if (choose_vec(a) == 4 && a.K % 32 == 0) return false;  // already 16-byte staged
+    const int64_t kp = cdiv(a.K, 32) * 32;
+    return cdiv(kp, 64) <= 65535;  // the transpose kernel's grid.y
+}
+
+// workspace layout of a packed plan: A' at 0, B' and then the product's own
+// workspace at 256-byte boundaries
+size_t pack_a_bytes(const mi_gemm_args& a, int64_t kp) {
+    return (size_t)cdiv(a.M * kp * (int64_t)sizeof(float), 256) * 256;
+}
+size_t pack_bytes(const mi_gemm_args& a, int64_t kp) {
+    return pack_a_bytes(a, kp) + (size_t)cdiv(a.N * kp * (int64_t)sizeof(float), 256) * 256;
+}
+
+}  // namespace
+
+int packed_k(const mi_gemm_args& a) { return (int)(cdiv(a.K, 32) * 32); }
+
+mi_gemm_args packed_problem(const mi_gemm_args& a, void* workspace, size_t workspace_bytes) {
+    const int64_t kp = packed_k(a);
+    mi_gemm_args p = a;
+    char* const ws = static_cast<char*>(workspace);
+    p.A = ws ? reinterpret_cast<const float*>(ws) : nullptr;
+    p.B = ws ? reinterpret_cast<const float*>(ws + pack_a_bytes(a, kp)) : nullptr;
+    p.K = kp;
+    p.op_a = MI_OP_N;
+    p.op_b = MI_OP_T;
+    p.lda = kp;
+    p.ldb = kp;
+    p.batch = 1;
+    p.stride_a = p.stride_b = 0;
+    // forced packing keeps the other override bits for the packed product;
+    // the planner's own choice keeps only the raster grouping
+    const int32_t keep = (a.plan_override & MI_PLAN_PACK) ? ~(MI_PLAN_NO_PACK | MI_PLAN_PACK) : (0x7FF << 20);
+    p.plan_override = (a.plan_override & keep) | MI_PLAN_NO_PACK;
+    const size_t pb = pack_bytes(a, kp);
+    p.workspace = ws && workspace_bytes > pb ? ws + pb : nullptr;
+    p.workspace_bytes = workspace_bytes > pb ? workspace_bytes - pb : 0;
+    return p;
+}
+
+size_t packed_operand_bytes(const mi_gemm_args& a) { return pack_bytes(a, packed_k(a)); }
+
+int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* launch) {
+    double t0 = -1.0;
+    int rc = plan_core(a, num_cus, out, launch, &t0);
+    if (rc != MI_OK) return rc;
+    const bool no_pack = (a.plan_override & MI_PLAN_NO_PACK) != 0;
+    const bool force_pack = (a.plan_override & MI_PLAN_PACK) != 0;
+    if (no_pack || !pack_eligible(a) || (t0 < 0 && !force_pack)) return MI_OK;
+    if (!force_pack && a.K < kPackMinK) return MI_OK;
+    const int64_t kp = packed_k(a);
+    const size_t pb = pack_bytes(a, kp);
+    if (a.workspace_bytes < pb || (a.workspace && ((uintptr_t)a.workspace & 255u) != 0)) return MI_OK;
+    const mi_gemm_args pa = packed_problem(a, nullptr, a.workspace_bytes);
+    mi_plan pp{};
+    GemmLaunch pg{};
+    double t1 = -1.0;
+    if (plan_core(pa, num_cus, pp, launch ? &pg : nullptr, &t1) != MI_OK) return MI_OK;
+    // the packing pass: read both operands, write them padded, two launches
+    const double moved = 4.0 * (double)(a.M + a.N) * (double)(a.K + kp);
+    t1 += moved / kPackBytesPerNs + 2.0 * kPackLaunchNs;
+    if (!force_pack && !(t1 >= 0 && t1 < kPackMargin * t0)) return MI_OK;
+    if (pp.workspace_bytes > SIZE_MAX - pb) return MI_OK;
+    out = pp;
+    out.workspace_bytes = pb + pp.workspace_bytes;
+    out.packed = 1;
+    out.packed_k = kp;
+    if (launch) *launch = pg;
     return MI_OK;
 }
 

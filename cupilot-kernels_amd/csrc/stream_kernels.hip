@@ -480,6 +480,78 @@ hipError_t launch_tri_finish(float* C, int64_t ldc, int nt, int cap, bool lower,
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Operand packing for the 16-byte staging path.  dst is R rows of kp floats
+// (kp a multiple of 32, dst 16-byte aligned): dst[r][k] = src(r, k) for
+// k < K and 0 for K <= k < kp.  K-contiguous sources, src(r, k) = src[r*ld + k],
+// are copied row by row (each thread one 16-byte group of dst); MN-contiguous
+// ones, src(r, k) = src[k*ld + r], are transposed through a 64 x 64 LDS tile
+// so that both the reads (along r) and the writes (along k) are coalesced.
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256)
+    pack_rows_kernel(const float* __restrict__ src, int64_t ld, int64_t R, int K, float* __restrict__ dst,
+                     int kp) {
+    const int g4 = kp / 4;  // 16-byte groups per dst row
+    const int64_t total = R * g4;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = e / g4;
+        const int k = (int)(e - r * g4) * 4;
+        const float* const row = src + r * ld;
+        f4 v;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = k + q < K ? row[k + q] : 0.f;
+        *reinterpret_cast<f4*>(dst + r * kp + k) = v;
+    }
+}
+
+__global__ void __launch_bounds__(256)
+    pack_transpose_kernel(const float* __restrict__ src, int64_t ld, int64_t R, int K, float* __restrict__ dst,
+                          int kp) {
+    __shared__ float t[64][65];  // [k][r]
+    const int64_t r0 = (int64_t)blockIdx.x * 64;
+    const int k0 = blockIdx.y * 64;
+    const int tid = threadIdx.x;
+    // read: lane r = tid % 64 along the source's contiguous r, 16 k-rows each
+    const int rr = tid & 63;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int kk = (tid >> 6) + 4 * i;
+        const int64_t r = r0 + rr;
+        const int k = k0 + kk;
+        t[kk][rr] = (r < R && k < K) ? src[(int64_t)k * ld + r] : 0.f;
+    }
+    __syncthreads();
+    // write: 64 rows x 16 groups of 4 k
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int idx = tid + 256 * i;
+        const int wr = idx >> 4, g = idx & 15;
+        const int64_t r = r0 + wr;
+        const int k = k0 + 4 * g;
+        if (r < R && k < kp) {
+            const f4 v = {t[4 * g][wr], t[4 * g + 1][wr], t[4 * g + 2][wr], t[4 * g + 3][wr]};
+            *reinterpret_cast<f4*>(dst + r * kp + k) = v;
+        }
+    }
+}
+
+hipError_t launch_pack_rows(const float* src, int64_t ld, bool k_contig, int64_t R, int64_t K, float* dst,
+                            int64_t kp, hipStream_t s) {
+    if (R == 0 || kp == 0) return hipSuccess;
+    if (k_contig) {
+        int64_t blocks = (R * (kp / 4) + 255) / 256;
+        if (blocks > 65536) blocks = 65536;
+        hipLaunchKernelGGL(pack_rows_kernel, dim3((unsigned)blocks), dim3(256), 0, s, src, ld, R, (int)K, dst,
+                           (int)kp);
+    } else {
+        // (the planner packs only with kp / 64 <= 65535: grid.y's limit)
+        const dim3 grid((unsigned)((R + 63) / 64), (unsigned)((kp + 63) / 64));
+        hipLaunchKernelGGL(pack_transpose_kernel, grid, dim3(256), 0, s, src, ld, R, (int)K, dst, (int)kp);
+    }
+    return hipGetLastError();
+}
+
 __global__ void zero_word_kernel(int* w) {
     if (threadIdx.x == 0) *w = 0;
 }

@@ -88,14 +88,21 @@ typedef struct {
     int32_t structure;        /* mi_structure; square, batch 1, N/N layouts */
     int32_t plan_override;    /* 0 = scheduler's choice; else (tests, tuning) bits 0-3 tile
                                  config id (mi_plan.plan_id), bit 4 stream-K where it applies,
-                                 bit 5 never stream-K, bits 8-19 split count, bits 20-30 raster
-                                 group rows; a config the problem cannot take is ignored */
+                                 bit 5 never stream-K, bit 6 (MI_PLAN_NO_PACK) never pack the
+                                 operands, bit 7 (MI_PLAN_PACK) pack them where packing applies
+                                 (the other bits then apply to the packed product), bits 8-19
+                                 split count, bits 20-30 raster group rows; a config the
+                                 problem cannot take is ignored */
     void* workspace;
     size_t workspace_bytes;
     const float* bias_m;      /* NULL, or M floats: C[b][i][j] = (sum over k) + bias_m[i],
                                  one fp32 add after the full sum, the same for every
                                  batch; dense structure and op_a = op_b = N only */
 } mi_gemm_args;
+
+/* plan_override bits 6 and 7 (operand packing, see mi_plan.packed) */
+#define MI_PLAN_NO_PACK 0x40
+#define MI_PLAN_PACK 0x80
 
 /* Scheduler decision for one contraction (host-only, no device access). */
 typedef struct {
@@ -116,6 +123,11 @@ typedef struct {
                                first num_tiles - sk_tiles tiles stay whole), partial
                                tiles are added in by a fixed-order fixup pass */
     int64_t sk_tiles;
+    int32_t packed;         /* 1: A and B are first packed into the workspace
+                               K-contiguous with K zero-padded to packed_k, and the
+                               fields above describe the N/T product of the packed
+                               operands; workspace_bytes includes the packed copies */
+    int64_t packed_k;
 } mi_plan;
 
 /* One work item of a workgroup under a plan (host introspection). */
@@ -138,6 +150,9 @@ MI_API size_t mi_gemm_workspace_bytes(const mi_gemm_args* args);
  * bits -- but args->workspace and args->workspace_bytes are ignored: the
  * split-K partial tiles go to a fixed MI_NOALLOC_SCRATCH_BYTES array the
  * library holds on each device (for the life of the process) instead.
+ *   - A plan that packs its operands (mi_plan.packed) into more scratch than
+ *     that is replaced by the unpacked plan (MI_PLAN_NO_PACK), whose result
+ *     may then differ from mi_gemm_f32's in the last bits.
  *   - A problem whose plan needs more scratch than that returns
  *     MI_ERR_SCRATCH_LIMIT before anything is launched.
  *   - The first call on a device looks up that device's copy of the array

@@ -207,8 +207,13 @@ def test_k_split_tile_needs_sixteen_byte_operands_and_k_multiple_of_64(ck):
     rc, p = ck.abi.plan(1024, 1024, 1024, plan_override=10)
     assert rc == 0 and p.plan_id == 10 and p.block_k == 64 and p.grid == 256
     for kw in (dict(M=1024, N=1024, K=1000), dict(M=1024, N=1022, K=1024), dict(M=1024, N=1024, K=1056)):
+        # unpacked, the override is ignored and the planner picks another tile
+        rc, p = ck.abi.plan(workspace_bytes=1 << 40, plan_override=10 | ck.abi.PLAN_NO_PACK, **kw)
+        assert rc == 0 and p.plan_id != 10 and not p.packed, kw
+        # the planner's own choice may pack the operands, and then run any tile
+        # on the 16-byte copies (K padded to 32)
         rc, p = ck.abi.plan(workspace_bytes=1 << 40, plan_override=10, **kw)
-        assert rc == 0 and p.plan_id != 10, kw  # the override is ignored, the planner picks
+        assert rc == 0 and (p.plan_id != 10 or (p.packed and p.packed_k % 64 == 0)), kw
 
 
 def _cover(ck, args, num_cus=256):
@@ -593,8 +598,9 @@ def test_plan_regret_against_measured_timings(ck):
     6.1 % (up to 40 %)."""
     regrets, unmeasured = [], []
     for (M, N, K, B, lay), plans in _plan_timings().items():
+        # (the table times unpacked plans; packing is judged on its own below)
         rc, p = ck.abi.plan(M, N, K, batch=B, op_a=int(lay[0] == "T"), op_b=int(lay[1] == "T"),
-                            workspace_bytes=1 << 40)
+                            workspace_bytes=1 << 40, plan_override=ck.abi.PLAN_NO_PACK)
         assert rc == 0
         key = (p.plan_id, p.split_k, p.stream_k)
         if key not in plans:
