@@ -200,9 +200,10 @@ def configs(ck):
         return (r1 + r1.t()) / 2, (r2 + r2.t()) / 2
     add("symmetric_8192", sym, lambda a, b: ck.p13.symmetric_matmul_cuda(a, b), lambda a, b: a @ b,
         flops=2 * n ** 3, reps=5, cpu_note="A @ B")
-    # not BASELINE configs: the reference's literal PID 2 extents, shapes that
-    # show the stream-K schedule, and the next rows (PIDs 5, 87, 97)
-    add("pid2_2048x8192x4096", lambda u: (u((2048, 4096), 80), u((4096, 8192), 81)),
+    # not BASELINE configs: the reference's literal PID 2 extents (M = 2048,
+    # K = 8192, N = 4096: kernels/2_...:16-18), shapes that show the stream-K
+    # schedule, and the next rows (PIDs 5, 87, 97)
+    add("pid2_2048x8192x4096", lambda u: (u((2048, 8192), 80), u((8192, 4096), 81)),
         lambda a, b: ck.p02.matmul_cuda(a, b), lambda a, b: a @ b, flops=2 * 2048 * 8192 * 4096,
         cpu_note="A @ B", baseline=False)
     for (m_, n_, k_) in ((3072, 3072, 8192), (4608, 4608, 4608)):

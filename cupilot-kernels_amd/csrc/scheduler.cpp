@@ -50,12 +50,12 @@ struct CfgModel {
 // one measured.  The single-slice configs (K <= 32 / 64) take the 128 tile's
 // constants with half its exposed store time.
 constexpr CfgModel kModels[] = {
-    {kCfg256, {0.947, 0.947, 0.947}, 220.0, {1.38, 1.38}, 1.0},
+    {kCfg256, {0.9349, 0.9349, 0.9349}, 175.4, {1.475, 1.475}, 1.0},
     {kCfg128, {0.821, 0.907, 0.915}, 3393.0, {0.935, 0.495}, 1.0},
     {kCfg64, {0.433, 0.642, 0.718}, 2937.0, {0.935, 0.495}, 1.0},
     {kCfg128K32, {0.821, 0.907, 0.915}, 0.0, {0.47, 0.25}, 1.0},
     {kCfg128K64, {0.821, 0.907, 0.915}, 0.0, {0.47, 0.25}, 1.0},
-    {kCfg128B32, {0.850, 0.914, 0.914}, 4286.0, {0.935, 0.495}, 1.0},
+    {kCfg128B32, {0.8519, 0.914, 0.914}, 4320.0, {0.935, 0.495}, 1.0},
     {kCfg64W, {0.850, 0.850, 0.850}, 2361.0, {0.733, 0.733}, 0.798},
 };
 

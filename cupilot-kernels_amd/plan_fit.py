@@ -45,7 +45,7 @@ NAMES = ["e1_1", "e1_2", "e1_3", "e2_1", "e2_2", "e2_3", "e3", "e9_1", "e9_2",
          "o1", "o2", "o3", "o9", "x3", "x_occ1", "x_occ2", "reduce_bw", "reduce_ns", "sk_slot_ns",
          "e10", "o10", "x10", "sk10_eff", "sk10_ns", "s1v", "s3v", "e2v", "sk2v", "sk2v_ns", "rv", "xv", "o2v"]
 # the constants csrc/scheduler.cpp carries (the starting point of the search)
-X0 = [0.433, 0.642, 0.718, 0.821, 0.907, 0.915, 0.947, 0.850, 0.914, 2937, 3393, 220, 4286, 1.38, 0.935,
+X0 = [0.433, 0.642, 0.718, 0.821, 0.907, 0.915, 0.9349, 0.8519, 0.914, 2937, 3393, 175.4, 4320, 1.475, 0.935,
       0.495, 7661, 5354, 930, 0.850, 2361, 0.733, 0.798, 0.0, 0.5706, 0.8389, 0.8815, 1.121, 5552.0, 0.2811, 5.497, 1010.0]
 LO = [0.2] * 9 + [0.0] * 4 + [0.0, 0.0, 0.0, 1000, 0, 0] + [0.2, 0.0, 0.0, 0.3, 0.0] + [0.2] * 4 + [0.0, 0.05, 0.5, 0.0]
 HI = [1.2] * 9 + [5e4] * 4 + [1.5, 1.5, 1.5, 2e4, 5e4, 5e4] + [1.2, 5e4, 1.5, 1.2, 5e4] + [1.2, 1.2, 1.2, 1.5] + [5e4, 1.5, 12.0, 5e4]

@@ -613,7 +613,7 @@ def test_plan_regret_against_measured_timings(ck):
     assert max(regrets)[0] <= 0.12, max(regrets)
 
 
-@pytest.mark.parametrize("M,N,K", [(8192, 8192, 8192), (2048, 8192, 4096), (65536, 512, 256),
+@pytest.mark.parametrize("M,N,K", [(8192, 8192, 8192), (2048, 8192, 4096), (2048, 4096, 8192), (65536, 512, 256),
                                    (16384, 768, 2048), (1024, 1024, 1024), (3072, 3072, 8192),
                                    (4608, 4608, 4608)])
 def test_plan_for_baseline_shapes_within_one_percent_of_best(ck, M, N, K):
