@@ -210,6 +210,12 @@ def configs(ck):
         add(f"stream_k_{m_}x{n_}x{k_}", lambda u, m_=m_, n_=n_, k_=k_: (u((m_, k_), 82), u((k_, n_), 83)),
             lambda a, b: ck.p02.matmul_cuda(a, b), lambda a, b: a @ b, flops=2 * m_ * n_ * k_,
             cpu_note="A @ B", baseline=False)
+    # PID 8's irregular extents (M = 8205, K = 2949, N = 5921, the synthetic
+    # shape the evaluation runner uses): rows not 16-byte aligned, so the
+    # planner packs the operands before the 16-byte kernels run
+    add("irregular_8205x2949x5921", lambda u: (u((8205, 2949), 84), u((2949, 5921), 85)),
+        lambda a, b: ck.p08.matmul_cuda(a, b), lambda a, b: a @ b, flops=2 * 8205 * 2949 * 5921,
+        cpu_note="A @ B", baseline=False)
     add("scalar_16384x4096", lambda u: (u((16384, 4096), 57),),
         lambda a: ck.p05.matrix_scalar_mult_cuda(a, 3.14), lambda a: a * 3.14,
         nbytes=4 * 2 * 16384 * 4096, reps=20, warmup=4, sets=2, cpu_note="A * s", baseline=False)
