@@ -158,14 +158,14 @@ def test_operators_replay_in_a_hip_graph(ck, dev):
     q, k, v = (u(1, 2, 128, 1024).half() for _ in range(3))
     # plans: stream-K on the 256 tile, stream-K / data-parallel / split-K on
     # the 32-deep 128 tile (asserted below)
-    sk3a, sk3b = u(3072, 8192), u(8192, 3072)
+    sk3a, sk3b = u(3072, 12288), u(12288, 3072)
     sk9a, sk9b = u(1280, 8192), u(8192, 1280)
     d9a, d9b = u(2048, 2048), u(2048, 4096)
     s9a, s9b = u(1024, 8192), u(8192, 2048)
     # ... and the 64-tile k-split config, alone and split
     k10a, k10b = u(1024, 1024), u(1024, 1024)
     k10sa, k10sb = u(512, 8192), u(8192, 512)
-    for (m, kk, n), want in [((3072, 8192, 3072), (3, 1, 1)), ((1280, 8192, 1280), (9, 1, 1)),
+    for (m, kk, n), want in [((3072, 12288, 3072), (3, 1, 1)), ((1280, 8192, 1280), (9, 1, 1)),
                              ((2048, 2048, 4096), (9, 0, 1)), ((1024, 8192, 2048), (9, 0, 4)),
                              ((1024, 1024, 1024), (10, 0, 1)), ((512, 8192, 512), (10, 0, 4))]:
         rc, p = ck.abi.plan(m, n, kk, workspace_bytes=1 << 40)
