@@ -50,12 +50,12 @@ struct CfgModel {
 // one measured.  The single-slice configs (K <= 32 / 64) take the 128 tile's
 // constants with half its exposed store time.
 constexpr CfgModel kModels[] = {
-    {kCfg256, {0.9459, 0.9459, 0.9459}, 12.53, {1.391, 1.391}, 1.0},
-    {kCfg128, {0.8193, 0.9185, 0.9186}, 3187, {1.033, 0.4937}, 1.0},
-    {kCfg64, {0.433, 0.642, 0.718}, 2937, {1.033, 0.4937}, 1.0},
-    {kCfg128K32, {0.8193, 0.9185, 0.9186}, 0.0, {0.5165, 0.2469}, 1.0},
-    {kCfg128K64, {0.8193, 0.9185, 0.9186}, 0.0, {0.5165, 0.2469}, 1.0},
-    {kCfg128B32, {0.8509, 0.9251, 0.9251}, 3948, {1.033, 0.4937}, 1.0},
+    {kCfg256, {0.942, 0.942, 0.942}, 3.473, {1.291, 1.291}, 1.0},
+    {kCfg128, {0.8153, 0.9105, 0.9186}, 2843, {0.992, 0.4875}, 1.0},
+    {kCfg64, {0.433, 0.642, 0.718}, 2937, {0.992, 0.4875}, 1.0},
+    {kCfg128K32, {0.8153, 0.9105, 0.9186}, 0.0, {0.496, 0.2437}, 1.0},
+    {kCfg128K64, {0.8153, 0.9105, 0.9186}, 0.0, {0.496, 0.2437}, 1.0},
+    {kCfg128B32, {0.8598, 0.9239, 0.9239}, 5103, {0.992, 0.4875}, 1.0},
     {kCfg64W, {0.850, 0.850, 0.850}, 2361.0, {0.733, 0.733}, 0.798},
 };
 

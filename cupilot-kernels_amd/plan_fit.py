@@ -45,7 +45,7 @@ NAMES = ["e1_1", "e1_2", "e1_3", "e2_1", "e2_2", "e2_3", "e3", "e9_1", "e9_2",
          "o1", "o2", "o3", "o9", "x3", "x_occ1", "x_occ2", "reduce_bw", "reduce_ns", "sk_slot_ns",
          "e10", "o10", "x10", "sk10_eff", "sk10_ns", "s1v", "s3v", "e2v", "sk2v", "sk2v_ns", "rv", "xv", "o2v"]
 # the constants csrc/scheduler.cpp carries (the starting point of the search)
-X0 = [0.433, 0.642, 0.718, 0.8193, 0.9185, 0.9186, 0.9459, 0.8509, 0.9251, 2937, 3187, 12.53, 3948, 1.391, 1.033, 0.4937, 7661, 5354, 930, 0.85, 2361, 0.733, 0.798, 0, 0.5706, 0.8389, 0.8815, 1.121, 5552, 0.2811, 5.497, 1010]
+X0 = [0.433, 0.642, 0.718, 0.8153, 0.9105, 0.9186, 0.942, 0.8598, 0.9239, 2937, 2843, 3.473, 5103, 1.291, 0.992, 0.4875, 7661, 5354, 930, 0.85, 2361, 0.733, 0.798, 0, 0.5706, 0.8389, 0.8815, 1.121, 5552, 0.2811, 5.497, 1010]
 LO = [0.2] * 9 + [0.0] * 4 + [0.0, 0.0, 0.0, 1000, 0, 0] + [0.2, 0.0, 0.0, 0.3, 0.0] + [0.2] * 4 + [0.0, 0.05, 0.5, 0.0]
 HI = [1.2] * 9 + [5e4] * 4 + [1.5, 1.5, 1.5, 2e4, 5e4, 5e4] + [1.2, 5e4, 1.5, 1.2, 5e4] + [1.2, 1.2, 1.2, 1.5] + [5e4, 1.5, 12.0, 5e4]
 
@@ -53,7 +53,8 @@ HI = [1.2] * 9 + [5e4] * 4 + [1.5, 1.5, 1.5, 2e4, 5e4, 5e4] + [1.2, 5e4, 1.5, 1.
 PINNED = {(8192, 8192, 8192, 1, "NN"), (8192, 8192, 8192, 1, "TN"), (8192, 8192, 8192, 1, "NT"),
           (8192, 8192, 8192, 1, "TT"), (512, 768, 1024, 128, "NN"), (16384, 768, 2048, 1, "NN"),
           (65536, 512, 256, 1, "NN"), (1024, 1024, 1024, 1, "NN"), (2048, 4096, 8192, 1, "NN"),
-          (2048, 8192, 4096, 1, "NN"), (3072, 3072, 8192, 1, "NN"), (4608, 4608, 4608, 1, "NN")}
+          (2048, 8192, 4096, 1, "NN"), (3072, 3072, 8192, 1, "NN"), (4608, 4608, 4608, 1, "NN"),
+          (8205, 5921, 2976, 1, "NT")}  # (the last: PID 8's product after packing)
 
 
 def cdiv(a, b):
