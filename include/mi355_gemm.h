@@ -148,8 +148,9 @@ MI_API size_t mi_gemm_workspace_bytes(const mi_gemm_args* args);
  * result as mi_gemm_f32 -- the same plan, kernels and reduction order as a
  * call given a workspace of mi_gemm_workspace_bytes(args) bytes, so the same
  * bits -- but args->workspace and args->workspace_bytes are ignored: the
- * split-K partial tiles go to a fixed MI_NOALLOC_SCRATCH_BYTES array the
- * library holds on each device (for the life of the process) instead.
+ * scratch (split-K and stream-K partial tiles, packed operand copies) goes to
+ * a fixed MI_NOALLOC_SCRATCH_BYTES array the library holds on each device
+ * (for the life of the process) instead.
  *   - A plan that packs its operands (mi_plan.packed) into more scratch than
  *     that is replaced by the unpacked plan (MI_PLAN_NO_PACK), whose result
  *     may then differ from mi_gemm_f32's in the last bits.
