@@ -29,7 +29,7 @@ NOALLOC_SCRATCH_BYTES = 64 << 20
 MI_OP_N, MI_OP_T = 0, 1
 MI_DENSE, MI_LOWER, MI_UPPER, MI_SYMMETRIC = 0, 1, 2, 3
 (CFG64, CFG128, CFG256, CFG128K32, CFG128K64, CFG_PANEL32, CFG_PANEL64, CFG_PANEL128, CFG128B32,
- CFG64W) = (1, 2, 3, 4, 5, 6, 7, 8, 9, 10)
+ CFG64W, CFG128W8) = (1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11)
 PLAN_NO_PACK, PLAN_PACK = 0x40, 0x80  # plan_override bits (operand packing)
 
 _i64 = ctypes.c_int64

@@ -171,6 +171,7 @@ int mi_gemm_tile_of(const mi_gemm_args* args, int32_t num_cus, int64_t item, int
         case kCfg64:
         case kCfg64W: compute = MI_TILE_OF(64); break;
         case kCfg128:
+        case kCfg128W8:
         case kCfg128K32:
         case kCfg128K64:
         case kCfg128B32: compute = MI_TILE_OF(128); break;

@@ -815,6 +815,9 @@ template <bool AT, bool BT>
 inline hipError_t launch_direct(const GemmLaunch& g, hipStream_t s) {
     if (!direct_ok(g)) return launch_direct_tile<Tile128, AT, BT, 4>(g, s);
     if (g.cfg == kCfg128B32) return launch_direct_tile<Tile128B32, AT, BT, 16>(g, s);
+    if constexpr (!AT) {
+        if (g.cfg == kCfg128W8) return launch_direct_tile<Tile128W8, AT, BT, 16>(g, s);
+    }
     return g.cfg == kCfg128 ? launch_direct_tile<Tile128, AT, BT, 16>(g, s)
                             : launch_direct_tile<Tile256, AT, BT, 16>(g, s);
 }

@@ -58,6 +58,7 @@ using Tile256 = Tile<256, 256, 128, 64, 32, 2>;  // 1 workgroup of 8 waves per C
 using Tile128K32 = Tile<128, 128, 64, 64, 32, 3, 1>;  // K <= 32 in one slice, 3 WGs per CU
 using Tile128K64 = Tile<128, 128, 64, 64, 64, 2, 1>;  // K <= 64 in one slice, 2 WGs per CU
 using Tile128B32 = Tile<128, 128, 64, 64, 32, 2>;     // 32-deep slices, direct-staged, 2 WGs per CU
+using Tile128W8 = Tile<128, 128, 32, 64, 32, 4>;      // the same, 8 waves of 32 x 64, 2 WGs per CU
 
 enum { kDense = 0, kLower = 1, kUpper = 2 };
 

@@ -25,7 +25,7 @@ namespace mi {
 enum TileCfgId {
     kCfg64 = 1, kCfg128 = 2, kCfg256 = 3, kCfg128K32 = 4, kCfg128K64 = 5,
     kCfgPanel32 = 6, kCfgPanel64 = 7, kCfgPanel128x64 = 8, kCfg128B32 = 9, kCfg64W = 10,
-    kNumCfg = 11
+    kCfg128W8 = 11, kNumCfg = 12
 };
 inline bool is_panel_cfg(int id) {
     return id == kCfgPanel32 || id == kCfgPanel64 || id == kCfgPanel128x64;
@@ -46,6 +46,7 @@ inline CfgInfo cfg_info(int id) {
         case kCfgPanel128x64: return {128, 128, 64, 512};
         case kCfg128B32: return {128, 128, 32, 256};
         case kCfg64W: return {64, 64, 64, 512};
+        case kCfg128W8: return {128, 128, 32, 512};
         default: return {0, 0, 0, 0};
     }
 }
@@ -105,6 +106,13 @@ inline bool direct_ok(const GemmLaunch& g) {
         const int64_t lim_a = g.op_a == 0 ? (INT64_C(1) << 22) : (INT64_C(1) << 25);
         const int64_t lim_b = g.op_b != 0 ? (INT64_C(1) << 22) : (INT64_C(1) << 25);
         return g.K % 16 == 0 && g.k_chunk % 16 == 0 && g.lda <= lim_a && g.ldb <= lim_b;
+    }
+    if (g.cfg == kCfg128W8) {
+        // the 8-wave 32-deep 128 tile: A K-contiguous only (its waves hold one
+        // 32-row block, and MN-contiguous A is read in row-block pairs)
+        const int64_t lim_a = INT64_C(1) << 22;
+        const int64_t lim_b = g.op_b != 0 ? (INT64_C(1) << 22) : (INT64_C(1) << 24);
+        return g.op_a == 0 && g.K % 32 == 0 && g.k_chunk % 32 == 0 && g.lda <= lim_a && g.ldb <= lim_b;
     }
     if (g.cfg == kCfg128B32) {
         // 128 rows of a K-contiguous operand, 32 rows of an MN-contiguous one

@@ -8,7 +8,8 @@
 // with one cost model over (tile config c, split s) and stream-K:
 //   per_cu        = ceil(tiles(c) * batch * s / CUs) work items per CU
 //   occ           = min(resident workgroups of c, per_cu)
-//   time(c, s)    = per_cu * 2*BM*BN*(K/s) / (eff(c, occ) * CU peak)
+//   time(c, s)    = 2*BM*BN*(K/s) / CU peak * (rounds of occ items / eff(c, occ)
+//                     + the last round's leftover items / eff(c, leftover))
 //                   + items per workgroup * fixed item cost(c)
 //                   + exposed(c, occ) * output bytes * s / sustained write bandwidth
 //                   + split-K reduction (read s partials, write C; one pass)
@@ -39,35 +40,36 @@ struct CfgModel {
                            // the k-split tile's four-stage ring)
 };
 
-// Cost model of a dense plan, fitted to 3810 MI355X timings of candidate
-// plans -- 64 / 128 / 32-deep 128 / 256 tiles, the 64-tile k-split config,
-// split-K 1 - 32, stream-K -- over 213 shapes from 256 x 512 x 4096 to
+// Cost model of a dense plan, fitted to 4515 MI355X timings of candidate
+// plans -- 64 / 128 / 32-deep 128 / 8-wave 128 / 256 tiles, the 64-tile
+// k-split config, split-K 1 - 32, stream-K -- over 229 shapes from 256 x 512 x 4096 to
 // 8192 x 3072 x 16384: 141 with 16-byte operand rows, N/N plus all four
 // layouts of 12 of them, and 72 random ones in all four layouts whose rows or
 // K are not multiples of 4 floats (or K of 16) (tests/data/plan_timings_mi355x.csv,
 // fitted by plan_fit.py: a local search on the ranking from the previous
-// constants).  The plan it picks is on average 1.3 % slower than the fastest
-// one measured.  The single-slice configs (K <= 32 / 64) take the 128 tile's
+// constants).  The plan it picks is on average 0.7 % slower than the fastest
+// one measured, 11 % at worst.  The single-slice configs (K <= 32 / 64) take the 128 tile's
 // constants with half its exposed store time.
 constexpr CfgModel kModels[] = {
-    {kCfg256, {0.942, 0.942, 0.942}, 3.473, {1.291, 1.291}, 1.0},
-    {kCfg128, {0.8153, 0.9105, 0.9186}, 2843, {0.992, 0.4875}, 1.0},
-    {kCfg64, {0.433, 0.642, 0.718}, 2937, {0.992, 0.4875}, 1.0},
-    {kCfg128K32, {0.8153, 0.9105, 0.9186}, 0.0, {0.496, 0.2437}, 1.0},
-    {kCfg128K64, {0.8153, 0.9105, 0.9186}, 0.0, {0.496, 0.2437}, 1.0},
-    {kCfg128B32, {0.8598, 0.9239, 0.9239}, 5103, {0.992, 0.4875}, 1.0},
+    {kCfg256, {0.9547, 0.9547, 0.9547}, 1.372, {1.447, 1.447}, 1.0},
+    {kCfg128, {0.8892, 0.91, 0.9178}, 2904, {1.5, 0.4952}, 1.0},
+    {kCfg64, {0.4263, 0.654, 0.72}, 2961, {1.5, 0.4952}, 1.0},
+    {kCfg128K32, {0.8892, 0.91, 0.9178}, 0.0, {0.75, 0.2476}, 1.0},
+    {kCfg128K64, {0.8892, 0.91, 0.9178}, 0.0, {0.75, 0.2476}, 1.0},
+    {kCfg128B32, {0.861, 0.9231, 0.9231}, 4510, {1.5, 0.4952}, 1.0},
     {kCfg64W, {0.850, 0.850, 0.850}, 2361.0, {0.733, 0.733}, 0.798},
+    {kCfg128W8, {0.995, 0.9354, 0.9354}, 4815, {1.5, 0.4952}, 1.0},
 };
 
 constexpr double kPeakFlopsPerCuNs = 256.0 * 2.4;  // fp32 MFMA flop per ns per CU
 constexpr double kWriteBytesPerNs = 5500.0;        // sustained write-only bandwidth (measured)
 // split-K reduction and stream-K fixup passes: bytes per ns over what they
 // read and write, plus a fixed cost per reduction pass
-constexpr double kReduceBytesPerNs = 7661.0;
+constexpr double kReduceBytesPerNs = 7592.0;
 constexpr double kReduceNs = 5354.0;
 // stream-K: the fixup workgroup of a tile adds its G / S partials one after
 // another (G workgroups, S stream-K tiles)
-constexpr double kSkSlotNs = 930.0;
+constexpr double kSkSlotNs = 962.3;
 // Operands the 16-byte loaders cannot stage: efficiency relative to eff of
 // the 128 tile's 4-byte direct staging (data-parallel / split-K, and
 // stream-K) with its extra cost per work item (each sets up its 4-byte load
@@ -112,6 +114,7 @@ int resident_wgs(int cfg) {
         case kCfgPanel64: return 1;
         case kCfgPanel128x64: return 1;
         case kCfg128B32: return 2;
+        case kCfg128W8: return 2;
         case kCfg64W: return 1;
         default: return 8;
     }
@@ -242,6 +245,7 @@ int plan_core(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
     const bool w64_ok = ksplit_ok(a.structure, choose_vec(a), a.K, 64, a.lda, a.ldb) && a.K > 0;
     const bool override_ok =
         override_cfg >= kCfg64 && override_cfg < kNumCfg && (override_cfg != kCfg128B32 || b32_ok) &&
+        (override_cfg != kCfg128W8 || (b32_ok && a.op_a == MI_OP_N)) &&
         (override_cfg != kCfg64W || w64_ok) &&
         !((override_cfg == kCfg128K32 || override_cfg == kCfg128K64 || is_panel_cfg(override_cfg)) &&
           a.K > cfg_info(override_cfg).bk) &&
@@ -312,6 +316,9 @@ int plan_core(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
             const CfgInfo ci = cfg_info(m.id);
             if ((m.id == kCfg128K32 || m.id == kCfg128K64) && a.K > ci.bk) continue;
             if (m.id == kCfg128B32 && !b32_ok) continue;
+            // the 8-wave tile: its longer per-tile prologue and store pay off
+            // from K = 1024 (4096^2 x 512: 131 vs 127 us for the 128 tile)
+            if (m.id == kCfg128W8 && !(b32_ok && a.op_a == MI_OP_N && a.K >= 1024)) continue;
             if (m.id == kCfg64W && !w64_ok) continue;
             // the 64 tile stages through registers: with operands that are not
             // 16-byte aligned it loads one float at a time, where the 128 tile
@@ -328,6 +335,10 @@ int plan_core(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
             const double tile_bytes = 4.0 * ci.bm * ci.bn;
             for (int s = 1; s <= 1024; s *= 2) {
                 if (s > 1) {
+                    // the 8-wave tile is for one tile per CU: with split-K it
+                    // measured no faster than unsplit (1024 x 3072 x 16384:
+                    // 0.95, 0.94, 0.94 ms at split 1, 2, 4)
+                    if (m.id == kCfg128W8) break;
                     // split only to fill the machine, with >= kMinSplitK of K per
                     // split: while the previous split's items stay below four
                     // times the CUs (the k-split 64 tile, one workgroup per CU,
@@ -344,8 +355,12 @@ int plan_core(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
                 const int64_t per_cu = cdiv(items, (int64_t)num_cus);
                 const int occ = (int)std::min<int64_t>(res, per_cu);
                 const int64_t grid = std::min<int64_t>((int64_t)num_cus * res, items);
-                const double eff = scale * m.eff[std::min(occ, 3) - 1];
-                double t = (double)per_cu * 2.0 * ci.bm * ci.bn * (double)kc / (eff * kPeakFlopsPerCuNs);
+                // full rounds of occ resident items at that occupancy, then the
+                // last round's leftover items at their own, lower occupancy
+                const int64_t rounds = per_cu / occ, rem = per_cu % occ;
+                const double slots = (double)(rounds * occ) / m.eff[std::min(occ, 3) - 1] +
+                                     (rem ? (double)rem / m.eff[std::min<int64_t>(rem, 3) - 1] : 0.0);
+                double t = slots * 2.0 * ci.bm * ci.bn * (double)kc / (scale * kPeakFlopsPerCuNs);
                 t += (double)cdiv(items, grid) * (m.item_ns + (four_byte ? kFourByteItemNs : 0.0));
                 t += m.store_exp[occ > 1 ? 1 : 0] * st_x * out_bytes * s / kWriteBytesPerNs;
                 if (s > 1) t += (s + 1) * out_bytes / kReduceBytesPerNs * red_x + kReduceNs;
@@ -366,9 +381,13 @@ int plan_core(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
             // segments), and a data-parallel plan whose busiest CU has >= 12 %
             // more tiles than the mean (72 random unaligned shapes, all four
             // layouts); the cost model is not offered it otherwise
+            // Below K = 1024 stream-K measured slower than the data-parallel
+            // plan on all 25 shapes of the timing table; the 8-wave tile is
+            // offered data-parallel only.
             const bool sk_offered =
-                !four_byte || (a.K >= 1536 && 6 * tiles >= (int64_t)sk.grid &&
-                               (double)cdiv(tiles, num_cus) * num_cus >= 1.12 * (double)tiles);
+                a.K >= 1024 && m.id != kCfg128W8 &&
+                (!four_byte || (a.K >= 1536 && 6 * tiles >= (int64_t)sk.grid &&
+                                (double)cdiv(tiles, num_cus) * num_cus >= 1.12 * (double)tiles));
             if (sk.tiles > 0 && sk_offered) {
                 const double eff = (four_byte ? kFourByteSkEff : scale) * m.sk_eff *
                                    m.eff[std::min(res, 3) - 1];

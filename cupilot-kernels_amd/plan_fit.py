@@ -38,22 +38,23 @@ from scipy.optimize import least_squares
 NC = 256
 PEAK = 256 * 2.4  # fp32 MFMA flop per ns per CU
 WRITE = 5500.0
-BM = {1: 64, 2: 128, 3: 256, 9: 128, 10: 64}
-BK = {1: 16, 2: 16, 3: 32, 9: 32, 10: 64}
-RES = {1: 8, 2: 3, 3: 1, 9: 2, 10: 1}
+BM = {1: 64, 2: 128, 3: 256, 9: 128, 10: 64, 11: 128}
+BK = {1: 16, 2: 16, 3: 32, 9: 32, 10: 64, 11: 32}
+RES = {1: 8, 2: 3, 3: 1, 9: 2, 10: 1, 11: 2}
 NAMES = ["e1_1", "e1_2", "e1_3", "e2_1", "e2_2", "e2_3", "e3", "e9_1", "e9_2",
          "o1", "o2", "o3", "o9", "x3", "x_occ1", "x_occ2", "reduce_bw", "reduce_ns", "sk_slot_ns",
-         "e10", "o10", "x10", "sk10_eff", "sk10_ns", "s1v", "s3v", "e2v", "sk2v", "sk2v_ns", "rv", "xv", "o2v"]
+         "e10", "o10", "x10", "sk10_eff", "sk10_ns", "s1v", "s3v", "e2v", "sk2v", "sk2v_ns", "rv", "xv", "o2v", "e11_1", "e11_2", "o11"]
 # the constants csrc/scheduler.cpp carries (the starting point of the search)
-X0 = [0.433, 0.642, 0.718, 0.8153, 0.9105, 0.9186, 0.942, 0.8598, 0.9239, 2937, 2843, 3.473, 5103, 1.291, 0.992, 0.4875, 7661, 5354, 930, 0.85, 2361, 0.733, 0.798, 0, 0.5706, 0.8389, 0.8815, 1.121, 5552, 0.2811, 5.497, 1010]
-LO = [0.2] * 9 + [0.0] * 4 + [0.0, 0.0, 0.0, 1000, 0, 0] + [0.2, 0.0, 0.0, 0.3, 0.0] + [0.2] * 4 + [0.0, 0.05, 0.5, 0.0]
-HI = [1.2] * 9 + [5e4] * 4 + [1.5, 1.5, 1.5, 2e4, 5e4, 5e4] + [1.2, 5e4, 1.5, 1.2, 5e4] + [1.2, 1.2, 1.2, 1.5] + [5e4, 1.5, 12.0, 5e4]
+X0 = [0.4263, 0.654, 0.72, 0.8892, 0.91, 0.9178, 0.9547, 0.861, 0.9231, 2961, 2904, 1.372, 4510, 1.447, 1.5, 0.4952, 7592, 5354, 962.3, 0.85, 2361, 0.733, 0.798, 0, 0.5706, 0.8389, 0.8815, 1.121, 5552, 0.2811, 5.497, 1010, 0.995, 0.9354, 4815]
+LO = [0.2] * 9 + [0.0] * 4 + [0.0, 0.0, 0.0, 1000, 0, 0] + [0.2, 0.0, 0.0, 0.3, 0.0] + [0.2] * 4 + [0.0, 0.05, 0.5, 0.0] + [0.2, 0.2, 0.0]
+HI = [1.2] * 9 + [5e4] * 4 + [1.5, 1.5, 1.5, 2e4, 5e4, 5e4] + [1.2, 5e4, 1.5, 1.2, 5e4] + [1.2, 1.2, 1.2, 1.5] + [5e4, 1.5, 12.0, 5e4] + [1.2, 1.2, 5e4]
 
 
 PINNED = {(8192, 8192, 8192, 1, "NN"), (8192, 8192, 8192, 1, "TN"), (8192, 8192, 8192, 1, "NT"),
           (8192, 8192, 8192, 1, "TT"), (512, 768, 1024, 128, "NN"), (16384, 768, 2048, 1, "NN"),
           (65536, 512, 256, 1, "NN"), (1024, 1024, 1024, 1, "NN"), (2048, 4096, 8192, 1, "NN"),
           (2048, 8192, 4096, 1, "NN"), (3072, 3072, 8192, 1, "NN"), (4608, 4608, 4608, 1, "NN"),
+          (4096, 4096, 512, 1, "NN"),
           (8205, 5921, 2976, 1, "NT")}  # (the last: PID 8's product after packing)
 
 
@@ -90,7 +91,8 @@ def model(r, x):
     scale = (P["s3v"] if c == 3 and not (v4 and K % 32 == 0) else P["s1v"] if c == 1 and not v4
              else P["e2v"] if four_byte and not sk else 1.0)
     eff = {1: [P["e1_1"], P["e1_2"], P["e1_3"]], 2: [P["e2_1"], P["e2_2"], P["e2_3"]],
-           3: [P["e3"]] * 3, 9: [P["e9_1"], P["e9_2"], P["e9_2"]], 10: [P["e10"]] * 3}[c]
+           3: [P["e3"]] * 3, 9: [P["e9_1"], P["e9_2"], P["e9_2"]], 10: [P["e10"]] * 3,
+           11: [P["e11_1"], P["e11_2"], P["e11_2"]]}[c]
     xs = ([P["x3"], P["x3"]] if c == 3 else [P["x10"], P["x10"]] if c == 10
           else [P["x_occ1"], P["x_occ2"]])
     o = P["o%d" % c]
@@ -114,7 +116,11 @@ def model(r, x):
     per_cu = cdiv(items, NC)
     occ = min(RES[c], per_cu)
     grid = min(NC * RES[c], items)
-    t = (per_cu * 2.0 * bm * bm * kc / (scale * eff[min(occ, 3) - 1] * PEAK)
+    # full rounds of RES[c] resident tiles at that occupancy, then the tail's
+    # leftover tiles at their own (lower) occupancy
+    rounds, rem = divmod(per_cu, occ)
+    slots = rounds * occ / eff[min(occ, 3) - 1] + (rem / eff[min(rem, 3) - 1] if rem else 0.0)
+    t = (slots * 2.0 * bm * bm * kc / (scale * PEAK)
          + cdiv(items, grid) * (o + (P["o2v"] if four_byte else 0.0)))
     t += xs[1 if occ > 1 else 0] * xst * out * s / WRITE
     if s > 1:
@@ -154,9 +160,13 @@ def main(argv=None):
         # plan_gemm's order (kModels: 256, 128, 64, ..., then split 1, 2, 4, ...
         # before stream-K per config) and its rule: a later plan replaces the
         # best so far only if at least 0.1 % faster
-        order = {3: 0, 2: 1, 1: 2, 9: 5, 10: 6}
+        order = {3: 0, 2: 1, 1: 2, 9: 5, 10: 6, 11: 7}
         best_r, best_t = None, math.inf
         for r in sorted(v, key=lambda r: (order[r["cfg"]], r["stream_k"], r["split"])):
+            if r["cfg"] == 11 and (r["split"] > 1 or r["stream_k"] or r["K"] < 1024):
+                continue  # the planner offers the 8-wave tile data-parallel from K = 1024
+            if r["stream_k"] and r["K"] < 1024:
+                continue  # nor stream-K below K = 1024
             t = model(r, x)
             if t < best_t * 0.999:
                 best_r, best_t = r, t
@@ -172,7 +182,7 @@ def main(argv=None):
     def score(x):
         reg = regrets(x)
         pin = sum(max(0.0, pick(by[k], x)["ms"] / best[k] - 1.01) for k in pinned)
-        return np.mean(reg) + 0.1 * max(reg) + 0.2 * float(np.sqrt(np.mean(resid(x) ** 2))) + 2.0 * pin
+        return np.mean(reg) + 0.1 * max(reg) + 0.2 * float(np.sqrt(np.mean(resid(x) ** 2))) + 10.0 * pin
 
     def report(x, what):
         reg = regrets(x)

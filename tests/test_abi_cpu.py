@@ -183,7 +183,7 @@ def test_plan_splits_only_where_tiles_are_few(ck, M, N, K, at_least, at_most):
     (256, 4096, 1536, 10, 1),
     (1024, 1024, 2048, 10, 1),
     (8192, 8192, 8192, 3, 1),    # many tiles: the 256 tile (150 / 135)
-    (2048, 2048, 1024, 9, 1),    # 118 / 113
+    (2048, 2048, 1024, 11, 1),   # the 8-wave 128 tile: 129 / 118 (the 32-deep 128 tile)
 ])
 def test_plan_small_problems_take_the_k_split_tile(ck, M, N, K, want, split):
     """Where the 128 / 256 tiles fill the CUs only through split-K, the
@@ -197,7 +197,7 @@ def test_plan_small_problems_take_the_k_split_tile(ck, M, N, K, want, split):
 @pytest.mark.parametrize("M,N,K,cfg,grid", [
     (65536, 512, 256, 2, 2048),      # 2048 tiles of 128: 2.7 waves of 768 -> one tile per workgroup
     (16384, 16384, 256, 2, 16384),
-    (16384, 768, 2048, 2, 768),      # one wave: the persistent grid (the same 768)
+    (16384, 768, 2048, 11, 512),     # the 8-wave tile, 1.5 waves of its 512 resident: persistent
     (4096, 4096, 512, 2, 768),       # 1.3 waves: persistent
     (8192, 8192, 8192, 3, 256),      # the 256 tile stays persistent
 ])

@@ -195,6 +195,47 @@ def test_ksplit_tile_config(ck, orc, dev, op_a, op_b, M, N, K, batch, pad, split
             assert np.isnan(got[:, :, N:]).all(), "a store landed in the ldc padding"
 
 
+@pytest.mark.parametrize("op_b", [0, 1])
+@pytest.mark.parametrize("M,N,K,batch,pad,split", [(2048, 2048, 2048, 1, 0, 1), (300, 520, 1088, 1, 0, 1),
+                                                   (260, 252, 2048, 1, 4, 1), (516, 260, 1024, 3, 0, 1),
+                                                   (128, 128, 32, 1, 0, 1), (1000, 900, 4096, 1, 4, 2)])
+def test_eight_wave_128_tile_config(ck, orc, dev, op_b, M, N, K, batch, pad, split):
+    """The 32-deep 128 tile on 8 waves of 32 x 64 (config 11; A K-contiguous
+    only): edge rows and columns, padded leading dimensions, batched,
+    split-K, row bias (N/N)."""
+    op_a = 0
+    a_st = orc.uniform((batch, M, K), 151)
+    b_st = orc.uniform((batch,) + ((N, K) if op_b else (K, N)), 152)
+    bias = orc.uniform((M,), 153)
+    lda, ldb, ldc = K + pad, (K if op_b else N) + pad, N + pad
+    a_pad = np.zeros((batch, M, lda), np.float32)
+    a_pad[:, :, :K] = a_st
+    b_pad = np.zeros((batch, b_st.shape[1], ldb), np.float32)
+    b_pad[:, :, :b_st.shape[2]] = b_st
+    A, B, Bi = to_dev(a_pad), to_dev(b_pad), to_dev(bias)
+    lb = np.swapaxes(b_st, 1, 2) if op_b else b_st
+    ov = 11 | (split << 8)
+    rc, p = ck.abi.plan(M, N, K, batch=batch, op_a=op_a, op_b=op_b, workspace_bytes=1 << 40,
+                        plan_override=ov)
+    assert rc == 0 and p.plan_id == 11 and p.block_k == 32 and p.split_k == split
+    for with_bias in ((False, True) if op_b == 0 else (False,)):
+        C = torch.full((batch, M, ldc), float("nan"), device="cuda")
+        args = gemm_args(ck, A, B, C, M, N, K, op_a, op_b, batch=batch, lda=lda, ldb=ldb, ldc=ldc,
+                         sa=a_pad[0].size, sb=b_pad[0].size, sc=M * ldc, override=ov)
+        ws = workspace(ck, args)
+        args = gemm_args(ck, A, B, C, M, N, K, op_a, op_b, batch=batch, lda=lda, ldb=ldb, ldc=ldc,
+                         sa=a_pad[0].size, sb=b_pad[0].size, sc=M * ldc, override=ov, ws=ws)
+        if with_bias:
+            args.bias_m = Bi.data_ptr()
+        ck.abi.check(run_gemm(ck, args))
+        ref = orc.gemm(a_st, lb) + (bias.astype(np.float64)[None, :, None] if with_bias else 0.0)
+        got = to_host(C)
+        assert_close(orc, got[:, :, :N], ref, K,
+                     what=f"cfg 11 0{op_b} {M}x{N}x{K}x{batch} pad={pad} split={split} bias={with_bias}")
+        if pad:
+            assert np.isnan(got[:, :, N:]).all(), "a store landed in the ldc padding"
+
+
 @pytest.mark.parametrize("op_a,op_b", LAYOUTS)
 def test_ksplit_integer_inputs_bitwise_and_repeatable(ck, orc, dev, op_a, op_b):
     """Config 10 on small-integer operands is exact, and its fixed-order
