@@ -176,7 +176,9 @@ def main(argv=None):
         return [pick(v, x)["ms"] / best[k] - 1 for k, v in by.items()]
 
     # the BASELINE configs' shapes (and PID 2's): the planner must stay within
-    # 1 % of their best measured plan (tests/test_abi_cpu.py holds it to that)
+    # 1 % of their best measured plan (tests/test_abi_cpu.py holds it to that);
+    # 4096^2 x 512 likewise (the shallow-K shape the tests expect on the 128
+    # tile, where the model has the 256 tile within a hair of it)
     pinned = [k for k in by if k in PINNED]
 
     def score(x):
