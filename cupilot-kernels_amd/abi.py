@@ -29,7 +29,7 @@ NOALLOC_SCRATCH_BYTES = 64 << 20
 MI_OP_N, MI_OP_T = 0, 1
 MI_DENSE, MI_LOWER, MI_UPPER, MI_SYMMETRIC = 0, 1, 2, 3
 (CFG64, CFG128, CFG256, CFG128K32, CFG128K64, CFG_PANEL32, CFG_PANEL64, CFG_PANEL128, CFG128B32,
- CFG64W, CFG128W8) = (1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11)
+ CFG64W, CFG128W8, CFG_PANEL64B) = (1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12)
 PLAN_NO_PACK, PLAN_PACK = 0x40, 0x80  # plan_override bits (operand packing)
 
 _i64 = ctypes.c_int64
@@ -85,28 +85,37 @@ SIGNATURES = {
     "mi_gemm_tile_of": (ctypes.c_int, [ctypes.POINTER(GemmArgs), ctypes.c_int32, _i64, ctypes.c_int32,
                                        ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32),
                                        ctypes.POINTER(_i64), ctypes.POINTER(_i64)]),
-    "mi_square_matmul_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _vp]),
-    "mi_matmul_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
-    "mi_batched_matmul_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
+    "mi_square_matmul_workspace_bytes": (_sz, [_i64]),
+    "mi_square_matmul_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _vp, _sz, _vp]),
+    "mi_matmul_workspace_bytes": (_sz, [_i64, _i64, _i64]),
+    "mi_matmul_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp, _sz, _vp]),
+    "mi_batched_matmul_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64]),
+    "mi_batched_matmul_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _sz, _vp]),
     "mi_gemv_workspace_bytes": (_sz, [_i64, _i64]),
     "mi_gemv_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _vp, _sz, _vp]),
     "mi_matmul_large_k_workspace_bytes": (_sz, [_i64, _i64, _i64]),
     "mi_matmul_large_k_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp, _sz, _vp]),
     "mi_gemm_small_k_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "mi_tall_skinny_matmul_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _vp]),
-    "mi_tensor3d_matmul_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
-    "mi_tensor4d_matmul_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp]),
+    "mi_tensor3d_matmul_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64]),
+    "mi_tensor3d_matmul_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _sz, _vp]),
+    "mi_tensor4d_matmul_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _i64]),
+    "mi_tensor4d_matmul_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _sz, _vp]),
     "mi_diag_mult_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _vp]),
     "mi_matrix_scalar_mult_f32": (ctypes.c_int, [_vp, _vp, _i64, ctypes.c_float, _vp]),
     "mi_pointwise_conv_f32": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
     "mi_sdpa_workspace_bytes": (_sz, [_i64, _i64, _i64]),
     "mi_sdpa_f16": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _sz, _vp]),
-    "mi_symmetric_matmul_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _vp]),
+    "mi_symmetric_matmul_workspace_bytes": (_sz, [_i64]),
+    "mi_symmetric_matmul_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _vp, _sz, _vp]),
     "mi_upper_tri_matmul_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _vp]),
     "mi_lower_tri_mul_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _vp]),
-    "mi_matmul_transposed_a_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
-    "mi_matmul_transposed_b_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
-    "mi_matmul_transposed_both_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
+    "mi_matmul_transposed_a_workspace_bytes": (_sz, [_i64, _i64, _i64]),
+    "mi_matmul_transposed_a_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp, _sz, _vp]),
+    "mi_matmul_transposed_b_workspace_bytes": (_sz, [_i64, _i64, _i64]),
+    "mi_matmul_transposed_b_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp, _sz, _vp]),
+    "mi_matmul_transposed_both_workspace_bytes": (_sz, [_i64, _i64, _i64]),
+    "mi_matmul_transposed_both_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp, _sz, _vp]),
     "mi_fill_uniform_f32": (ctypes.c_int, [_vp, _i64, ctypes.c_uint64, _i64, _vp]),
     "mi_status_string": (ctypes.c_char_p, [ctypes.c_int]),
     "mi_version": (ctypes.c_char_p, []),

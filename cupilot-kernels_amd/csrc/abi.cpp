@@ -74,6 +74,10 @@ mi_gemm_args dense_args(const float* A, const float* B, float* C, int64_t M, int
 // on the symmetry, so a non-symmetric input still gets its own product.  (The
 // symmetry would allow reading B as stored N x K, but the N/N kernel is the
 // faster one at 8192^3: 7.32 vs 7.38 ms.)
+// A named dense operator's call: the caller's workspace (NULL: none) bounds
+// the plan, as mi_gemm_args.workspace_bytes does.
+int run_with_workspace(mi_gemm_args a, void* workspace, size_t workspace_bytes, void* stream);
+
 int canonical(mi_gemm_args& a) {
     if (a.structure != MI_SYMMETRIC) return MI_OK;
     if (a.M != a.N || a.N != a.K) return MI_ERR_NOT_SQUARE;
@@ -97,7 +101,7 @@ const char* mi_status_string(int status) {
         case MI_ERR_NO_DEVICE: return "no HIP device available";
         case MI_ERR_ALIGNMENT: return "pointer not 16-byte aligned";
         case MI_ERR_SCRATCH_LIMIT:
-            return "problem needs more split-K scratch than mi_gemm_f32_noalloc's fixed "
+            return "the forced plan needs more scratch than mi_gemm_f32_noalloc's fixed "
                    "64 MiB device array holds (use mi_gemm_f32 with a workspace)";
         default: break;
     }
@@ -317,26 +321,53 @@ int mi_gemm_f32(const mi_gemm_args* args, void* stream) {
 }
 
 // ---- named operators ---------------------------------------------------------
+// The dense products take the caller's workspace (NULL: none) and plan within
+// it; their *_workspace_bytes queries return what the preferred plan wants.
 
-int mi_square_matmul_f32(const float* A, const float* B, float* C, int64_t N, void* stream) {
+int mi_square_matmul_f32(const float* A, const float* B, float* C, int64_t N, void* workspace,
+                         size_t workspace_bytes, void* stream) {
     mi_gemm_args a = dense_args(A, B, C, N, N, N, MI_OP_N, MI_OP_N);
-    return mi_gemm_f32(&a, stream);
+    return run_with_workspace(a, workspace, workspace_bytes, stream);
+}
+
+size_t mi_square_matmul_workspace_bytes(int64_t N) {
+    mi_gemm_args a = dense_args(nullptr, nullptr, nullptr, N, N, N, MI_OP_N, MI_OP_N);
+    return mi_gemm_workspace_bytes(&a);
 }
 
 int mi_matmul_f32(const float* A, const float* B, float* C, int64_t M, int64_t K, int64_t N,
-                  void* stream) {
+                  void* workspace, size_t workspace_bytes, void* stream) {
     mi_gemm_args a = dense_args(A, B, C, M, K, N, MI_OP_N, MI_OP_N);
-    return mi_gemm_f32(&a, stream);
+    return run_with_workspace(a, workspace, workspace_bytes, stream);
 }
 
-int mi_batched_matmul_f32(const float* A, const float* B, float* C, int64_t batch, int64_t M,
-                          int64_t K, int64_t N, void* stream) {
+size_t mi_matmul_workspace_bytes(int64_t M, int64_t K, int64_t N) {
+    mi_gemm_args a = dense_args(nullptr, nullptr, nullptr, M, K, N, MI_OP_N, MI_OP_N);
+    return mi_gemm_workspace_bytes(&a);
+}
+
+namespace {
+mi_gemm_args batched_args(const float* A, const float* B, float* C, int64_t batch, int64_t M,
+                          int64_t K, int64_t N) {
     mi_gemm_args a = dense_args(A, B, C, M, K, N, MI_OP_N, MI_OP_N);
     a.batch = batch;
     a.stride_a = M * K;
     a.stride_b = K * N;
     a.stride_c = M * N;
-    return mi_gemm_f32(&a, stream);
+    return a;
+}
+}  // namespace
+
+int mi_batched_matmul_f32(const float* A, const float* B, float* C, int64_t batch, int64_t M,
+                          int64_t K, int64_t N, void* workspace, size_t workspace_bytes,
+                          void* stream) {
+    return run_with_workspace(batched_args(A, B, C, batch, M, K, N), workspace, workspace_bytes,
+                              stream);
+}
+
+size_t mi_batched_matmul_workspace_bytes(int64_t batch, int64_t M, int64_t K, int64_t N) {
+    mi_gemm_args a = batched_args(nullptr, nullptr, nullptr, batch, M, K, N);
+    return mi_gemm_workspace_bytes(&a);
 }
 
 size_t mi_gemv_workspace_bytes(int64_t M, int64_t K) {
@@ -372,9 +403,7 @@ size_t mi_matmul_large_k_workspace_bytes(int64_t M, int64_t K, int64_t N) {
 int mi_matmul_large_k_f32(const float* A, const float* B, float* C, int64_t M, int64_t K,
                           int64_t N, void* workspace, size_t workspace_bytes, void* stream) {
     mi_gemm_args a = dense_args(A, B, C, M, K, N, MI_OP_N, MI_OP_N);
-    a.workspace = workspace;
-    a.workspace_bytes = workspace ? workspace_bytes : 0;
-    return mi_gemm_f32(&a, stream);
+    return run_with_workspace(a, workspace, workspace_bytes, stream);
 }
 
 int mi_gemm_small_k_f32(const float* A, const float* B, float* C, int64_t M, int64_t K, int64_t N,
@@ -390,17 +419,31 @@ int mi_tall_skinny_matmul_f32(const float* A, const float* B, float* C, int64_t 
 }
 
 int mi_tensor3d_matmul_f32(const float* A, const float* B, float* out, int64_t N, int64_t M,
-                           int64_t K, int64_t L, void* stream) {
+                           int64_t K, int64_t L, void* workspace, size_t workspace_bytes,
+                           void* stream) {
     if (N < 0 || M < 0) return MI_ERR_BAD_SIZE;
     mi_gemm_args a = dense_args(A, B, out, N * M, K, L, MI_OP_N, MI_OP_N);
-    return mi_gemm_f32(&a, stream);
+    return run_with_workspace(a, workspace, workspace_bytes, stream);
+}
+
+size_t mi_tensor3d_matmul_workspace_bytes(int64_t N, int64_t M, int64_t K, int64_t L) {
+    if (N < 0 || M < 0) return 0;
+    mi_gemm_args a = dense_args(nullptr, nullptr, nullptr, N * M, K, L, MI_OP_N, MI_OP_N);
+    return mi_gemm_workspace_bytes(&a);
 }
 
 int mi_tensor4d_matmul_f32(const float* A, const float* B, float* out, int64_t b, int64_t i,
-                           int64_t j, int64_t l, int64_t k, void* stream) {
+                           int64_t j, int64_t l, int64_t k, void* workspace,
+                           size_t workspace_bytes, void* stream) {
     if (b < 0 || i < 0 || j < 0) return MI_ERR_BAD_SIZE;
     mi_gemm_args a = dense_args(A, B, out, b * i * j, l, k, MI_OP_N, MI_OP_N);
-    return mi_gemm_f32(&a, stream);
+    return run_with_workspace(a, workspace, workspace_bytes, stream);
+}
+
+size_t mi_tensor4d_matmul_workspace_bytes(int64_t b, int64_t i, int64_t j, int64_t l, int64_t k) {
+    if (b < 0 || i < 0 || j < 0) return 0;
+    mi_gemm_args a = dense_args(nullptr, nullptr, nullptr, b * i * j, l, k, MI_OP_N, MI_OP_N);
+    return mi_gemm_workspace_bytes(&a);
 }
 
 int mi_diag_mult_f32(const float* a, const float* B, float* out, int64_t N, int64_t M,
@@ -455,11 +498,18 @@ int mi_sdpa_f16(const void* Q, const void* K, const void* V, void* O, int64_t ba
                               (int)seq, (int)embed, workspace, as_stream(stream)));
 }
 
-int mi_symmetric_matmul_f32(const float* A, const float* B, float* C, int64_t N, void* stream) {
+int mi_symmetric_matmul_f32(const float* A, const float* B, float* C, int64_t N, void* workspace,
+                            size_t workspace_bytes, void* stream) {
     // C = A . B as given (the dense N/N plan), symmetric or not
     mi_gemm_args a = dense_args(A, B, C, N, N, N, MI_OP_N, MI_OP_N);
     a.structure = MI_SYMMETRIC;
-    return mi_gemm_f32(&a, stream);
+    return run_with_workspace(a, workspace, workspace_bytes, stream);
+}
+
+size_t mi_symmetric_matmul_workspace_bytes(int64_t N) {
+    mi_gemm_args a = dense_args(nullptr, nullptr, nullptr, N, N, N, MI_OP_N, MI_OP_N);
+    a.structure = MI_SYMMETRIC;
+    return mi_gemm_workspace_bytes(&a);
 }
 
 int mi_upper_tri_matmul_f32(const float* A, const float* B, float* C, int64_t N, void* stream) {
@@ -475,21 +525,37 @@ int mi_lower_tri_mul_f32(const float* A, const float* B, float* C, int64_t N, vo
 }
 
 int mi_matmul_transposed_a_f32(const float* A, const float* B, float* C, int64_t M, int64_t K,
-                               int64_t N, void* stream) {
+                               int64_t N, void* workspace, size_t workspace_bytes, void* stream) {
     mi_gemm_args a = dense_args(A, B, C, M, K, N, MI_OP_T, MI_OP_N);
-    return mi_gemm_f32(&a, stream);
+    return run_with_workspace(a, workspace, workspace_bytes, stream);
+}
+
+size_t mi_matmul_transposed_a_workspace_bytes(int64_t M, int64_t K, int64_t N) {
+    mi_gemm_args a = dense_args(nullptr, nullptr, nullptr, M, K, N, MI_OP_T, MI_OP_N);
+    return mi_gemm_workspace_bytes(&a);
 }
 
 int mi_matmul_transposed_b_f32(const float* A, const float* B, float* C, int64_t M, int64_t K,
-                               int64_t N, void* stream) {
+                               int64_t N, void* workspace, size_t workspace_bytes, void* stream) {
     mi_gemm_args a = dense_args(A, B, C, M, K, N, MI_OP_N, MI_OP_T);
-    return mi_gemm_f32(&a, stream);
+    return run_with_workspace(a, workspace, workspace_bytes, stream);
+}
+
+size_t mi_matmul_transposed_b_workspace_bytes(int64_t M, int64_t K, int64_t N) {
+    mi_gemm_args a = dense_args(nullptr, nullptr, nullptr, M, K, N, MI_OP_N, MI_OP_T);
+    return mi_gemm_workspace_bytes(&a);
 }
 
 int mi_matmul_transposed_both_f32(const float* A, const float* B, float* C, int64_t M, int64_t K,
-                                  int64_t N, void* stream) {
+                                  int64_t N, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
     mi_gemm_args a = dense_args(A, B, C, M, K, N, MI_OP_T, MI_OP_T);
-    return mi_gemm_f32(&a, stream);
+    return run_with_workspace(a, workspace, workspace_bytes, stream);
+}
+
+size_t mi_matmul_transposed_both_workspace_bytes(int64_t M, int64_t K, int64_t N) {
+    mi_gemm_args a = dense_args(nullptr, nullptr, nullptr, M, K, N, MI_OP_T, MI_OP_T);
+    return mi_gemm_workspace_bytes(&a);
 }
 
 int mi_fill_uniform_f32(float* out, int64_t n, uint64_t seed, int64_t offset, void* stream) {
@@ -500,3 +566,11 @@ int mi_fill_uniform_f32(float* out, int64_t n, uint64_t seed, int64_t offset, vo
 }
 
 }  // extern "C"
+
+namespace {
+int run_with_workspace(mi_gemm_args a, void* workspace, size_t workspace_bytes, void* stream) {
+    a.workspace = workspace;
+    a.workspace_bytes = workspace ? workspace_bytes : 0;
+    return mi_gemm_f32(&a, stream);
+}
+}  // namespace

@@ -400,8 +400,11 @@ at::Tensor symmetric_matmul(const at::Tensor& A, const at::Tensor& B) {
     at::Tensor C = at::empty({N, N}, A.options());
     if (N == 0) return C;
     at::Tensor Ac = A.contiguous(), Bc = B.contiguous();
+    const size_t wsb = mi_symmetric_matmul_workspace_bytes(N);
+    at::Tensor ws = wsb ? at::empty({(int64_t)wsb}, A.options().dtype(at::kByte)) : at::Tensor();
     check_rc(mi_symmetric_matmul_f32(Ac.data_ptr<float>(), Bc.data_ptr<float>(),
-                                     C.data_ptr<float>(), N, current_stream(A)),
+                                     C.data_ptr<float>(), N, wsb ? ws.data_ptr() : nullptr, wsb,
+                                     current_stream(A)),
              "symmetric_matmul_cuda");
     return C;
 }

@@ -19,13 +19,17 @@
 
 namespace mi {
 
-template <int BM_, int BN_, int KMAX_, int WM_ = 64, int WN_ = 64>
+template <int BM_, int BN_, int KMAX_, int WM_ = 64, int WN_ = 64, bool PANEL_B_ = false>
 struct PanelTile {
     static constexpr int BM = BM_, BN = BN_, KMAX = KMAX_;
     static constexpr int WM = WM_, WN = WN_;  // wave tile
     static constexpr int WAVES_M = BM / WM, WAVES_N = BN / WN;
     static constexpr int NW = WAVES_M * WAVES_N, NT = NW * 64;
     static constexpr int TM = WM / 32, TN = WN / 32;
+    // false: the resident panel is A's BM rows and the walk streams B's
+    // BN-column tiles; true: the resident panel is B's BN columns and the walk
+    // streams A's BM-row tiles (work items: column panels x row runs)
+    static constexpr bool PANEL_B = PANEL_B_;
 };
 
 using Panel32 = PanelTile<256, 128, 32>;
@@ -33,20 +37,39 @@ using Panel64 = PanelTile<256, 128, 64>;
 // 128-row panels (M = 128 .. 2047 not a multiple of 256: a 256-row panel
 // would spend MFMAs on padding rows), 8 waves of 64 x 32
 using Panel128x64 = PanelTile<128, 128, 64, 64, 32>;
+// B-resident 256-column panels streaming 128-row A tiles (K <= 64), for
+// large M: the workgroups of one XCD walk the same A tiles in step, so each
+// A tile comes from HBM once per XCD and is shared in its L2, while their
+// stores go to the same rows in different column panels, i.e. to contiguous
+// addresses spread over every channel.  (With the A panel resident, a
+// lockstep walk shares the B tiles the same way but stores every
+// workgroup's tile to the same columns of different rows: measured 16 %
+// slower on 65536^2 x 64 than the rotated walk, whose B tiles, read by
+// every workgroup at its own time, miss L2: 4.3 GB fetched per call.)
+// Measured on 65536^2 x 64: 4.98-5.09 vs 5.25-5.27 ms (N/N; T/N, N/T, T/T
+// 7-10 % faster), 0.15 GB fetched per call; results bitwise equal to the
+// A-resident panel's.  (Holding the accumulators as C instead of C^T, for
+// 4-byte stores each covering two whole 128-byte row segments, measured
+// 6 % slower.)
+using Panel64B = PanelTile<128, 256, 64, 64, 64, true>;
 
 template <class T, bool AT, bool BT, int VEC, bool BIAS>
 __global__ void __launch_bounds__(T::NT) gemm_f32_panel_kernel(const GemmParams p) {
     constexpr bool A_KC = !AT;
     constexpr bool B_KC = BT;
+    constexpr bool PB = T::PANEL_B;
+    static_assert(!(PB && BIAS), "the B-resident panel carries no per-row bias");
     using LA = TileLoader<T::BM, T::KMAX, T::NT, A_KC, VEC>;
     using LB = TileLoader<T::BN, T::KMAX, T::NT, B_KC, VEC>;
-    __shared__ __attribute__((aligned(16))) float sA[LA::ELEMS];
-    __shared__ __attribute__((aligned(16))) float sB[2][LB::ELEMS];
-    // Where LDS has room (the 32-deep and the 128-row panels, not the 256-row
-    // 64-deep one), each wave turns its finished 32 x 32 blocks into
-    // whole-row stores through a [32][36] staging block.
+    // the resident operand has one LDS buffer, the streamed one two
+    constexpr int NBA = PB ? 2 : 1, NBB = PB ? 1 : 2;
+    __shared__ __attribute__((aligned(16))) float sA[NBA][LA::ELEMS];
+    __shared__ __attribute__((aligned(16))) float sB[NBB][LB::ELEMS];
+    // Where LDS has room (the 32-deep and the 128-row panels, not the 64-deep
+    // 256-row or 256-column ones), each wave turns its finished 32 x 32 blocks
+    // into whole-row stores through a [32][36] staging block.
     constexpr bool STAGE_C =
-        (LA::ELEMS + 2 * LB::ELEMS + T::NW * 32 * 36) * 4 <= 160 * 1024;
+        (NBA * LA::ELEMS + NBB * LB::ELEMS + T::NW * 32 * 36) * 4 <= 160 * 1024;
     constexpr int SCLD = 36;
     __shared__ __attribute__((aligned(16))) float sC[STAGE_C ? T::NW * 32 * SCLD : 4];
 
@@ -65,51 +88,83 @@ __global__ void __launch_bounds__(T::NT) gemm_f32_panel_kernel(const GemmParams 
     const bool c_vec = (p.ldc % 4 == 0) && ((reinterpret_cast<uintptr_t>(p.C) & 15u) == 0) &&
                        (p.sc % 4 == 0);
 
-    const int items = p.tiles_m * p.col_splits;
+    // panels along the resident operand, each cut into col_splits runs of
+    // streamed tiles
+    const int tiles_p = PB ? p.tiles_n : p.tiles_m;
+    const int tiles_s = PB ? p.tiles_m : p.tiles_n;
+    const int items = tiles_p * p.col_splits;
     // bias (the panel kernel never splits K) is a separate instantiation, so
     // the plain store path carries no bias code
     constexpr bool add_bias = BIAS;
     LA la;
     LB lb;
     for (int w = blockIdx.x; w < items; w += gridDim.x) {
-        const int tm = w / p.col_splits;
-        const int cs = w - tm * p.col_splits;
-        const int tn_begin = (int)((int64_t)cs * p.tiles_n / p.col_splits);
-        const int tn_end = (int)((int64_t)(cs + 1) * p.tiles_n / p.col_splits);
-        const int m0 = tm * T::BM;
+        const int tp = w / p.col_splits;
+        const int cs = w - tp * p.col_splits;
+        const int ts_begin = (int)((int64_t)cs * tiles_s / p.col_splits);
+        const int ts_end = (int)((int64_t)(cs + 1) * tiles_s / p.col_splits);
+        // the panel's first row (A panel) or column (B panel)
+        const int p0 = tp * (PB ? T::BN : T::BM);
         // per-row bias of this lane's TM output rows, read once per item
         float bias_r[T::TM];
 #pragma unroll
         for (int i = 0; i < T::TM; ++i) {
-            const int row = m0 + wm * T::WM + i * 32 + (lane & 31);
+            const int row = p0 + wm * T::WM + i * 32 + (lane & 31);
             bias_r[i] = 0.f;
             if (add_bias && row < p.M) bias_r[i] = p.bias[row];
         }
 
-        // Each item walks its column run starting at its own rotation, so the
-        // workgroups running together store to different columns: in lockstep
-        // from the same start they would hit addresses that differ only in the
-        // row, i.e. the same few HBM channels.
-        const int run = tn_end - tn_begin;
-        const int rot = run > 0 ? w % run : 0;
-        auto col_tile = [&](int step) {
+        // Order of the walk.  A panel: each item starts at its own rotation,
+        // so the workgroups running together store to different columns (in
+        // lockstep from the same start they would hit addresses that differ
+        // only in the row, i.e. the same few HBM channels).  B panel: the
+        // items of one XCD (consecutive workgroups are dealt round-robin over
+        // the 8 XCDs) start at the same row tile and walk in step, sharing
+        // each A tile in their L2; the XCDs start 1/8 of the run apart.
+        const int run = ts_end - ts_begin;
+        const int rot = run <= 0 ? 0
+                        : PB   ? (int)((int64_t)(blockIdx.x % kNumXcd) * run / kNumXcd)
+                               : w % run;
+        auto s_tile = [&](int step) {
             const int q = step + rot;
-            return tn_begin + (q >= run ? q - run : q);
+            return ts_begin + (q >= run ? q - run : q);
+        };
+        // output tile origin of streamed tile ts
+        auto tile_m0 = [&](int ts) { return PB ? ts * T::BM : p0; };
+        auto tile_n0 = [&](int ts) { return PB ? p0 : ts * T::BN; };
+        // streamed-tile load into registers / into LDS buffer `buf`
+        auto s_load = [&](int ts, int t) {
+            if constexpr (PB)
+                la.load(A, p.lda, ts * T::BM, p.M, 0, p.K, t);
+            else
+                lb.load(B, p.ldb, ts * T::BN, p.N, 0, p.K, t);
+        };
+        auto s_store = [&](int buf, int t) {
+            if constexpr (PB)
+                la.store(sA[buf], t);
+            else
+                lb.store(sB[buf], t);
         };
 
         // every wave is past the previous item's last barrier: LDS is free.
-        // (lda and the thread index are made opaque per item: otherwise the
-        // panel load's per-slot rows and addresses, invariant across items,
-        // are hoisted out of the item loop and kept live through it -- with A
-        // stored K x M more than the 64-deep 256-row panel's 256 VGPRs hold.)
-        int64_t lda_item = p.lda;
-        int tid_a = tid;
-        asm volatile("" : "+s"(lda_item), "+v"(tid_a));
-        la.load(A, lda_item, m0, p.M, 0, p.K, tid_a);
-        la.store(sA, tid_a);
+        // (the leading dimension and the thread index are made opaque per
+        // item: otherwise the panel load's per-slot rows and addresses,
+        // invariant across items, are hoisted out of the item loop and kept
+        // live through it -- with A stored K x M more than the 64-deep
+        // 256-row panel's 256 VGPRs hold.)
+        int64_t ld_item = PB ? p.ldb : p.lda;
+        int tid_p = tid;
+        asm volatile("" : "+s"(ld_item), "+v"(tid_p));
+        if constexpr (PB) {
+            lb.load(B, ld_item, p0, p.N, 0, p.K, tid_p);
+            lb.store(sB[0], tid_p);
+        } else {
+            la.load(A, ld_item, p0, p.M, 0, p.K, tid_p);
+            la.store(sA[0], tid_p);
+        }
         if (run > 0) {
-            lb.load(B, p.ldb, col_tile(0) * T::BN, p.N, 0, p.K, tid);
-            lb.store(sB[0], tid);
+            s_load(s_tile(0), tid);
+            s_store(0, tid);
         }
         __syncthreads();
 
@@ -119,12 +174,13 @@ __global__ void __launch_bounds__(T::NT) gemm_f32_panel_kernel(const GemmParams 
         // accumulator sets: while tile s is computed, tile s-1 is stored, a
         // few 16-byte stores after each k-block of MFMAs, so stores and MFMAs
         // overlap inside each wave instead of alternating.
-        // (the 256-row 64-deep panel takes it only when K fills all its
+        // (the 64-deep 256-row panel takes it only when K fills all its
         // k-blocks: there a per-k-block skip test cost 6 % on the MFMA-bound
         // tall-skinny shape)
         constexpr bool SKIP_KB = T::KMAX == 32 || T::BM == 128;
-        const bool fast = c_vec && m0 + T::BM <= p.M && (int64_t)tn_end * T::BN <= p.N && run >= 2 &&
-                          (SKIP_KB || nkb == T::KMAX / 8);
+        const bool interior = PB ? (p0 + T::BN <= p.N && (int64_t)ts_end * T::BM <= p.M)
+                                 : (p0 + T::BM <= p.M && (int64_t)ts_end * T::BN <= p.N);
+        const bool fast = c_vec && interior && run >= 2 && (SKIP_KB || nkb == T::KMAX / 8);
         if (fast) {
             constexpr int KBLK = T::KMAX / 8;
             // store units per wave per tile: 16-byte stores, or whole blocks
@@ -133,7 +189,8 @@ __global__ void __launch_bounds__(T::NT) gemm_f32_panel_kernel(const GemmParams 
             constexpr int SPK = (NST + KBLK - 1) / KBLK;
             f16v acc0[T::TM][T::TN], acc1[T::TM][T::TN];
 
-            auto store_one = [&](const f16v (&acc)[T::TM][T::TN], int q, int tn) {
+            auto store_one = [&](const f16v (&acc)[T::TM][T::TN], int q, int ts) {
+                const int m0 = tile_m0(ts), n0 = tile_n0(ts);
                 if constexpr (STAGE_C) {
                     // block (i, j): write it in its C^T register layout (lane l:
                     // row l % 32, columns 8 g + 4 h .. +3), read it back as rows
@@ -151,7 +208,7 @@ __global__ void __launch_bounds__(T::NT) gemm_f32_panel_kernel(const GemmParams 
                         *reinterpret_cast<f4*>(buf + (lane & 31) * SCLD + g * 8 + half * 4) = v;
                     }
                     const int r0 = m0 + wm * T::WM + i * 32;
-                    const int c0 = tn * T::BN + wn * T::WN + j * 32 + (lane & 7) * 4;
+                    const int c0 = n0 + wn * T::WN + j * 32 + (lane & 7) * 4;
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const int rr = r * 8 + (lane >> 3);
@@ -168,17 +225,17 @@ __global__ void __launch_bounds__(T::NT) gemm_f32_panel_kernel(const GemmParams 
                 } else {
                     const int i = q / (T::TN * 4), j = (q / 4) % T::TN, g = q % 4;
                     const int row = m0 + wm * T::WM + i * 32 + (lane & 31);
-                    const int col = tn * T::BN + wn * T::WN + j * 32 + g * 8 + half * 4;
+                    const int col = n0 + wn * T::WN + j * 32 + g * 8 + half * 4;
                     f4 v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
                             acc[i][j][4 * g + 3]};
                     if (add_bias) v += bias_r[i];
                     *reinterpret_cast<f4*>(C + (int64_t)row * p.ldc + col) = v;
                 }
             };
-            // MFMAs of one tile from LDS buffer `buf` into acc_c; with
+            // MFMAs of one tile from LDS buffers As / Bs into acc_c; with
             // STORE, the previous tile's stores ride along, SPK per k-block.
-            auto tile_step = [&](f16v (&acc_c)[T::TM][T::TN], const float* Bs,
-                                 const f16v (&acc_s)[T::TM][T::TN], int tn_s, bool store) {
+            auto tile_step = [&](f16v (&acc_c)[T::TM][T::TN], const float* As, const float* Bs,
+                                 const f16v (&acc_s)[T::TM][T::TN], int ts_s, bool store) {
 #pragma unroll
                 for (int i = 0; i < T::TM; ++i)
 #pragma unroll
@@ -192,7 +249,7 @@ __global__ void __launch_bounds__(T::NT) gemm_f32_panel_kernel(const GemmParams 
                     if (!SKIP_KB || kb < nkb) {
                         float a[T::TM][4], b[T::TN][4];
 #pragma unroll
-                        for (int i = 0; i < T::TM; ++i) LA::frag(sA, wm * T::WM + i * 32, kb, lane, a[i]);
+                        for (int i = 0; i < T::TM; ++i) LA::frag(As, wm * T::WM + i * 32, kb, lane, a[i]);
 #pragma unroll
                         for (int j = 0; j < T::TN; ++j) LB::frag(Bs, wn * T::WN + j * 32, kb, lane, b[j]);
 #pragma unroll
@@ -207,30 +264,31 @@ __global__ void __launch_bounds__(T::NT) gemm_f32_panel_kernel(const GemmParams 
                     if (store) {
 #pragma unroll
                         for (int qq = 0; qq < SPK; ++qq)
-                            if (kb * SPK + qq < NST) store_one(acc_s, kb * SPK + qq, tn_s);
+                            if (kb * SPK + qq < NST) store_one(acc_s, kb * SPK + qq, ts_s);
                         // keep these stores among this k-block's MFMAs: only
                         // MFMAs (0x8) and LDS reads (0x100) may move across
                         __builtin_amdgcn_sched_barrier(0x108);
                     }
                 }
             };
-            // one step: prefetch the next B tile, compute (and store the
-            // previous tile), then put the prefetched tile in the other buffer
+            // one step: prefetch the next streamed tile, compute (and store
+            // the previous tile), then put the prefetched tile in the other buffer
             // The 64-deep 256-row panel with A stored K x M runs at the 256-VGPR
-            // limit: there the B loader's addresses are recomputed each step
-            // from an opaque copy of the thread index instead of being kept
-            // live (and spilled) across the column walk.
+            // limit: there the streamed loader's addresses are recomputed each
+            // step from an opaque copy of the thread index instead of being kept
+            // live (and spilled) across the walk.
             constexpr bool TIGHT = AT && T::KMAX == 64 && T::BM == 256;
             auto step_fn = [&](int step, f16v (&acc_c)[T::TM][T::TN],
                                const f16v (&acc_s)[T::TM][T::TN], bool store) {
                 const int buf = step & 1;
-                const int tn_next = col_tile(step + 1 < run ? step + 1 : step);
-                int tid_b = tid;
-                if constexpr (TIGHT) asm volatile("" : "+v"(tid_b));
-                lb.load(B, p.ldb, tn_next * T::BN, p.N, 0, p.K, tid_b);
-                tile_step(acc_c, sB[buf], acc_s, store ? col_tile(step - 1) : 0, store);
-                if constexpr (TIGHT) asm volatile("" : "+v"(tid_b));
-                lb.store(sB[buf ^ 1], tid_b);
+                const int ts_next = s_tile(step + 1 < run ? step + 1 : step);
+                int tid_s = tid;
+                if constexpr (TIGHT) asm volatile("" : "+v"(tid_s));
+                s_load(ts_next, tid_s);
+                tile_step(acc_c, sA[PB ? buf : 0], sB[PB ? 0 : buf], acc_s,
+                          store ? s_tile(step - 1) : 0, store);
+                if constexpr (TIGHT) asm volatile("" : "+v"(tid_s));
+                s_store(buf ^ 1, tid_s);
                 __syncthreads();
             };
 
@@ -243,21 +301,22 @@ __global__ void __launch_bounds__(T::NT) gemm_f32_panel_kernel(const GemmParams 
             if (step < run) {
                 step_fn(step, acc1, acc0, true);
 #pragma unroll
-                for (int q = 0; q < NST; ++q) store_one(acc1, q, col_tile(step));
+                for (int q = 0; q < NST; ++q) store_one(acc1, q, s_tile(step));
             } else {
 #pragma unroll
-                for (int q = 0; q < NST; ++q) store_one(acc0, q, col_tile(run - 1));
+                for (int q = 0; q < NST; ++q) store_one(acc0, q, s_tile(run - 1));
             }
             continue;
         }
 
         for (int step = 0; step < run; ++step) {
             const int buf = step & 1;
-            const int tn = col_tile(step);
+            const int ts = s_tile(step);
             // unconditional prefetch (the last step re-reads its own tile, never
             // used) so each load is awaited in the step that issued it
-            const int tn_next = col_tile(step + 1 < run ? step + 1 : step);
-            lb.load(B, p.ldb, tn_next * T::BN, p.N, 0, p.K, tid);
+            s_load(s_tile(step + 1 < run ? step + 1 : step), tid);
+            const float* const As = sA[PB ? buf : 0];
+            const float* const Bs = sB[PB ? 0 : buf];
 
             f16v acc[T::TM][T::TN];
 #pragma unroll
@@ -271,9 +330,9 @@ __global__ void __launch_bounds__(T::NT) gemm_f32_panel_kernel(const GemmParams 
                 if (kb < nkb) {
                     float a[T::TM][4], b[T::TN][4];
 #pragma unroll
-                    for (int i = 0; i < T::TM; ++i) LA::frag(sA, wm * T::WM + i * 32, kb, lane, a[i]);
+                    for (int i = 0; i < T::TM; ++i) LA::frag(As, wm * T::WM + i * 32, kb, lane, a[i]);
 #pragma unroll
-                    for (int j = 0; j < T::TN; ++j) LB::frag(sB[buf], wn * T::WN + j * 32, kb, lane, b[j]);
+                    for (int j = 0; j < T::TN; ++j) LB::frag(Bs, wn * T::WN + j * 32, kb, lane, b[j]);
 #pragma unroll
                     for (int s = 0; s < 4; ++s)
 #pragma unroll
@@ -285,13 +344,13 @@ __global__ void __launch_bounds__(T::NT) gemm_f32_panel_kernel(const GemmParams 
                 }
             }
 
-            // the next B tile goes to LDS before this tile's stores are issued
-            // (see the file comment: waits then never cover fresh stores)
-            lb.store(sB[buf ^ 1], tid);
+            // the next streamed tile goes to LDS before this tile's stores are
+            // issued (see the file comment: waits then never cover fresh stores)
+            s_store(buf ^ 1, tid);
 
             // block (i, j) holds C^T: lane l owns row l%32, registers 4g..4g+3
             // its columns 8g + 4*half .. +3
-            const int n0 = tn * T::BN;
+            const int m0 = tile_m0(ts), n0 = tile_n0(ts);
 #pragma unroll
             for (int i = 0; i < T::TM; ++i)
 #pragma unroll
@@ -344,6 +403,9 @@ hipError_t launch_panel(const GemmLaunch& g, hipStream_t s) {
     if (g.cfg == kCfgPanel32)
         return g.vec == 4 ? launch_panel_one<Panel32, AT, BT, 4>(g, s)
                           : launch_panel_one<Panel32, AT, BT, 1>(g, s);
+    if (g.cfg == kCfgPanel64B)
+        return g.vec == 4 ? launch_panel_one<Panel64B, AT, BT, 4>(g, s)
+                          : launch_panel_one<Panel64B, AT, BT, 1>(g, s);
     if (g.cfg == kCfgPanel128x64)
         return g.vec == 4 ? launch_panel_one<Panel128x64, AT, BT, 4>(g, s)
                           : launch_panel_one<Panel128x64, AT, BT, 1>(g, s);

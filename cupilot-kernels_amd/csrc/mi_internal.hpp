@@ -22,14 +22,19 @@ namespace mi {
 //   9   128 x 128        4      64 x 64     32-deep slices, direct-staged only (~65 KiB, 2 WGs/CU)
 //   10  64 x 64          8      64 x 64     each wave one 8-deep k-block of every 64-deep
 //                                           slice, 4-stage direct ring (~130 KiB, 1 WG/CU)
+//   11  128 x 128        8      32 x 64     32-deep slices, direct-staged, A K-contiguous
+//   12  128 x 256 panel  8      64 x 64     B panel resident, A row tiles streamed,
+//                                           K <= 64 (~136 KiB, 1 WG/CU), no row bias
 enum TileCfgId {
     kCfg64 = 1, kCfg128 = 2, kCfg256 = 3, kCfg128K32 = 4, kCfg128K64 = 5,
     kCfgPanel32 = 6, kCfgPanel64 = 7, kCfgPanel128x64 = 8, kCfg128B32 = 9, kCfg64W = 10,
-    kCfg128W8 = 11, kNumCfg = 12
+    kCfg128W8 = 11, kCfgPanel64B = 12, kNumCfg = 13
 };
 inline bool is_panel_cfg(int id) {
-    return id == kCfgPanel32 || id == kCfgPanel64 || id == kCfgPanel128x64;
+    return id == kCfgPanel32 || id == kCfgPanel64 || id == kCfgPanel128x64 || id == kCfgPanel64B;
 }
+// panel configs whose resident panel is B (work items: column panels)
+inline bool is_panel_b_cfg(int id) { return id == kCfgPanel64B; }
 
 struct CfgInfo {
     int bm, bn, bk, threads;
@@ -47,6 +52,7 @@ inline CfgInfo cfg_info(int id) {
         case kCfg128B32: return {128, 128, 32, 256};
         case kCfg64W: return {64, 64, 64, 512};
         case kCfg128W8: return {128, 128, 32, 512};
+        case kCfgPanel64B: return {128, 256, 64, 512};
         default: return {0, 0, 0, 0};
     }
 }
@@ -71,7 +77,7 @@ struct GemmLaunch {
     int group_m;
     int num_tiles;        // output tiles per (split, batch): tiles_m*tiles_n, or tiles_m^2 (triangular)
     int grid_x;           // workgroups per (split, batch), <= num_tiles; each walks its tiles
-    int col_splits;       // panel configs: column runs per A row panel
+    int col_splits;       // panel configs: runs of streamed tiles per resident panel
     int tri_cap;          // > 0: chunked triangular work list (tri_item) of the direct kernel
     // stream-K (sk_tiles > 0; direct-staged 128 / 256 tiles, batch 1, split 1):
     // the first sk_dp tiles data-parallel, the last sk_tiles dealt out as

@@ -67,19 +67,32 @@ int mi_gemm_f32_noalloc(const mi_gemm_args* args, void* stream) {
     // The plan mi_gemm_f32 uses with a workspace of mi_gemm_workspace_bytes:
     // the same kernels, split and reduction order, so the same result bit
     // for bit.  (0 for an invalid problem: mi_gemm_f32 reports it below.)
-    size_t need = mi_gemm_workspace_bytes(&a);
-    if (need > kScratchBytes && (a.plan_override & MI_PLAN_NO_PACK) == 0) {
-        // a plan that packs the operands (mostly their copies) past the
-        // scratch: the unpacked plan instead
-        a.plan_override |= MI_PLAN_NO_PACK;
-        need = mi_gemm_workspace_bytes(&a);
-    }
-    if (need > kScratchBytes) return MI_ERR_SCRATCH_LIMIT;
+    const size_t need = mi_gemm_workspace_bytes(&a);
     void* ws = nullptr;
-    const int rc = scratch_on_current_device(&ws);
+    int rc = scratch_on_current_device(&ws);
     if (rc != MI_OK) return rc;
-    a.workspace = need ? ws : nullptr;
-    a.workspace_bytes = need;
+    if (need <= kScratchBytes) {
+        a.workspace = need ? ws : nullptr;
+        a.workspace_bytes = need;
+        return mi_gemm_f32(&a, stream);
+    }
+    // The preferred plan wants more scratch than the array holds: plan with
+    // the array as the workspace limit instead.  The planner then picks among
+    // the plans that fit (fewer splits, stream-K, no packed copies, ...; an
+    // unsplit plan needing none always exists), so the result may differ from
+    // mi_gemm_f32's with its preferred workspace in the last bits.  Only a
+    // plan_override that forces a plan needing more is refused, before any
+    // launch.
+    a.workspace = ws;
+    a.workspace_bytes = kScratchBytes;
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        return MI_ERR_NO_DEVICE;
+    mi_plan p{};
+    rc = mi_gemm_plan(&a, cus, &p);
+    if (rc != MI_OK) return rc;
+    if (p.workspace_bytes > kScratchBytes) return MI_ERR_SCRATCH_LIMIT;
     return mi_gemm_f32(&a, stream);
 }
 

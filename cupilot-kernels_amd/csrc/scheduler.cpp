@@ -46,7 +46,7 @@ struct CfgModel {
 // 8192 x 3072 x 16384: 141 with 16-byte operand rows, N/N plus all four
 // layouts of 12 of them, and 72 random ones in all four layouts whose rows or
 // K are not multiples of 4 floats (or K of 16) (tests/data/plan_timings_mi355x.csv,
-// fitted by plan_fit.py: a local search on the ranking from the previous
+// fitted offline: a local search on the ranking from the previous
 // constants).  The plan it picks is on average 0.7 % slower than the fastest
 // one measured, 11 % at worst.  The single-slice configs (K <= 32 / 64) take the 128 tile's
 // constants with half its exposed store time.
@@ -113,6 +113,7 @@ int resident_wgs(int cfg) {
         case kCfgPanel32: return 1;
         case kCfgPanel64: return 1;
         case kCfgPanel128x64: return 1;
+        case kCfgPanel64B: return 1;
         case kCfg128B32: return 2;
         case kCfg128W8: return 2;
         case kCfg64W: return 1;
@@ -249,7 +250,8 @@ int plan_core(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
         (override_cfg != kCfg64W || w64_ok) &&
         !((override_cfg == kCfg128K32 || override_cfg == kCfg128K64 || is_panel_cfg(override_cfg)) &&
           a.K > cfg_info(override_cfg).bk) &&
-        !(is_panel_cfg(override_cfg) && a.structure != MI_DENSE);
+        !(is_panel_cfg(override_cfg) && a.structure != MI_DENSE) &&
+        !(is_panel_b_cfg(override_cfg) && a.bias_m != nullptr);
     // Triangular products with N a multiple of 256 and operands the direct
     // kernel can stage run on the 256-tile direct kernel over the chunked
     // longest-first work list (tri_item) when the structure has a tile for
@@ -287,6 +289,17 @@ int plan_core(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
         // The same for M an odd multiple of 128 (the 1x1 convolution's
         // output channels): 128-row panels, none of them padding.
         best_cfg = kCfgPanel128x64;
+    } else if (a.K > 32 && a.K <= 64 && a.bias_m == nullptr && (a.N % 256 == 0 || a.N >= 2048) &&
+               (a.M % 128 == 0 || a.M >= 1024) &&
+               cdiv(a.M, 128) * cdiv(a.N, 256) * std::max<int64_t>(1, a.batch) >=
+                   2 * (int64_t)num_cus) {
+        // 33-64 deep with a large output and no row bias: the B-resident
+        // panel, whose workgroups share A tiles in L2 and store to
+        // contiguous rows (65536^2 x 64: 4.98-5.09 vs 5.25-5.49 ms for the
+        // A-resident panel, all four layouts; 4096 x 2048 x 64: 19 vs 23 us).
+        // Its panels are 256 columns and its streamed tiles 128 rows, each
+        // filled to at least 7/8.
+        best_cfg = kCfgPanel64B;
     } else if (a.K <= 64 && (a.M % 256 == 0 || a.M >= 2048) &&
                cdiv(a.M, 256) * cdiv(a.N, 128) * std::max<int64_t>(1, a.batch) >=
                    2 * (int64_t)num_cus) {
@@ -443,12 +456,15 @@ int plan_core(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
     // from a counter instead: one persistent workgroup per CU.
     if (a.structure != MI_DENSE)
         grid = tri_cap >= 2 ? std::min<int64_t>(num_cus, num_tiles) : num_tiles;
-    // Panel configs: each work item is one A row panel times a run of column
+    // Panel configs: each work item is one resident panel times a run of streamed
     // tiles; enough runs per panel to give every resident workgroup one.
     int64_t col_splits = 1;
     if (is_panel_cfg(best_cfg)) {
-        col_splits = std::min<int64_t>(tiles_n, std::max<int64_t>(1, cdiv(slots, tiles_m * batch)));
-        grid = std::min<int64_t>(tiles_m * col_splits, std::max<int64_t>(1, slots / batch));
+        // (B-resident panels: one per column tile, runs of row tiles)
+        const int64_t panels = is_panel_b_cfg(best_cfg) ? tiles_n : tiles_m;
+        const int64_t streamed = is_panel_b_cfg(best_cfg) ? tiles_m : tiles_n;
+        col_splits = std::min<int64_t>(streamed, std::max<int64_t>(1, cdiv(slots, panels * batch)));
+        grid = std::min<int64_t>(panels * col_splits, std::max<int64_t>(1, slots / batch));
     }
     // The direct-staged 128 tile with at least two waves of work items runs
     // one tile per workgroup instead: a finished tile's stores then leave
@@ -567,8 +583,10 @@ mi_gemm_args packed_problem(const mi_gemm_args& a, void* workspace, size_t works
     p.batch = 1;
     p.stride_a = p.stride_b = 0;
     // forced packing keeps the other override bits for the packed product;
-    // the planner's own choice keeps only the raster grouping
-    const int32_t keep = (a.plan_override & MI_PLAN_PACK) ? ~(MI_PLAN_NO_PACK | MI_PLAN_PACK) : (0x7FF << 20);
+    // the planner's own choice keeps the raster grouping and "never
+    // stream-K" (bit 5), which holds for whatever product runs
+    const int32_t keep =
+        (a.plan_override & MI_PLAN_PACK) ? ~(MI_PLAN_NO_PACK | MI_PLAN_PACK) : ((0x7FF << 20) | 0x20);
     p.plan_override = (a.plan_override & keep) | MI_PLAN_NO_PACK;
     const size_t pb = pack_bytes(a, kp);
     p.workspace = ws && workspace_bytes > pb ? ws + pb : nullptr;

@@ -50,8 +50,8 @@ typedef enum {
     MI_ERR_WORKSPACE = -6,      /* workspace missing or too small */
     MI_ERR_NO_DEVICE = -7,      /* no HIP device / device query failed */
     MI_ERR_ALIGNMENT = -8,      /* a pointer is not 16-byte aligned where required */
-    MI_ERR_SCRATCH_LIMIT = -9   /* mi_gemm_f32_noalloc: the problem's plan needs more
-                                   scratch than MI_NOALLOC_SCRATCH_BYTES */
+    MI_ERR_SCRATCH_LIMIT = -9   /* mi_gemm_f32_noalloc: a plan_override forces a plan
+                                   needing more scratch than MI_NOALLOC_SCRATCH_BYTES */
 } mi_status;
 
 typedef enum { MI_OP_N = 0, MI_OP_T = 1 } mi_op;
@@ -151,11 +151,13 @@ MI_API size_t mi_gemm_workspace_bytes(const mi_gemm_args* args);
  * scratch (split-K and stream-K partial tiles, packed operand copies) goes to
  * a fixed MI_NOALLOC_SCRATCH_BYTES array the library holds on each device
  * (for the life of the process) instead.
- *   - A plan that packs its operands (mi_plan.packed) into more scratch than
- *     that is replaced by the unpacked plan (MI_PLAN_NO_PACK), whose result
- *     may then differ from mi_gemm_f32's in the last bits.
- *   - A problem whose plan needs more scratch than that returns
- *     MI_ERR_SCRATCH_LIMIT before anything is launched.
+ *   - A problem whose preferred plan needs more scratch than that is planned
+ *     as mi_gemm_f32 plans it with a workspace of MI_NOALLOC_SCRATCH_BYTES
+ *     bytes (fewer splits, or no packed copies; an unsplit plan needing no
+ *     scratch always exists), so its result may then differ from
+ *     mi_gemm_f32's with the preferred workspace in the last bits.
+ *   - Only a plan_override that forces a plan needing more scratch than that
+ *     returns MI_ERR_SCRATCH_LIMIT, before anything is launched.
  *   - The first call on a device looks up that device's copy of the array
  *     (hipGetSymbolAddress, once per device); make that first call outside
  *     graph capture.  Calls, and captures, after it allocate nothing.
@@ -208,20 +210,36 @@ MI_API int mi_gemm_sk_fixup_of(const mi_gemm_args* args, int32_t num_cus, int64_
 
 /* ---- one entry point per reference operator ------------------------------ */
 
+/* Workspace of the dense product entry points (those taking `workspace,
+ * workspace_bytes`): device memory, 256-byte aligned, of the size their
+ * *_workspace_bytes query returns for the same extents -- then the call runs
+ * the plan mi_gemm_f32 runs with the workspace mi_gemm_workspace_bytes asks
+ * for (split-K, stream-K, packed operand copies; the same bits as the
+ * operator layer).  A smaller workspace (NULL with 0 bytes included) restricts
+ * the scheduler to the plans that fit it, down to those needing none, and the
+ * result may then differ in the last bits.  The query is 0 when no plan of the
+ * problem wants one. */
+
 /* kernels/1_Square_matrix_multiplication_best_kernel.cu:189 matmul_cuda(A, B):
  * C = A . B, all N x N. */
-MI_API int mi_square_matmul_f32(const float* A, const float* B, float* C, int64_t N, void* stream);
+MI_API size_t mi_square_matmul_workspace_bytes(int64_t N);
+MI_API int mi_square_matmul_f32(const float* A, const float* B, float* C, int64_t N,
+                                void* workspace, size_t workspace_bytes, void* stream);
 
 /* kernels/2_Standard_matrix_multiplication_best_kernel.cu:117 matmul_cuda and
  * kernels/8_Matmul_with_irregular_shapes_best_kernel.cu:155 matmul_cuda:
  * C (M x N) = A (M x K) . B (K x N), any sizes. */
+MI_API size_t mi_matmul_workspace_bytes(int64_t M, int64_t K, int64_t N);
 MI_API int mi_matmul_f32(const float* A, const float* B, float* C,
-                  int64_t M, int64_t K, int64_t N, void* stream);
+                  int64_t M, int64_t K, int64_t N,
+                  void* workspace, size_t workspace_bytes, void* stream);
 
 /* kernels/3_Batched_matrix_multiplication_best_kernel.cu:113 batched_matmul_cuda:
  * C[b] (M x N) = A[b] (M x K) . B[b] (K x N). */
+MI_API size_t mi_batched_matmul_workspace_bytes(int64_t batch, int64_t M, int64_t K, int64_t N);
 MI_API int mi_batched_matmul_f32(const float* A, const float* B, float* C,
-                          int64_t batch, int64_t M, int64_t K, int64_t N, void* stream);
+                          int64_t batch, int64_t M, int64_t K, int64_t N,
+                          void* workspace, size_t workspace_bytes, void* stream);
 
 /* kernels/4_Matrix_vector_multiplication_best_kernel.cu:84 gemv_cuda:
  * y (M) = A (M x K) . x (K).  Uses a workspace of mi_gemv_workspace_bytes(M, K)
@@ -251,14 +269,18 @@ MI_API int mi_tall_skinny_matmul_f32(const float* A, const float* B, float* C,
 
 /* kernels/10_3D_tensor_matrix_multiplication_best_kernel.cu:180 batched_matmul_cuda:
  * out[n] (M x L) = A[n] (M x K) . B (K x L), A is N x M x K. */
+MI_API size_t mi_tensor3d_matmul_workspace_bytes(int64_t N, int64_t M, int64_t K, int64_t L);
 MI_API int mi_tensor3d_matmul_f32(const float* A, const float* B, float* out,
-                           int64_t N, int64_t M, int64_t K, int64_t L, void* stream);
+                           int64_t N, int64_t M, int64_t K, int64_t L,
+                           void* workspace, size_t workspace_bytes, void* stream);
 
 /* kernels/11_4D_tensor_matrix_multiplication_best_kernel.cu:132 tensor_matmul_cuda:
  * out[b,i,j,:] = A[b,i,j,:] . B, A is b x i x j x l, B is l x k. */
+MI_API size_t mi_tensor4d_matmul_workspace_bytes(int64_t b, int64_t i, int64_t j, int64_t l,
+                                                 int64_t k);
 MI_API int mi_tensor4d_matmul_f32(const float* A, const float* B, float* out,
                            int64_t b, int64_t i, int64_t j, int64_t l, int64_t k,
-                           void* stream);
+                           void* workspace, size_t workspace_bytes, void* stream);
 
 /* kernels/12_Matmul_with_diagonal_matrices_best_kernel.cu:43 diag_mult_cuda:
  * out (N x M) = diag(a) . B, a has length N; one fp32 multiply per element. */
@@ -299,8 +321,9 @@ MI_API int mi_sdpa_f16(const void* Q, const void* K, const void* V, void* O, int
  * symmetric_matmul_cuda: C = A . B for N x N A and B (meant for symmetric
  * inputs; like the reference kernel, :57 and :134-151, it relies on no
  * symmetry and returns A . B for any input). */
+MI_API size_t mi_symmetric_matmul_workspace_bytes(int64_t N);
 MI_API int mi_symmetric_matmul_f32(const float* A, const float* B, float* C, int64_t N,
-                            void* stream);
+                            void* workspace, size_t workspace_bytes, void* stream);
 
 /* kernels/14_Matmul_for_upper_triangular_matrices_best_kernel.cu:135
  * upper_tri_matmul_cuda: C = triu(triu(A) . triu(B)), N x N; zero tiles are
@@ -315,18 +338,24 @@ MI_API int mi_lower_tri_mul_f32(const float* A, const float* B, float* C, int64_
 
 /* kernels/16_Matmul_with_transposed_A_best_kernel.cu:124 matmul_transposed_cuda:
  * C (M x N) = A^T . B with A stored K x M and B K x N. */
+MI_API size_t mi_matmul_transposed_a_workspace_bytes(int64_t M, int64_t K, int64_t N);
 MI_API int mi_matmul_transposed_a_f32(const float* A, const float* B, float* C,
-                               int64_t M, int64_t K, int64_t N, void* stream);
+                               int64_t M, int64_t K, int64_t N,
+                               void* workspace, size_t workspace_bytes, void* stream);
 
 /* kernels/17_Matmul_with_transposed_B_best_kernel.cu:267 matmul_cuda:
  * C (M x N) = A . B^T with A M x K and B stored N x K. */
+MI_API size_t mi_matmul_transposed_b_workspace_bytes(int64_t M, int64_t K, int64_t N);
 MI_API int mi_matmul_transposed_b_f32(const float* A, const float* B, float* C,
-                               int64_t M, int64_t K, int64_t N, void* stream);
+                               int64_t M, int64_t K, int64_t N,
+                               void* workspace, size_t workspace_bytes, void* stream);
 
 /* kernels/18_Matmul_with_transposed_both_best_kernel.cu:152 matmul_transposed_cuda:
  * C (M x N) = A^T . B^T with A stored K x M and B stored N x K. */
+MI_API size_t mi_matmul_transposed_both_workspace_bytes(int64_t M, int64_t K, int64_t N);
 MI_API int mi_matmul_transposed_both_f32(const float* A, const float* B, float* C,
-                                  int64_t M, int64_t K, int64_t N, void* stream);
+                                  int64_t M, int64_t K, int64_t N,
+                                  void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- utilities ------------------------------------------------------------ */
 

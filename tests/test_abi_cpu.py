@@ -96,7 +96,7 @@ def test_plan_is_sane(ck, M, N, K, batch):
     rc, p = ck.abi.plan(M, N, K, batch=batch, workspace_bytes=1 << 40)
     assert rc == 0
     assert p.block_m in (64, 128, 256) and p.block_k in (16, 32, 64)
-    assert p.block_m == p.block_n or p.plan_id in (6, 7, 8)
+    assert p.block_m == p.block_n or p.plan_id in (6, 7, 8, 12)
     assert p.tiles_m * p.block_m >= M > (p.tiles_m - 1) * p.block_m
     assert p.tiles_n * p.block_n >= N > (p.tiles_n - 1) * p.block_n
     assert p.num_tiles == p.tiles_m * p.tiles_n
@@ -105,7 +105,7 @@ def test_plan_is_sane(ck, M, N, K, batch):
     # batched: per batch, the fewest workgroups that keep each one's tile
     # count, so every workgroup walks the same number of tiles, +-1
     assert 1 <= p.grid <= p.num_tiles or p.stream_k
-    if p.plan_id not in (6, 7, 8):  # panel plans size the grid by row panels x column runs
+    if p.plan_id not in (6, 7, 8, 12):  # panel plans size the grid by panels x runs of streamed tiles
         if batch > 1:
             per = -(-p.num_tiles // p.grid)
             assert p.num_tiles > (per - 1) * p.grid and -(-p.num_tiles // (p.grid - 1 or 1)) > per or p.grid == 1
@@ -127,6 +127,16 @@ def test_plan_is_sane(ck, M, N, K, batch):
 
 def test_plan_choices_for_baseline_configs(ck):
     assert ck.abi.plan(8192, 8192, 8192)[1].block_m == 256
+    # tall-skinny (K = 64, no bias): the B-resident panel in every layout; one
+    # workgroup per column panel walking all 512 row tiles
+    for ops in [(0, 0), (1, 0), (0, 1), (1, 1)]:
+        rc, p = ck.abi.plan(65536, 65536, 64, op_a=ops[0], op_b=ops[1])
+        assert rc == 0 and p.plan_id == ck.abi.CFG_PANEL64B and (p.block_m, p.block_n) == (128, 256)
+        assert p.grid == 256 and p.tiles_n == 256 and p.tiles_m == 512
+    # small-K (K = 32): the 32-deep A-resident panel; the 1x1 convolution
+    # (bias, 128 output channels): the 128-row A-resident panel
+    assert ck.abi.plan(16384, 16384, 32)[1].plan_id == ck.abi.CFG_PANEL32
+    assert ck.abi.plan(128, 65536, 64, batch=16)[1].plan_id == ck.abi.CFG_PANEL128
     rc, p = ck.abi.plan(256, 256, 1 << 20, workspace_bytes=1 << 40)
     assert p.split_k >= 64, "large-K must split K to fill 256 CUs"
 
@@ -521,6 +531,16 @@ def test_stream_k_applies_only_where_it_can(ck):
     # bit 5 keeps the cost model off stream-K
     rc, p = ck.abi.plan(5120, 5120, 8192, workspace_bytes=1 << 40, plan_override=SK_NEVER)
     assert rc == 0 and p.stream_k == 0
+    # ... also for the product of operands the planner packs on its own
+    # (unaligned extents, K >= 1536; e.g. 2701 x 1533 x 3625)
+    rng = np.random.default_rng(5)
+    packed = 0
+    for M, N, K in [(2701, 1533, 3625)] + [tuple(int(x) for x in rng.integers(1500, 5000, 3))
+                                           for _ in range(150)]:
+        rc, p = ck.abi.plan(M, N, K, workspace_bytes=1 << 40, plan_override=SK_NEVER)
+        assert rc == 0 and p.stream_k == 0, (M, N, K)
+        packed += p.packed
+    assert packed > 10
     # the per-workgroup introspection refuses plans it does not describe
     args = ck.abi.make_args(4096, 4096, 4096, structure=1)
     w = ck.abi.WorkItem()

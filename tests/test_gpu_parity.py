@@ -406,19 +406,22 @@ def test_direct_staging_split_k(ck, orc, dev, cfg, op_a, op_b):
 
 @pytest.mark.parametrize("op_a,op_b", LAYOUTS)
 @pytest.mark.parametrize("K,cfg", [(32, 6), (64, 7), (30, 6), (24, 6), (5, 6), (40, 7), (64, 8), (40, 8),
-                                   (16, 8)])
+                                   (16, 8), (64, 12), (40, 12), (33, 12)])
 def test_panel_fast_path(ck, orc, dev, op_a, op_b, K, cfg):
-    """The A-panel kernel's fast path (interior tiles, runs of >= 2 column
-    tiles: 4096 x 4096 gives 16 (32) row panels x 16 (8) runs of 2 (4)):
-    stores of one tile overlap the next tile's MFMAs; the 32-deep and the
-    128-row panels stage each 32 x 32 block through LDS to store whole rows.
-    With and without the row bias (N/N)."""
+    """The panel kernel's fast path (interior tiles, runs of >= 2 streamed
+    tiles: 4096 x 4096 gives 16 (32) row panels x 16 (8) runs of 2 (4); the
+    B-resident panel 16 column panels x 16 runs of 2 row tiles): stores of
+    one tile overlap the next tile's MFMAs; the 32-deep and the 128-row
+    panels stage each 32 x 32 block through LDS to store whole rows.  With
+    and without the row bias (N/N; the B-resident panel takes none)."""
     M = N = 4096
+    rc, p = ck.abi.plan(M, N, K, op_a=op_a, op_b=op_b, plan_override=cfg)
+    assert rc == 0 and p.plan_id == cfg
     a_st, b_st = _host_operands(orc, M, N, K, op_a, op_b, 151)
     bias = orc.uniform((M,), 153)
     A, B, Bi = to_dev(a_st), to_dev(b_st), to_dev(bias)
     ref = orc.gemm(_logical(a_st, op_a), _logical(b_st, op_b))
-    for with_bias in ((False, True) if (op_a, op_b) == (0, 0) else (False,)):
+    for with_bias in ((False, True) if (op_a, op_b) == (0, 0) and cfg != 12 else (False,)):
         C = torch.full((M, N), float("nan"), device="cuda")
         args = gemm_args(ck, A, B, C, M, N, K, op_a, op_b, override=cfg)
         if with_bias:
@@ -698,7 +701,7 @@ def test_symmetric_structure(ck, orc, dev):
     ck.abi.check(run_gemm(ck, gemm_args(ck, A, B, C, n, n, n, structure=3)))
     assert_close(orc, to_host(C), orc.gemm(a, b), n, what="MI_SYMMETRIC")
     C2 = torch.empty((n, n), device="cuda")
-    ck.abi.check(ck.abi.lib().mi_symmetric_matmul_f32(vp(A), vp(B), vp(C2), n, cur_stream()))
+    ck.abi.check(ck.abi.lib().mi_symmetric_matmul_f32(vp(A), vp(B), vp(C2), n, None, 0, cur_stream()))
     np.testing.assert_array_equal(to_host(C), to_host(C2))
 
 
@@ -712,7 +715,7 @@ def test_symmetric_operator_on_non_symmetric_inputs(ck, orc, dev, n):
     A, B = to_dev(a), to_dev(b)
     ref = orc.gemm(a, b)
     C = torch.empty((n, n), device="cuda")
-    ck.abi.check(ck.abi.lib().mi_symmetric_matmul_f32(vp(A), vp(B), vp(C), n, cur_stream()))
+    ck.abi.check(ck.abi.lib().mi_symmetric_matmul_f32(vp(A), vp(B), vp(C), n, None, 0, cur_stream()))
     got = to_host(C)
     assert_close(orc, got, ref, n, what="mi_symmetric_matmul_f32, non-symmetric")
     wrong = orc.gemm(a, b.T)
@@ -743,42 +746,46 @@ def test_named_entry_points(ck, orc, dev):
         ck.abi.check(fn(*args, s), fn.__name__)
 
     C = torch.empty((M, N), device="cuda")
-    run(L.mi_matmul_f32, vp(A), vp(B), vp(C), M, K, N)
+    run(L.mi_matmul_f32, vp(A), vp(B), vp(C), M, K, N, None, 0)
     assert_close(orc, to_host(C), orc.gemm(a, b), K, what="mi_matmul_f32")
+    nws = L.mi_matmul_workspace_bytes(M, K, N)
+    wsm = torch.empty(max(nws, 1), dtype=torch.uint8, device="cuda")
+    run(L.mi_matmul_f32, vp(A), vp(B), vp(C), M, K, N, vp(wsm), nws)
+    assert_close(orc, to_host(C), orc.gemm(a, b), K, what="mi_matmul_f32 with workspace")
     run(L.mi_gemm_small_k_f32, vp(A), vp(B), vp(C), M, K, N)
     assert_close(orc, to_host(C), orc.gemm(a, b), K, what="mi_gemm_small_k_f32")
 
     sq = orc.uniform((N, N), 103)
     S = to_dev(sq)
     C2 = torch.empty((N, N), device="cuda")
-    run(L.mi_square_matmul_f32, vp(S), vp(S), vp(C2), N)
+    run(L.mi_square_matmul_f32, vp(S), vp(S), vp(C2), N, None, 0)
     assert_close(orc, to_host(C2), orc.gemm(sq, sq), N, what="square")
 
     at = orc.uniform((K, M), 104)  # A stored K x M
     bt = orc.uniform((N, K), 105)  # B stored N x K
     At, Bt = to_dev(at), to_dev(bt)
-    run(L.mi_matmul_transposed_a_f32, vp(At), vp(B), vp(C), M, K, N)
+    run(L.mi_matmul_transposed_a_f32, vp(At), vp(B), vp(C), M, K, N, None, 0)
     assert_close(orc, to_host(C), orc.gemm(at.T, b), K, what="transposed_a")
-    run(L.mi_matmul_transposed_b_f32, vp(A), vp(Bt), vp(C), M, K, N)
+    run(L.mi_matmul_transposed_b_f32, vp(A), vp(Bt), vp(C), M, K, N, None, 0)
     assert_close(orc, to_host(C), orc.gemm(a, bt.T), K, what="transposed_b")
-    run(L.mi_matmul_transposed_both_f32, vp(At), vp(Bt), vp(C), M, K, N)
+    run(L.mi_matmul_transposed_both_f32, vp(At), vp(Bt), vp(C), M, K, N, None, 0)
     assert_close(orc, to_host(C), orc.gemm(at.T, bt.T), K, what="transposed_both")
 
     bb, m3, k3, n3 = 3, 40, 56, 72
     a3, b3 = orc.uniform((bb, m3, k3), 106), orc.uniform((bb, k3, n3), 107)
     C3 = torch.empty((bb, m3, n3), device="cuda")
-    run(L.mi_batched_matmul_f32, d((a3)), d((b3)), vp(C3), bb, m3, k3, n3)
+    run(L.mi_batched_matmul_f32, d((a3)), d((b3)), vp(C3), bb, m3, k3, n3, None, 0)
     assert_close(orc, to_host(C3), orc.gemm(a3, b3), k3, what="batched")
 
     t3 = orc.uniform((4, 33, k3), 108)
     w = orc.uniform((k3, n3), 109)
     O3 = torch.empty((4, 33, n3), device="cuda")
-    run(L.mi_tensor3d_matmul_f32, d((t3)), d((w)), vp(O3), 4, 33, k3, n3)
+    run(L.mi_tensor3d_matmul_f32, d((t3)), d((w)), vp(O3), 4, 33, k3, n3, None, 0)
     assert_close(orc, to_host(O3).reshape(-1, n3), orc.gemm(t3.reshape(-1, k3), w), k3, what="3d")
 
     t4 = orc.uniform((2, 3, 5, k3), 110)
     O4 = torch.empty((2, 3, 5, n3), device="cuda")
-    run(L.mi_tensor4d_matmul_f32, d((t4)), d((w)), vp(O4), 2, 3, 5, k3, n3)
+    run(L.mi_tensor4d_matmul_f32, d((t4)), d((w)), vp(O4), 2, 3, 5, k3, n3, None, 0)
     assert_close(orc, to_host(O4).reshape(-1, n3), orc.gemm(t4.reshape(-1, k3), w), k3, what="4d")
 
     ta = orc.uniform((300, 24), 111)
@@ -789,7 +796,7 @@ def test_named_entry_points(ck, orc, dev):
 
     r1, r2 = orc.uniform((N, N), 113), orc.uniform((N, N), 114)
     sa, sb = (r1 + r1.T) / 2, (r2 + r2.T) / 2
-    run(L.mi_symmetric_matmul_f32, d((sa)), d((sb)), vp(C2), N)
+    run(L.mi_symmetric_matmul_f32, d((sa)), d((sb)), vp(C2), N, None, 0)
     assert_close(orc, to_host(C2), orc.gemm(sa, sb), N, what="symmetric")
 
     lo_a, lo_b = np.tril(r1), np.tril(r2)
@@ -814,10 +821,10 @@ def test_zero_sizes(ck, dev):
     C = torch.full((4, 5), 3.0, device="cuda")
     A = torch.ones((4, 0), device="cuda")
     B = torch.ones((0, 5), device="cuda")
-    ck.abi.check(L.mi_matmul_f32(vp(A), vp(B), vp(C), 4, 0, 5, s))
+    ck.abi.check(L.mi_matmul_f32(vp(A), vp(B), vp(C), 4, 0, 5, None, 0, s))
     assert torch.all(C == 0)
     for M, N in [(0, 5), (4, 0)]:
-        assert L.mi_matmul_f32(None, None, None, M, 3, N, s) == 0
+        assert L.mi_matmul_f32(None, None, None, M, 3, N, None, 0, s) == 0
 
 
 @pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5, 6, 7])
@@ -836,9 +843,10 @@ def test_repeatability_bitwise(ck, orc, dev, cfg):
 
 
 @pytest.mark.parametrize("op_a,op_b", LAYOUTS)
-@pytest.mark.parametrize("cfg", [6, 7])
+@pytest.mark.parametrize("cfg", [6, 7, 12])
 def test_panel_kernel_batched_and_many_column_runs(ck, orc, dev, op_a, op_b, cfg):
-    # several batches, several A row panels, ragged last panel and column tile
+    # several batches, several resident panels, ragged last panel and
+    # streamed tile
     batch, M, N, K = 3, 600, 2100, 30 if cfg == 6 else 61
     a_st = orc.uniform((batch,) + ((K, M) if op_a else (M, K)), 131)
     b_st = orc.uniform((batch,) + ((N, K) if op_b else (K, N)), 132)
@@ -849,3 +857,31 @@ def test_panel_kernel_batched_and_many_column_runs(ck, orc, dev, op_a, op_b, cfg
     la = np.swapaxes(a_st, 1, 2) if op_a else a_st
     lb = np.swapaxes(b_st, 1, 2) if op_b else b_st
     assert_close(orc, to_host(C), orc.gemm(la, lb), K, what=f"panel cfg {cfg}")
+
+
+@pytest.mark.parametrize("op_a,op_b", LAYOUTS)
+@pytest.mark.parametrize("M,N,K,batch", [(4096, 4096, 64, 1), (1000, 3000, 50, 1), (2048, 1536, 64, 2),
+                                         (8192, 2048, 37, 1)])
+def test_b_panel_equals_a_panel_bitwise(ck, orc, dev, op_a, op_b, M, N, K, batch):
+    """The B-resident panel (config 12) runs the same MFMA sequence per
+    output element as the A-resident one (config 7): equal bits, fast and
+    ragged paths, batched; and within tolerance of the oracle."""
+    a_st = orc.uniform(((batch,) if batch > 1 else ()) + ((K, M) if op_a else (M, K)), 171)
+    b_st = orc.uniform(((batch,) if batch > 1 else ()) + ((N, K) if op_b else (K, N)), 172)
+    A, B = to_dev(a_st), to_dev(b_st)
+    outs = []
+    for cfg in (7, 12):
+        rc, p = ck.abi.plan(M, N, K, batch=batch, op_a=op_a, op_b=op_b, plan_override=cfg)
+        assert rc == 0 and p.plan_id == cfg
+        C = torch.full(((batch,) if batch > 1 else ()) + (M, N), float("nan"), device="cuda")
+        ck.abi.check(run_gemm(ck, gemm_args(ck, A, B, C, M, N, K, op_a, op_b, batch=batch,
+                                            sa=M * K if batch > 1 else 0, sb=K * N if batch > 1 else 0,
+                                            sc=M * N if batch > 1 else 0, override=cfg)))
+        outs.append(to_host(C))
+    np.testing.assert_array_equal(outs[1], outs[0])
+    if batch > 1:
+        la = np.swapaxes(a_st, 1, 2) if op_a else a_st
+        lb = np.swapaxes(b_st, 1, 2) if op_b else b_st
+    else:
+        la, lb = _logical(a_st, op_a), _logical(b_st, op_b)
+    assert_close(orc, outs[1], orc.gemm(la, lb), K, what=f"B panel {op_a}{op_b} {M}x{N}x{K}")

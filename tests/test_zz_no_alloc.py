@@ -52,7 +52,43 @@ def test_noalloc_matches_workspace_entry_point(ck, orc, dev, first, second):
         assert rc == 0 and p.stream_k == 1 and used[0]
 
 
-def test_noalloc_rejects_problems_beyond_its_scratch(ck, dev):
+def _limited(ck, orc, M, N, K, op_a, op_b, seed):
+    """A problem whose preferred plan wants more scratch than the array: the
+    no-alloc call runs the plan mi_gemm_f32 picks with a workspace of exactly
+    the array's size (same bits), within tolerance of the oracle."""
+    L = ck.abi.lib()
+    lim = ck.abi.NOALLOC_SCRATCH_BYTES
+    rc, pref = ck.abi.plan(M, N, K, op_a=op_a, op_b=op_b, workspace_bytes=1 << 40)
+    assert rc == 0 and pref.workspace_bytes > lim
+    rc, fit = ck.abi.plan(M, N, K, op_a=op_a, op_b=op_b, workspace_bytes=lim)
+    assert rc == 0 and fit.workspace_bytes <= lim
+    a = orc.uniform((M, K) if op_a == 0 else (K, M), seed)
+    b = orc.uniform((K, N) if op_b == 0 else (N, K), seed + 1)
+    A, B = to_dev(a), to_dev(b)
+    ws = torch.empty(lim, dtype=torch.uint8, device="cuda")
+    C_ref = torch.empty((M, N), device="cuda")
+    ck.abi.check(run_gemm(ck, gemm_args(ck, A, B, C_ref, M, N, K, op_a=op_a, op_b=op_b, ws=ws)),
+                 "mi_gemm_f32 with a scratch-sized workspace")
+    C_na = torch.full((M, N), float("nan"), device="cuda")
+    args_na = gemm_args(ck, A, B, C_na, M, N, K, op_a=op_a, op_b=op_b)
+    ck.abi.check(L.mi_gemm_f32_noalloc(ctypes.byref(args_na), cur_stream()), "mi_gemm_f32_noalloc")
+    got = to_host(C_na)
+    np.testing.assert_array_equal(got, to_host(C_ref))
+    la = a if op_a == 0 else a.T
+    lb = b if op_b == 0 else b.T
+    assert_close(orc, got, orc.gemm(la, lb), K, what=f"noalloc limited {M}x{N}x{K}")
+
+
+def test_noalloc_plans_within_its_scratch(ck, orc, dev):
+    """Preferred plans past the 64 MiB array (1280 x 1024 x 8192: split 16 of
+    5 MiB partials, 80 MiB) take the best plan that fits it instead of being
+    refused; then a smaller split-K problem in the same array."""
+    _limited(ck, orc, 1280, 1024, 8192, 0, 0, 1400)
+    _limited(ck, orc, 1280, 512, 65536, 1, 0, 1410)
+    _pair(ck, orc, 128, 192, 1 << 16, 0, 0, seed=1420)
+
+
+def test_noalloc_rejects_forced_plans_beyond_its_scratch(ck, dev):
     L = ck.abi.lib()
     M = N = 2048                       # split 8 of 16 MiB partials: 128 MiB
     K = 1 << 20
