@@ -201,8 +201,16 @@ SkChoice plan_stream_k(const mi_gemm_args& a, int cfg, int num_cus) {
     const int64_t T = cdiv(a.M, ci.bm) * cdiv(a.N, ci.bn);
     const int64_t G = (int64_t)num_cus * resident_wgs(cfg);
     if (G % 8 != 0 || T % G == 0) return sk;
+    // Every whole wave of tiles runs data-parallel and only the remainder is
+    // dealt out in K-slices.  The data-parallel tiles of one XCD, neighbours
+    // in the raster, run in step and share their A rows and B columns in L2;
+    // stream-K segments start at different K offsets and share nothing.
+    // Measured against keeping the last whole wave in the stream-K part
+    // (one process, 11 shapes with 1-6 waves): equal or faster on all, by
+    // 0.2-1.7 % (4608^3 1.360 vs 1.375 ms in every layout, fetching 1.09 vs
+    // 3.06 GB from beyond L2; 10240^2 x 2048 2.94 vs 2.99 ms).
     const int64_t waves = T / G;
-    const int64_t dp = waves >= 1 ? (waves - 1) * G : 0;
+    const int64_t dp = waves * G;
     const int64_t S = T - dp;
     const int64_t ipt = cdiv(a.K, ci.bk);
     if (S * ipt < 2 * G || T > INT32_MAX) return sk;

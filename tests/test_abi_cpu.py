@@ -510,7 +510,7 @@ def test_stream_k_schedule_covers_every_tile_once(ck, M, N, K, cfg, ops):
     p, segs = _sk_cover(ck, args)
     T, G = p.num_tiles, p.grid
     waves = T // G
-    assert p.sk_tiles == (T - (waves - 1) * G if waves >= 1 else T)
+    assert p.sk_tiles == T - waves * G  # whole waves data-parallel, the rest stream-K
     # balance: every workgroup reduces the same number of K-slices, +-1 (a
     # partial last slice counts as one)
     per_wg = []
