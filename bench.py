@@ -491,7 +491,8 @@ def pmc_passes():
     """The counter sets of the per-config profiles, one rocprofv3 run each
     (within the per-block limits: 8 SQ, 4 TCC -- FETCH_SIZE takes 3, WRITE_SIZE 2)."""
     return [["SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_VALU_MFMA_MOPS_F32", "SQ_INSTS_VALU_MFMA_MOPS_F16",
-             "GRBM_GUI_ACTIVE"], ["TCC_HIT_sum", "TCC_MISS_sum", "WRITE_SIZE"], ["FETCH_SIZE"]]
+             "SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE", "GRBM_GUI_ACTIVE"],
+            ["TCC_HIT_sum", "TCC_MISS_sum", "WRITE_SIZE"], ["FETCH_SIZE"]]
 
 
 def summary_header(cfg, timed, warmup, root):
@@ -611,6 +612,11 @@ def summarize(dirs, calib, timed, cfg=None, warmup=None):
                         fl = last[c] * 512
                         line.append(f"{what} MFMA flops {fl:.4g} ({c} x 512) = "
                                     f"{fl / (sum(ns) / len(ns)) / 1e3:.1f} TFLOP/s over the profiled dispatch")
+            if "SQ_LDS_IDX_ACTIVE" in last and "SQ_LDS_BANK_CONFLICT" in last:
+                bc, act = last["SQ_LDS_BANK_CONFLICT"], last["SQ_LDS_IDX_ACTIVE"]
+                line.append(f"LDS bank conflicts {bc:.4g} cycles = {bc / max(act, 1):.4f} of the "
+                            f"{act:.4g} indexed-LDS cycles (SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE; "
+                            f"direct buffer-to-LDS loads are not indexed operations)")
             if "TCC_HIT_sum" in last and "TCC_MISS_sum" in last:
                 h, m = last["TCC_HIT_sum"], last["TCC_MISS_sum"]
                 line.append(f"L2 hit {100 * h / max(h + m, 1):.1f} % ({h:.4g} hits, {m:.4g} misses)")
@@ -625,7 +631,7 @@ def summarize(dirs, calib, timed, cfg=None, warmup=None):
             for c in cnames:
                 if c not in ("GRBM_GUI_ACTIVE", "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_VALU_MFMA_MOPS_F32",
                              "SQ_INSTS_VALU_MFMA_MOPS_F16", "TCC_HIT_sum", "TCC_MISS_sum", "FETCH_SIZE",
-                             "WRITE_SIZE"):
+                             "WRITE_SIZE", "SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE"):
                     line.append(f"{c} {last[c]:.6g}")
             for x in line:
                 out.append(f"    {x}")

@@ -217,3 +217,57 @@ def test_cfg4_symmetric(ck, orc):
     a, b = to_host(A), to_host(B)
     assert_close(orc, to_host(C[rows]), orc.gemm(a, b, rows=rows), n, what="symmetric")
     _whole(orc, C, a, b, n, 800, "symmetric every element")
+
+
+def test_sdpa_bench_shape_every_chunk(ck, orc, dev):
+    """PID 97 at the bench shape (32, 32, 512, 1024): 1,024 heads, i.e. eight
+    chunks of 128 heads through the workspace.  One head of every chunk (at a
+    different position in each) is checked against the fp64 oracle to the
+    attention bound (one binary16 spacing + 2^-17 max|V|); every head is
+    checked for the convexity of softmax weights: each output lies within the
+    [min, max] of its V column (plus one fp16 spacing), with no NaN."""
+    shape = (32, 32, 512, 1024)
+    Q, K, V = (dev_uniform(ck, shape, 970 + i).half() for i in range(3))
+    O = ck.p97.fused_attention_cuda(Q, K, V)
+    torch.cuda.synchronize()
+    assert not torch.isnan(O).any()
+    Of, Vf = O.float().view(1024, 512, 1024), V.float().view(1024, 512, 1024)
+    lo, hi = Vf.amin(dim=1, keepdim=True), Vf.amax(dim=1, keepdim=True)
+    slack = 2.0 ** -10 * torch.maximum(lo.abs(), hi.abs())
+    assert bool(((Of >= lo - slack) & (Of <= hi + slack)).all())
+    qh, kh, vh = (t.view(1024, 512, 1024) for t in (Q, K, V))
+    for c in range(8):
+        h = 128 * c + (37 * c + 5) % 128
+        q, k, v = (to_host(t[h]) for t in (qh, kh, vh))
+        ref = orc.sdpa(q, k, v)
+        err = np.abs(to_host(Of[h]).astype(np.float64) - ref)
+        bound = orc.half_ulp(ref) + 2.0 ** -17 * float(np.max(np.abs(v.astype(np.float64))))
+        assert float(np.max(err / bound)) <= 1.0, f"head {h}: error {float(np.max(err / bound)):.2f} x bound"
+
+
+def test_pointwise_conv_bench_shape(ck, orc, dev):
+    """PID 87 at the bench shape (16, 64, 128, 256, 256) with bias: the
+    128-row A-resident panel over 16 images of 65,536 pixels.  Every output
+    element enters per-image fp64 row and column checksums (the conv is
+    out[n] = W . X[n] + bias, tests/freivalds.py), and sampled pixels of every
+    image are compared with the fp64 oracle element by element."""
+    n, cin, cout, hw = 16, 64, 128, 256 * 256
+    X = dev_uniform(ck, (n, cin, 256, 256), 980)
+    W = dev_uniform(ck, (cout, cin, 1, 1), 981)
+    bias = dev_uniform(ck, (cout,), 982)
+    out = ck.p87.pointwise_conv_cuda(X, W, bias)
+    assert tuple(out.shape) == (n, cout, 256, 256)
+    w = to_host(W).reshape(cout, cin)
+    b64 = to_host(bias).astype(np.float64)
+    cols = np.r_[0:200, 32768 - 100:32768 + 100, hw - 200:hw]
+    for i in range(n):
+        x = to_host(X[i]).reshape(cin, hw)
+        got = to_host(out[i]).reshape(cout, hw)
+        v, u = fv.signs(hw, 990 + i), fv.signs(cout, 1990 + i)
+        ref_cv, ref_utc = fv.reference(orc, w, x, v, u)
+        ref_cv = ref_cv + b64 * v.sum()
+        ref_utc = ref_utc + float(u @ b64)
+        fv.check(orc, got.astype(np.float64) @ v, u @ got.astype(np.float64), ref_cv, ref_utc, cin,
+                 1.0, 1.0, what=f"conv image {i}")
+        ref = orc.gemm(w, np.ascontiguousarray(x[:, cols])) + b64[:, None]
+        assert_close(orc, got[:, cols], ref, cin, what=f"conv image {i} sampled pixels")
