@@ -446,17 +446,34 @@ __global__ void __launch_bounds__(256)
     // zeroed: the main kernel wrote every zero tile but the mirrors and the
     // item counter's tile (zero-triangle tile 0, (0, 1) / (1, 0))
     if (zeroed && !add && blockIdx.x != 0) return;
-    const int64_t row0 = (int64_t)blockIdx.y * 64;
+    // 16 rows of the tile per workgroup, four 16-byte groups per thread, all
+    // of a thread's loads issued before its stores (one memory round trip
+    // per workgroup instead of one per group: the mirror and its tile never
+    // overlap, but the compiler cannot know that and would not reorder them)
+    const int64_t row0 = (int64_t)blockIdx.y * 16;
     float* const z0 = C + ((int64_t)a * 256 + row0) * ldc + (int64_t)b * 256;
     float* const d0 = C + ((int64_t)b * 256 + row0) * ldc + (int64_t)a * 256;
-    for (int e = threadIdx.x; e < 64 * 64; e += 256) {
-        const int r = e >> 6, c = (e & 63) * 4;
-        float* const z = z0 + (int64_t)r * ldc + c;
-        float* const d = d0 + (int64_t)r * ldc + c;
-        if (VEC) {
-            if (add) *reinterpret_cast<f4*>(d) += *reinterpret_cast<const f4*>(z);
-            *reinterpret_cast<f4*>(z) = f4{0.f, 0.f, 0.f, 0.f};
-        } else {
+    if (VEC) {
+        f4 zv[4], dv[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int e = threadIdx.x + 256 * q, r = e >> 6, c = (e & 63) * 4;
+            if (add) {
+                zv[q] = *reinterpret_cast<const f4*>(z0 + (int64_t)r * ldc + c);
+                dv[q] = *reinterpret_cast<const f4*>(d0 + (int64_t)r * ldc + c);
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int e = threadIdx.x + 256 * q, r = e >> 6, c = (e & 63) * 4;
+            if (add) *reinterpret_cast<f4*>(d0 + (int64_t)r * ldc + c) = dv[q] + zv[q];
+            *reinterpret_cast<f4*>(z0 + (int64_t)r * ldc + c) = f4{0.f, 0.f, 0.f, 0.f};
+        }
+    } else {
+        for (int e = threadIdx.x; e < 16 * 64; e += 256) {
+            const int r = e >> 6, c = (e & 63) * 4;
+            float* const z = z0 + (int64_t)r * ldc + c;
+            float* const d = d0 + (int64_t)r * ldc + c;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 if (add) d[q] += z[q];
@@ -470,7 +487,7 @@ hipError_t launch_tri_finish(float* C, int64_t ldc, int nt, int cap, bool lower,
                              hipStream_t s) {
     const int zero_tiles = nt * (nt - 1) / 2;
     if (zero_tiles == 0) return hipSuccess;
-    const dim3 grid((unsigned)zero_tiles, 4);
+    const dim3 grid((unsigned)zero_tiles, 16);
     if (ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(C) & 15u) == 0)
         hipLaunchKernelGGL(tri_finish_kernel<true>, grid, dim3(256), 0, s, C, ldc, nt, cap, (int)lower,
                            (int)zeroed);
