@@ -455,8 +455,9 @@ __global__ void __launch_bounds__(T::NT)
     // fragments of one k-block, kept at kernel scope (two sets, by k-block parity)
     float fa[2][T::TM][4], fb[2][T::TN][4];
     // Triangular modes: the slice lies in one K unit; in the unit of A's row
-    // tile (mask_a) / B's column tile (mask_b) entries past the diagonal read
-    // as zero.  kl0 = the slice's first k within that unit.
+    // tile (mask_a) / B's column tile (mask_b) entries past the diagonal are
+    // set to +0.0 in LDS (zero_masked) before any fragment of the slice is
+    // read.  kl0 = the slice's first k within that unit.
     int mask_a = 0, mask_b = 0, kl0 = 0;
     // the wave's fragments of the slice are all zero (masked): its MFMAs are
     // skipped (they would add exact zeros)
@@ -501,24 +502,50 @@ __global__ void __launch_bounds__(T::NT)
                 }
             }
         }
+    };
+    // Triangular modes, a slice in a masked unit, once its loads have landed
+    // (after the barrier) and before any of its fragments are read: +0.0 over
+    // the entries past the diagonal, so the fragment reads and MFMAs are the
+    // dense kernel's.  (Zeroing the fragments in registers instead put compare
+    // and select code after every k-block's fragment reads, masked unit or
+    // not: full units ran ~5 % slower than the dense kernel's.)  The slice is
+    // N/N: A K-contiguous (row r: 32 floats, 16-byte chunk g at slot
+    // g ^ (r / 2) % 8), B MN-contiguous (k-row k at LDS row 8 (k % 4) + k / 4,
+    // rows of 256 floats + 4 padding).  A(m, k): lower keeps k <= m, upper
+    // k >= m; B(k, n): lower keeps n <= k, upper n >= k.
+    auto zero_masked = [&](float* As, float* Bs) __attribute__((always_inline)) {
         if constexpr (MODE != kDense) {
-            const int klb = kl0 + 8 * kb + 4 * (lane >> 5);  // + s
-            if (mask_a) {  // A(m, k): lower keeps k <= m, upper k >= m
+            static_assert(A_KC && !B_KC && T::BM == 256 && T::BK == 32, "N/N 256 x 32 slices");
+            if (mask_a) {
 #pragma unroll
-                for (int i = 0; i < T::TM; ++i) {
-                    const int ml = wm * T::WM + 32 * i + (lane & 31);
+                for (int q = 0; q < 256 * 8 / T::NT; ++q) {
+                    const int c = tid + q * T::NT;
+                    const int r = c >> 3, g = c & 7;
+                    const int k0 = kl0 + 4 * g;  // unit-local k of the chunk's first entry
+                    float* const ptr = As + r * 32 + ((g ^ ((r >> 1) & 7)) << 2);
+                    if (MODE == kLower ? k0 > r : k0 + 3 < r) {
+                        *reinterpret_cast<f4*>(ptr) = f4{0.f, 0.f, 0.f, 0.f};
+                    } else if (MODE == kLower ? k0 + 3 > r : k0 < r) {
 #pragma unroll
-                    for (int s = 0; s < 4; ++s)
-                        if (MODE == kLower ? klb + s > ml : klb + s < ml) fa[kb & 1][i][s] = 0.f;
+                        for (int e = 0; e < 4; ++e)
+                            if (MODE == kLower ? k0 + e > r : k0 + e < r) ptr[e] = 0.f;
+                    }
                 }
             }
-            if (mask_b) {  // B(k, n): lower keeps n <= k, upper n >= k
+            if (mask_b) {
 #pragma unroll
-                for (int t = 0; t < 2; ++t) {
-                    const int nl = wn * T::WN + 2 * (lane & 31) + t;
+                for (int q = 0; q < 32 * 64 / T::NT; ++q) {
+                    const int c = tid + q * T::NT;
+                    const int kr = c >> 6, n0 = (c & 63) * 4;
+                    const int k = kl0 + kr;  // unit-local k of this k-row
+                    float* const ptr = Bs + (8 * (kr & 3) + (kr >> 2)) * LB::IPITCH + n0;
+                    if (MODE == kLower ? n0 > k : n0 + 3 < k) {
+                        *reinterpret_cast<f4*>(ptr) = f4{0.f, 0.f, 0.f, 0.f};
+                    } else if (MODE == kLower ? n0 + 3 > k : n0 < k) {
 #pragma unroll
-                    for (int s = 0; s < 4; ++s)
-                        if (MODE == kLower ? nl > klb + s : nl < klb + s) fb[kb & 1][t][s] = 0.f;
+                        for (int e = 0; e < 4; ++e)
+                            if (MODE == kLower ? n0 + e > k : n0 + e < k) ptr[e] = 0.f;
+                    }
                 }
             }
         }
@@ -667,6 +694,10 @@ __global__ void __launch_bounds__(T::NT)
     issue(cur, 0, sA0, sB0);
     __syncthreads();
     slice_state(cur, 0);
+    if (MODE != kDense && (mask_a || mask_b)) {
+        zero_masked(sA0, sB0);
+        __syncthreads();
+    }
     frags(sA0, sB0, 0);
 
     // One slice from buffer CB; returns true after the workgroup's last tile.
@@ -725,6 +756,10 @@ __global__ void __launch_bounds__(T::NT)
         const int tail_idle = idle;  // (slice_state below moves on to the next slice)
         if (has_next) {
             slice_state(nw, nit);
+            if (MODE != kDense && (mask_a || mask_b)) {
+                zero_masked(nxtA, nxtB);
+                __syncthreads();
+            }
             frags(nxtA, nxtB, 0);
         }
         __builtin_amdgcn_sched_barrier(0);
