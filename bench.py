@@ -76,7 +76,8 @@ def parse_args():
     p.add_argument("--no-configs", action="store_true", help="skip the per-config table")
     p.add_argument("--override", type=lambda x: int(x, 0), default=0,
                    help="with --mode gemm:MxNxK[:TN|NT|TT]: mi_gemm_args.plan_override (bits 0-3 tile "
-                        "config, 4 take stream-K, 5 no stream-K, 8-19 split count)")
+                        "config, 4 take stream-K, 5 no stream-K, 8-19 split count, 30 stream-K over "
+                        "contiguous ranges instead of phases)")
     p.add_argument("--summarize", nargs="+", metavar="DIR",
                    help="summarise rocprofv3 CSV output under DIR(s) and exit")
     p.add_argument("--calib", metavar="DIR", default=None,
@@ -701,7 +702,8 @@ def main() -> int:
             ck.abi.check(rc, "mi_gemm_plan")
             r = run_config(c, u, stream, reps=args.steps, warmup=args.warmup, exact_warmup=True)
             print(json.dumps({"config": spec, "override": hex(override), "plan": plan.plan_id,
-                              "split_k": plan.split_k, "stream_k": plan.stream_k, **r}), flush=True)
+                              "split_k": plan.split_k, "stream_k": plan.stream_k,
+                              "sk_phases": plan.sk_phases, **r}), flush=True)
         return 0
     if args.mode.startswith("torch:"):
         for spec in args.mode.split(","):

@@ -59,7 +59,7 @@ class Plan(ctypes.Structure):
         ("split_k", ctypes.c_int32), ("k_chunk", _i64), ("group_m", ctypes.c_int32),
         ("num_tiles", _i64), ("grid", _i64), ("workspace_bytes", _sz),
         ("stream_k", ctypes.c_int32), ("sk_tiles", _i64),
-        ("packed", ctypes.c_int32), ("packed_k", _i64),
+        ("packed", ctypes.c_int32), ("packed_k", _i64), ("sk_phases", ctypes.c_int32),
     ]
 
 

@@ -204,8 +204,10 @@ int mi_gemm_work_item(const mi_gemm_args* args, int32_t num_cus, int64_t wg, int
     if (item > INT32_MAX) return 0;
     const CfgInfo ci = cfg_info(g.cfg);
     if (g.sk_tiles > 0) {
-        int lt, s0, s1, to_ws;
-        if (!sk_work((int)wg, (int)item, g.grid_x, g.sk_dp, g.sk_tiles, g.sk_ipt, lt, s0, s1, to_ws))
+        int lt, s0, s1;
+        int64_t slot;
+        if (!sk_item((int)wg, (int)item, g.grid_x, g.sk_dp, g.sk_tiles, g.sk_ipt, g.sk_ph, g.sk_nph,
+                     lt, s0, s1, slot))
             return 0;
         int tm, tn;
         raster(lt, g.tiles_m, g.tiles_n, g.group_m, tm, tn);
@@ -213,8 +215,8 @@ int mi_gemm_work_item(const mi_gemm_args* args, int32_t num_cus, int64_t wg, int
         out->tile_n = tn;
         out->k_begin = (int64_t)s0 * ci.bk;
         out->k_end = std::min<int64_t>((int64_t)s1 * ci.bk, g.K);  // (4-byte staging: last slice partial)
-        out->dest = to_ws;
-        out->slot = to_ws ? xcd_remap((int)wg, g.grid_x) : 0;
+        out->dest = slot >= 0 ? 1 : 0;
+        out->slot = slot >= 0 ? (int32_t)slot : 0;
         return 1;
     }
     const int64_t t = wg + item * g.grid_x;
@@ -253,7 +255,7 @@ int mi_gemm_sk_fixup_of(const mi_gemm_args* args, int32_t num_cus, int64_t t, in
     raster(g.sk_dp + (int)t, g.tiles_m, g.tiles_n, g.group_m, tm, tn);
     *tile_m = tm;
     *tile_n = tn;
-    sk_fixup_slots(t, g.sk_tiles, g.sk_ipt, g.grid_x, *first_slot, *n_slots);
+    sk_tile_slots(t, g.sk_tiles, g.sk_ipt, g.grid_x, g.sk_ph, g.sk_nph, *first_slot, *n_slots);
     return 1;
 }
 

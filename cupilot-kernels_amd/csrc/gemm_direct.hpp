@@ -344,10 +344,10 @@ __device__ __forceinline__ void store_tile_direct(const GemmParams& p, float* C,
 // the wrong side of the diagonal are zeroed in the fragments of the diagonal
 // K unit (tril(A) tril(B) / triu(A) triu(B) for any input).
 //
-// SK: the stream-K schedule (sk_work): workgroup b runs its items 0, 1, ...
-// -- whole tiles, then the segments of its K-slice range -- and stores a
-// segment that does not start at k = 0 into its workspace slot
-// (xcd_remap(b, grid)), tile-local, for sk_fixup to add in.  With 4-byte
+// SK: the stream-K schedule (sk_item): workgroup b runs its items 0, 1, ...
+// -- whole tiles, then its stream-K segments -- and stores a segment that
+// does not start at k = 0 into that segment's workspace slot, tile-local,
+// for sk_fixup to add in.  With 4-byte
 // staging (128 tile) a tile's last slice may be partial: the segment that
 // holds it ends at K.
 template <class T, bool AT, bool BT, bool BIAS, int MODE = kDense, int VB = 16, bool SK = false>
@@ -425,18 +425,23 @@ __global__ void __launch_bounds__(T::NT)
         if constexpr (SK) {
             // compute = 0: past the workgroup's last item
             TileWork w;
-            int lt, s0, s1, to_ws;
-            w.compute = sk_work(blockIdx.x, item, gridDim.x, p.sk_dp, p.sk_tiles, p.sk_ipt, lt,
-                                s0, s1, to_ws)
+            int lt, s0, s1;
+            int64_t slot;
+            w.compute = sk_item(blockIdx.x, item, gridDim.x, p.sk_dp, p.sk_tiles, p.sk_ipt,
+                                p.sk_ph, p.sk_nph, lt, s0, s1, slot)
                             ? 1
                             : 0;
-            if (!w.compute) lt = s0 = s1 = to_ws = 0;
+            if (!w.compute) {
+                lt = s0 = s1 = 0;
+                slot = -1;
+            }
             raster(lt, p.tiles_m, p.tiles_n, p.group_m, w.tm, w.tn);
             w.k_begin = s0 * T::BK;
             // (4-byte staging: the tile's last slice may end past K)
             w.k_end = s1 * T::BK < p.K ? s1 * T::BK : p.K;
             w.nk = s1 - s0;
-            w.mirror = to_ws;
+            w.mirror = slot >= 0;
+            w.slot = slot >= 0 ? (int)slot : 0;
             return w;
         } else if constexpr (MODE == kDense) {
             return decode_tile<T, kDense>(p, item);
@@ -686,9 +691,6 @@ __global__ void __launch_bounds__(T::NT)
     if (!SK && t >= p.num_tiles) return;
     TileWork cur = decode(t);
     if (SK && !cur.compute) return;
-    // stream-K: this workgroup's workspace slot (tile-local, BM x BN)
-    float* const sk_slot =
-        SK ? p.ws + (int64_t)xcd_remap(blockIdx.x, gridDim.x) * (T::BM * T::BN) : nullptr;
     int it = 0;
     set_offsets(cur);
     issue(cur, 0, sA0, sB0);
@@ -770,9 +772,9 @@ __global__ void __launch_bounds__(T::NT)
             ++it;
             return false;
         }
-        if (SK && cur.mirror)
-            store_tile_direct<T, !A_KC, !B_KC, BIAS, MODE, true>(p, sk_slot, T::BN, true, cur, acc,
-                                                                 wm, wn, lane);
+        if (SK && cur.mirror)  // stream-K: the segment's workspace slot (tile-local, BM x BN)
+            store_tile_direct<T, !A_KC, !B_KC, BIAS, MODE, true>(
+                p, p.ws + (int64_t)cur.slot * (T::BM * T::BN), T::BN, true, cur, acc, wm, wn, lane);
         else
             store_tile_direct<T, !A_KC, !B_KC, BIAS, MODE>(p, C, ldc, c_vec, cur, acc, wm, wn, lane);
 #pragma unroll

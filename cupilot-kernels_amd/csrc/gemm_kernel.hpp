@@ -201,7 +201,9 @@ struct TileWork {
     // 0 or 1 (ints, so that the struct has no padding bytes: copies of a
     // padded struct keep the padding in memory -- here, in LDS)
     int compute;
-    int mirror;  // chunked triangular list: partial sum goes to tile (tn, tm)
+    int mirror;  // chunked triangular list: partial sum goes to tile (tn, tm);
+                 // stream-K: the segment goes to workspace slot `slot`
+    int slot;
 };
 
 template <class T, int MODE>
@@ -211,6 +213,7 @@ __device__ __forceinline__ TileWork decode_tile(const GemmParams& p, int tile) {
                                             w.k_begin, w.k_end);
     w.nk = w.compute && w.k_end > w.k_begin ? (w.k_end - w.k_begin + T::BK - 1) / T::BK : 0;
     w.mirror = 0;
+    w.slot = 0;
     return w;
 }
 
@@ -436,6 +439,8 @@ inline GemmParams make_params(const GemmLaunch& g) {
     p.sk_dp = g.sk_dp;
     p.sk_tiles = g.sk_tiles;
     p.sk_ipt = g.sk_ipt;
+    p.sk_nph = g.sk_nph;
+    for (int q = 0; q < kSkMaxPhases; ++q) p.sk_ph[q] = g.sk_ph[q];
     p.ws_batch_stride = (int64_t)g.M * g.N;
     p.ws_split_stride = p.ws_batch_stride * g.batch;
     return p;

@@ -37,10 +37,10 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// SK: the stream-K schedule (sk_work): workgroup b runs its items 0, 1, ...
-// -- whole tiles, then the segments of its K-slice range -- and stores a
-// segment that does not start at k = 0 into its workspace slot
-// (xcd_remap(b, grid), 64 x 64, tile-local) for sk_fixup to add in.
+// SK: the stream-K schedule (sk_item): workgroup b runs its items 0, 1, ...
+// -- whole tiles, then its stream-K segments -- and stores a segment that
+// does not start at k = 0 into that segment's workspace slot (64 x 64,
+// tile-local) for sk_fixup to add in.
 template <bool AT, bool BT, bool BIAS, bool SK = false>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
     gemm_f32_ksplit_kernel(const GemmParams p) {
@@ -90,18 +90,22 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     };
 
     uint32_t voA[LA::PER_WAVE], voB[LB::PER_WAVE];
-    // stream-K: this workgroup's workspace slot
-    float* const sk_slot = SK ? p.ws + (int64_t)xcd_remap(blockIdx.x, gridDim.x) * (BM * BM) : nullptr;
+    // stream-K: the current segment's workspace slot
+    float* sk_slot = nullptr;
     for (int t = SK ? 0 : blockIdx.x;; t += SK ? 1 : gridDim.x) {
         int tm, tn, k_begin, k_end;
         bool to_slot = false;
         if constexpr (SK) {
-            int lt, s0, s1, to_ws;
-            if (!sk_work(blockIdx.x, t, gridDim.x, p.sk_dp, p.sk_tiles, p.sk_ipt, lt, s0, s1, to_ws)) break;
+            int lt, s0, s1;
+            int64_t slot;
+            if (!sk_item(blockIdx.x, t, gridDim.x, p.sk_dp, p.sk_tiles, p.sk_ipt, p.sk_ph, p.sk_nph,
+                         lt, s0, s1, slot))
+                break;
             raster(lt, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
             k_begin = s0 * BK;
             k_end = s1 * BK;
-            to_slot = to_ws != 0;
+            to_slot = slot >= 0;
+            if (to_slot) sk_slot = p.ws + slot * (BM * BM);
         } else {
             if (t >= p.num_tiles) break;
             tile_of<BM, BM, kDense>(p, t, p.num_tiles, blockIdx.y, tm, tn, k_begin, k_end);

@@ -226,6 +226,186 @@ __host__ __device__ __forceinline__ void sk_fixup_slots(int64_t t, int64_t S, in
     count = last - head;
 }
 
+// Phased stream-K.  With the contiguous ranges above every workgroup starts
+// at its own K offset, so the workgroups that run together on one XCD read
+// unrelated slices and share nothing in L2 (3072^2 x 8192 on the 256 tile:
+// 11 % L2 hits, 10x the compulsory bytes fetched).  The phased schedule deals
+// the same S x ipt slices out so that, at any moment, the workgroups of one
+// XCD read the same K-slice of neighbouring tiles.  Each logical workgroup
+// has a budget of B slice-times, and a segment costs its slices plus kSkSegCost
+// (the store of its partial tile and the restart of the pipeline).  Charging
+// nothing for segments gave some workgroups a third one and ran 0.2-1 %
+// slower than the ranges; 1 slice, 0.3 % slower on 4608^3 and 1 % on 3584^3
+// (11 phases); 2 slices with at most 8 phases, against the ranges in one
+// process (10 shapes, medians of 3): 0.978-0.999 of their time on 7
+// (1536^2 x 4096 0.978, 3328^2 x 4096 0.983, 3072^2 x 8192 0.994-0.996),
+// 1.000-1.001 on 4352^3 and 4608^3, 1.005 on 3584^3.  A
+// phase serves n tiles t0 .. t0 + n - 1 with the n logical workgroups
+// w0 .. w0 + n - 1 (workgroup w0 + i takes tile t0 + i), every one of them
+// reducing the same K range [k0, k1) and starting it at the same moment:
+//   * n_t tiles left (each needing [k_lo, ipt), r = ipt - k_lo slices),
+//     n_w workgroups left (each with budget c left);
+//   * n_t <= n_w: the first n_t workgroups reduce [k_lo, k_lo + min(c - cost,
+//     r)) of every tile and are used up; if that was all of r, the schedule
+//     is complete;
+//   * n_t > n_w: every workgroup reduces the whole rest [k_lo, ipt) of one
+//     tile and keeps c - r - cost for the next phase.
+// All workgroups in a phase have run the same earlier phases, so their
+// segments start together; consecutive logical workgroups (one XCD's, via
+// xcd_remap) take consecutive tiles of the raster, which share A row and B
+// column panels.  A segment that starts at k = 0 is written to C; every
+// other segment to its own workspace slot, slots numbered tile by tile in k
+// order, so the fixup adds a tile's slots [first, first + count) in order --
+// deterministic.  The planner takes the smallest budget the phases can meet
+// within kSkMaxPhases entries and kSkMaxSegments segments per workgroup, and
+// uses the phases only where that budget is no more than the busiest
+// workgroup's cost under the contiguous ranges (sk_ranges_cost); otherwise
+// the ranges (nph = 0).  Example, 3072^2 x 8192 on the 256 tile (S = 144
+// tiles of ipt = 256 slices, G = 256): tiles 0..143 reduce [0, 145) on
+// workgroups 0..143; tiles 0..111 [145, 256) on 144..255; tiles 112..143
+// [145, 177), [177, 209), [209, 241) on 144..175, 176..207, 208..239; then
+// [241, 256) on 240..255 for tiles 112..127 and again for 128..143.
+constexpr int kSkMaxPhases = 8;
+constexpr int kSkMaxSegments = 3;
+constexpr int kSkSegCost = 2;
+struct SkPhase {
+    int t0, n, k0, k1, w0;
+};
+
+// Host: the phase table of S tiles x ipt slices over G workgroups with a
+// budget of B slice-times each.  Returns the most segments any workgroup
+// gets, or -1 where the budget is too small or the table would not fit
+// kSkMaxPhases; slots = the segments that do not start at k = 0.
+inline int sk_build_phases(int64_t S, int64_t ipt, int64_t G, int64_t B, SkPhase* ph, int& nph,
+                           int64_t& slots) {
+    nph = 0;
+    slots = 0;
+    if (S <= 0 || ipt <= 0 || G <= 0 || S > G) return -1;
+    int64_t c = B;
+    int64_t t_lo = 0, k_lo = 0, w_lo = 0;
+    int t2 = 0, most = 0;  // whole-rest phases so far; most segments of a used-up workgroup
+    for (;;) {
+        const int64_t n_t = S - t_lo, r = ipt - k_lo, n_w = G - w_lo;
+        if (n_t == 0) break;
+        if (nph == kSkMaxPhases || n_w <= 0) return -1;
+        if (n_t <= n_w) {
+            const int64_t len = c - kSkSegCost < r ? c - kSkSegCost : r;
+            if (len <= 0) return -1;
+            ph[nph++] = SkPhase{(int)t_lo, (int)n_t, (int)k_lo, (int)(k_lo + len), (int)w_lo};
+            if (k_lo > 0) slots += n_t;
+            most = most > t2 + 1 ? most : t2 + 1;
+            if (len == r) break;
+            k_lo += len;
+            w_lo += n_t;
+        } else {
+            if (r + kSkSegCost > c) return -1;
+            ph[nph++] = SkPhase{(int)t_lo, (int)n_w, (int)k_lo, (int)ipt, (int)w_lo};
+            if (k_lo > 0) slots += n_w;
+            ++t2;
+            t_lo += n_w;
+            c -= r + kSkSegCost;
+        }
+    }
+    return most > t2 ? most : t2;
+}
+
+// Host: the busiest workgroup's cost (slices + kSkSegCost per segment) under
+// the contiguous ranges.
+inline int64_t sk_ranges_cost(int64_t S, int64_t ipt, int64_t G) {
+    const int64_t iters = S * ipt;
+    int64_t most = 0;
+    for (int64_t lg = 0; lg < G; ++lg) {
+        const int64_t b = lg * iters / G, e = (lg + 1) * iters / G;
+        if (e == b) continue;
+        const int64_t segs = (e - 1) / ipt - b / ipt + 1;
+        const int64_t cost = e - b + kSkSegCost * segs;
+        most = cost > most ? cost : most;
+    }
+    return most;
+}
+
+// Slot numbering of the phased schedule: the slots of tile t start after
+// those of tiles 0 .. t - 1; nph entries of ph.
+__host__ __device__ __forceinline__ int64_t sk_ph_first_slot(int64_t t, const SkPhase* ph, int nph) {
+    int64_t first = 0;
+    for (int q = 0; q < nph; ++q) {
+        if (ph[q].k0 == 0) continue;
+        const int64_t d = t - ph[q].t0;
+        first += d <= 0 ? 0 : d < ph[q].n ? d : ph[q].n;
+    }
+    return first;
+}
+
+// Phased schedule, the item-th segment (in run order) of logical workgroup
+// lg: tile t (0-based among the stream-K tiles), slice range [s0, s1), and
+// its slot (-1: the segment starts at k = 0 and goes to C).
+__host__ __device__ __forceinline__ bool sk_ph_work(int lg, int item, const SkPhase* ph, int nph,
+                                                    int64_t& t, int& s0, int& s1, int64_t& slot) {
+    int seen = 0;
+    for (int q = 0; q < nph; ++q) {
+        if (lg < ph[q].w0 || lg >= ph[q].w0 + ph[q].n) continue;
+        if (seen++ != item) continue;
+        t = ph[q].t0 + (lg - ph[q].w0);
+        s0 = ph[q].k0;
+        s1 = ph[q].k1;
+        if (s0 == 0) {
+            slot = -1;
+            return true;
+        }
+        int64_t before = 0;  // earlier phases that parked a part of tile t
+        for (int e = 0; e < q; ++e)
+            if (ph[e].k0 > 0 && t >= ph[e].t0 && t < ph[e].t0 + ph[e].n) ++before;
+        slot = sk_ph_first_slot(t, ph, nph) + before;
+        return true;
+    }
+    return false;
+}
+
+// Phased schedule: the slots of stream-K tile t, [first, first + count).
+__host__ __device__ __forceinline__ void sk_ph_fixup_slots(int64_t t, const SkPhase* ph, int nph,
+                                                           int64_t& first, int64_t& count) {
+    first = sk_ph_first_slot(t, ph, nph);
+    count = 0;
+    for (int q = 0; q < nph; ++q)
+        if (ph[q].k0 > 0 && t >= ph[q].t0 && t < ph[q].t0 + ph[q].n) ++count;
+}
+
+// Either schedule (nph = 0: contiguous ranges, else the phase table): work
+// item `item` of hardware workgroup b -- its n_dp / G data-parallel tiles,
+// then its stream-K segments.  lt = the tile's raster position, [s0, s1) its
+// slices, slot = the workspace slot of a segment that does not start at
+// k = 0, else -1 (written to C).
+__host__ __device__ __forceinline__ bool sk_item(int b, int item, int G, int n_dp, int64_t S,
+                                                 int ipt, const SkPhase* ph, int nph, int& lt,
+                                                 int& s0, int& s1, int64_t& slot) {
+    if (nph == 0 || item < n_dp / G) {
+        int to_ws;
+        if (!sk_work(b, item, G, n_dp, S, ipt, lt, s0, s1, to_ws)) return false;
+        slot = to_ws ? xcd_remap(b, G) : -1;
+        return true;
+    }
+    int64_t t;
+    if (!sk_ph_work(xcd_remap(b, G), item - n_dp / G, ph, nph, t, s0, s1, slot)) return false;
+    lt = n_dp + (int)t;
+    return true;
+}
+
+// Either schedule: the slots the fixup adds into stream-K tile t, in order.
+// Contiguous ranges leave a slot empty where its workgroup got no slices
+// (sk_slot_used); the phase table never does.
+__host__ __device__ __forceinline__ void sk_tile_slots(int64_t t, int64_t S, int ipt, int G,
+                                                       const SkPhase* ph, int nph, int64_t& first,
+                                                       int64_t& count) {
+    if (nph == 0)
+        sk_fixup_slots(t, S, ipt, G, first, count);
+    else
+        sk_ph_fixup_slots(t, ph, nph, first, count);
+}
+__host__ __device__ __forceinline__ bool sk_slot_used(int64_t slot, int64_t S, int ipt, int G, int nph) {
+    const int64_t iters = S * ipt;
+    return nph > 0 || sk_begin(slot + 1, iters, G) != sk_begin(slot, iters, G);
+}
+
 __device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
     uint64_t z = x + 0x9E3779B97F4A7C15ULL;
     z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;

@@ -7,6 +7,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "mi_device.hpp"
+
 namespace mi {
 
 // Tile configurations of the fp32 MFMA contraction engine (v_mfma_f32_32x32x2_f32).
@@ -81,9 +83,13 @@ struct GemmLaunch {
     int tri_cap;          // > 0: chunked triangular work list (tri_item) of the direct kernel
     // stream-K (sk_tiles > 0; direct-staged 128 / 256 tiles, batch 1, split 1):
     // the first sk_dp tiles data-parallel, the last sk_tiles dealt out as
-    // K-slices (sk_ipt per tile) over the grid_x workgroups (sk_work); the
-    // workspace holds grid_x partial tiles, added in by sk_fixup
+    // K-slices (sk_ipt per tile) over the grid_x workgroups (sk_item: the
+    // phase table sk_ph[0 .. sk_nph) when sk_nph > 0, else contiguous
+    // ranges); the workspace holds up to grid_x partial tiles, added in by
+    // sk_fixup
     int sk_dp, sk_tiles, sk_ipt;
+    int sk_nph;
+    SkPhase sk_ph[kSkMaxPhases];
 };
 
 // Direct global -> LDS staging (gemm_direct.hpp) takes launches of the 256
@@ -162,6 +168,8 @@ struct GemmParams {
     int col_splits;
     int tri_cap;
     int sk_dp, sk_tiles, sk_ipt;  // stream-K schedule (GemmLaunch)
+    int sk_nph;
+    SkPhase sk_ph[kSkMaxPhases];
     int k_chunk, split_k;
     int64_t lda, ldb, ldc;
     int64_t sa, sb, sc;
@@ -175,7 +183,7 @@ hipError_t launch_gemm_nt(const GemmLaunch& g, hipStream_t s);
 hipError_t launch_gemm_tt(const GemmLaunch& g, hipStream_t s);
 
 // After a stream-K launch: adds each split tile's workspace partials into C
-// in slot order (sk_fixup_slots).
+// in slot order (sk_tile_slots).
 hipError_t launch_sk_fixup(const GemmLaunch& g, hipStream_t s);
 hipError_t launch_splitk_reduce(const float* ws, float* C, int M, int N, int batch, int split_k,
                                 int64_t ldc, int64_t sc, const float* bias, hipStream_t s);

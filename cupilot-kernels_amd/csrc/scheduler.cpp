@@ -171,6 +171,8 @@ namespace {
 struct SkChoice {
     int dp = 0, tiles = 0, ipt = 0, grid = 0;
     size_t ws = 0;
+    int nph = 0;  // > 0: the phase table (sk_build_phases), else contiguous ranges
+    SkPhase ph[kSkMaxPhases] = {};
 };
 
 SkChoice plan_stream_k(const mi_gemm_args& a, int cfg, int num_cus) {
@@ -221,6 +223,24 @@ SkChoice plan_stream_k(const mi_gemm_args& a, int cfg, int num_cus) {
     sk.ipt = (int)ipt;
     sk.grid = (int)G;
     sk.ws = need;
+    // The phased schedule (sk_build_phases) at the smallest budget it meets,
+    // where that is no more than the contiguous ranges' busiest workgroup
+    // (plan_override MI_PLAN_SK_RANGES: always the ranges).  Its slots must
+    // not outnumber the workgroups, so the workspace stays the same.
+    if ((a.plan_override & MI_PLAN_SK_RANGES) == 0) {
+        const int64_t limit = sk_ranges_cost(S, ipt, G);
+        for (int64_t B = cdiv(S * ipt, G) + kSkSegCost; B <= limit; ++B) {
+            SkPhase ph[kSkMaxPhases];
+            int nph = 0;
+            int64_t slots = 0;
+            const int most = sk_build_phases(S, ipt, G, B, ph, nph, slots);
+            if (most > 0 && most <= kSkMaxSegments && slots <= G) {
+                sk.nph = nph;
+                for (int q = 0; q < nph; ++q) sk.ph[q] = ph[q];
+                break;
+            }
+        }
+    }
     return sk;
 }
 
@@ -242,7 +262,7 @@ int plan_core(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
     const bool no_sk = (a.plan_override & 0x20) != 0;
     const int override_cfg = a.plan_override & 0xF;
     const int override_split = (a.plan_override >> 8) & 0xFFF;
-    const int override_group = (a.plan_override >> 20) & 0x7FF;
+    const int override_group = (a.plan_override >> 20) & 0x3FF;
 
     // the 32-deep 128 tile exists only direct-staged (16-byte operands, K % 32 == 0)
     // (its row limits: the buffer offsets of 128 K-contiguous rows or 32
@@ -507,6 +527,7 @@ int plan_core(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
         best_split > 1 ? (size_t)best_split * batch * a.M * a.N * sizeof(float) : best_sk.ws;
     out.stream_k = best_sk.tiles > 0 ? 1 : 0;
     out.sk_tiles = best_sk.tiles;
+    out.sk_phases = best_sk.tiles > 0 ? best_sk.nph : 0;
 
     if (launch) {
         GemmLaunch& g = *launch;
@@ -542,6 +563,8 @@ int plan_core(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
         g.sk_dp = best_sk.dp;
         g.sk_tiles = best_sk.tiles;
         g.sk_ipt = best_sk.ipt;
+        g.sk_nph = best_sk.nph;
+        for (int q = 0; q < kSkMaxPhases; ++q) g.sk_ph[q] = best_sk.ph[q];
     }
     out.packed = 0;
     out.packed_k = 0;
@@ -594,7 +617,8 @@ mi_gemm_args packed_problem(const mi_gemm_args& a, void* workspace, size_t works
     // the planner's own choice keeps the raster grouping and "never
     // stream-K" (bit 5), which holds for whatever product runs
     const int32_t keep =
-        (a.plan_override & MI_PLAN_PACK) ? ~(MI_PLAN_NO_PACK | MI_PLAN_PACK) : ((0x7FF << 20) | 0x20);
+        (a.plan_override & MI_PLAN_PACK) ? ~(MI_PLAN_NO_PACK | MI_PLAN_PACK)
+                                         : ((0x3FF << 20) | 0x20 | MI_PLAN_SK_RANGES);
     p.plan_override = (a.plan_override & keep) | MI_PLAN_NO_PACK;
     const size_t pb = pack_bytes(a, kp);
     p.workspace = ws && workspace_bytes > pb ? ws + pb : nullptr;

@@ -347,21 +347,26 @@ hipError_t launch_splitk_reduce(const float* ws, float* C, int M, int N, int bat
 }
 
 // Stream-K fixup: one workgroup per (stream-K tile, band of rows).  The tile's
-// head segment (k from 0) is already in C; the partials of the workgroups
-// whose K-slice ranges start inside the tile sit in their workspace slots
-// (tile-local, bm x bn) and are added in slot order, i.e. in k order -- a
-// fixed order, so the result is the same on every call.  A slot whose
-// workgroup had an empty range holds nothing and is skipped.
+// head segment (k from 0) is already in C; its other segments sit in their
+// workspace slots (tile-local, bm x bn) and are added in slot order, i.e. in
+// k order -- a fixed order, so the result is the same on every call.  A slot
+// whose workgroup had an empty range (contiguous ranges only) holds nothing
+// and is skipped.  The schedule (SkSched, by value) is the launch's.
+struct SkSched {
+    int n_dp, S, ipt, G, nph;
+    SkPhase ph[kSkMaxPhases];
+};
+
 template <bool VEC>
 __global__ void __launch_bounds__(256)
     sk_fixup_kernel(float* __restrict__ C, const float* __restrict__ ws, int64_t ldc, int M, int N,
-                    int bm, int bn, int tiles_m, int tiles_n, int group_m, int n_dp, int S, int ipt,
-                    int G, int band_rows) {
+                    int bm, int bn, int tiles_m, int tiles_n, int group_m, const SkSched sc,
+                    int band_rows) {
     const int t = blockIdx.x;
     int64_t first, count;
-    sk_fixup_slots(t, S, ipt, G, first, count);
+    sk_tile_slots(t, sc.S, sc.ipt, sc.G, sc.ph, sc.nph, first, count);
     if (count == 0) return;
-    const int64_t iters = (int64_t)S * ipt;
+    const int n_dp = sc.n_dp;
     int tm, tn;
     raster(n_dp + t, tiles_m, tiles_n, group_m, tm, tn);
     constexpr int W = VEC ? 4 : 1;
@@ -377,17 +382,17 @@ __global__ void __launch_bounds__(256)
         if constexpr (VEC) {
             f4 v = *reinterpret_cast<const f4*>(dst);
             for (int64_t q = 0; q < count; ++q) {
-                const int64_t lg = first + q;
-                if (sk_begin(lg + 1, iters, G) == sk_begin(lg, iters, G)) continue;
-                v += *reinterpret_cast<const f4*>(src + lg * slot_elems);
+                const int64_t slot = first + q;
+                if (!sk_slot_used(slot, sc.S, sc.ipt, sc.G, sc.nph)) continue;
+                v += *reinterpret_cast<const f4*>(src + slot * slot_elems);
             }
             *reinterpret_cast<f4*>(dst) = v;
         } else {
             float v = *dst;
             for (int64_t q = 0; q < count; ++q) {
-                const int64_t lg = first + q;
-                if (sk_begin(lg + 1, iters, G) == sk_begin(lg, iters, G)) continue;
-                v += src[lg * slot_elems];
+                const int64_t slot = first + q;
+                if (!sk_slot_used(slot, sc.S, sc.ipt, sc.G, sc.nph)) continue;
+                v += src[slot * slot_elems];
             }
             *dst = v;
         }
@@ -400,14 +405,19 @@ hipError_t launch_sk_fixup(const GemmLaunch& g, hipStream_t s) {
     const dim3 grid((unsigned)g.sk_tiles, (unsigned)(ci.bm / band_rows));
     const bool vec = g.N % 4 == 0 && g.ldc % 4 == 0 && ((uintptr_t)g.C & 15u) == 0 &&
                      ((uintptr_t)g.ws & 15u) == 0;
+    SkSched sc;
+    sc.n_dp = g.sk_dp;
+    sc.S = g.sk_tiles;
+    sc.ipt = g.sk_ipt;
+    sc.G = g.grid_x;
+    sc.nph = g.sk_nph;
+    for (int q = 0; q < kSkMaxPhases; ++q) sc.ph[q] = g.sk_ph[q];
     if (vec)
         hipLaunchKernelGGL(sk_fixup_kernel<true>, grid, dim3(256), 0, s, g.C, g.ws, g.ldc, g.M, g.N,
-                           ci.bm, ci.bn, g.tiles_m, g.tiles_n, g.group_m, g.sk_dp, g.sk_tiles,
-                           g.sk_ipt, g.grid_x, band_rows);
+                           ci.bm, ci.bn, g.tiles_m, g.tiles_n, g.group_m, sc, band_rows);
     else
         hipLaunchKernelGGL(sk_fixup_kernel<false>, grid, dim3(256), 0, s, g.C, g.ws, g.ldc, g.M, g.N,
-                           ci.bm, ci.bn, g.tiles_m, g.tiles_n, g.group_m, g.sk_dp, g.sk_tiles,
-                           g.sk_ipt, g.grid_x, band_rows);
+                           ci.bm, ci.bn, g.tiles_m, g.tiles_n, g.group_m, sc, band_rows);
     return hipGetLastError();
 }
 

@@ -91,8 +91,10 @@ typedef struct {
                                  bit 5 never stream-K, bit 6 (MI_PLAN_NO_PACK) never pack the
                                  operands, bit 7 (MI_PLAN_PACK) pack them where packing applies
                                  (the other bits then apply to the packed product), bits 8-19
-                                 split count, bits 20-30 raster group rows; a config the
-                                 problem cannot take is ignored */
+                                 split count, bits 20-29 raster group rows, bit 30
+                                 (MI_PLAN_SK_RANGES) stream-K over contiguous K-slice ranges
+                                 instead of phases (mi_plan.sk_phases); a config the problem
+                                 cannot take is ignored */
     void* workspace;
     size_t workspace_bytes;
     const float* bias_m;      /* NULL, or M floats: C[b][i][j] = (sum over k) + bias_m[i],
@@ -103,6 +105,8 @@ typedef struct {
 /* plan_override bits 6 and 7 (operand packing, see mi_plan.packed) */
 #define MI_PLAN_NO_PACK 0x40
 #define MI_PLAN_PACK 0x80
+/* plan_override bit 30 (see mi_plan.sk_phases) */
+#define MI_PLAN_SK_RANGES 0x40000000
 
 /* Scheduler decision for one contraction (host-only, no device access). */
 typedef struct {
@@ -116,8 +120,8 @@ typedef struct {
     int64_t grid;           /* workgroups launched per (split, batch); each walks tiles
                                wg, wg + grid, ... (persistent; stream-K plans: see
                                mi_gemm_work_item) */
-    size_t workspace_bytes; /* split-K partial tiles, or one stream-K partial tile per
-                               workgroup */
+    size_t workspace_bytes; /* split-K partial tiles, or stream-K partial tiles (one
+                               slot per workgroup) */
     int32_t stream_k;       /* 1: stream-K schedule -- the last sk_tiles tiles' K-slices
                                are dealt out evenly over the grid workgroups (the
                                first num_tiles - sk_tiles tiles stay whole), partial
@@ -128,6 +132,12 @@ typedef struct {
                                fields above describe the N/T product of the packed
                                operands; workspace_bytes includes the packed copies */
     int64_t packed_k;
+    int32_t sk_phases;      /* stream-K plans: 0 -- each workgroup reduces one contiguous
+                               range of the tiles' K-slices (each starting at its own
+                               offset); > 0 -- that many phases, in each of which a run of
+                               workgroups reduces the same K range of neighbouring tiles,
+                               starting together, so that one XCD's workgroups read the
+                               same slices (mi_gemm_work_item shows the segments) */
 } mi_plan;
 
 /* One work item of a workgroup under a plan (host introspection). */

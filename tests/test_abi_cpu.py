@@ -432,14 +432,17 @@ def test_symmetric_structure_is_the_nn_dense_plan(ck):
 
 SK_FORCE = 0x10
 SK_NEVER = 0x20
+SK_RANGES = 0x40000000   # MI_PLAN_SK_RANGES: contiguous ranges instead of phases
 
 
 def _sk_cover(ck, args, num_cus=256):
     """Enumerate every workgroup's items under a stream-K plan and check the
     schedule: each output tile's K range is covered exactly once, in whole
     slices; the segment that starts at k = 0 is written to C and every other
-    segment to its workgroup's own slot (one per workgroup); the data-parallel
-    tiles come whole; the fixup adds exactly a tile's slot segments, in k order."""
+    segment to a slot of its own (at most one per workgroup for contiguous
+    ranges, at most three segments per workgroup for phases); the
+    data-parallel tiles come whole; the fixup adds exactly a tile's slot
+    segments, in k order."""
     rc, p = ck.abi.plan(args.M, args.N, args.K, num_cus=num_cus, op_a=args.op_a, op_b=args.op_b,
                         workspace_bytes=args.workspace_bytes, plan_override=args.plan_override)
     assert rc == 0 and p.stream_k == 1 and p.split_k == 1
@@ -460,7 +463,11 @@ def _sk_cover(ck, args, num_cus=256):
                 slots_used[slot] = (tm, tn, kb, ke)
                 assert 0 <= slot < p.grid
             segs.setdefault((tm, tn), []).append((kb, ke, dest, slot))
-        assert n_ws <= 1, "a workgroup's range starts inside a tile at most once"
+        if p.sk_phases == 0:
+            assert n_ws <= 1, "a workgroup's range starts inside a tile at most once"
+        else:
+            n_dp = (p.num_tiles - p.sk_tiles) // p.grid
+            assert len(items) - n_dp <= 3, "at most kSkMaxSegments segments per workgroup"
     assert set(segs) == {(i, j) for i in range(p.tiles_m) for j in range(p.tiles_n)}
     for tile, parts in segs.items():
         parts.sort()
@@ -504,19 +511,81 @@ def _sk_cover(ck, args, num_cus=256):
     (3001, 3001, 3001, 2, (0, 1)),    # 576 tiles, every one stream-K
     (2048, 2048, 4100, 2, (1, 1)),    # 16-byte rows, K % 16 == 4
 ])
-def test_stream_k_schedule_covers_every_tile_once(ck, M, N, K, cfg, ops):
+@pytest.mark.parametrize("ranges", [False, True])
+def test_stream_k_schedule_covers_every_tile_once(ck, M, N, K, cfg, ops, ranges):
     args = ck.abi.make_args(M, N, K, op_a=ops[0], op_b=ops[1], workspace_bytes=1 << 40,
-                            plan_override=cfg | SK_FORCE)
+                            plan_override=cfg | SK_FORCE | (SK_RANGES if ranges else 0))
     p, segs = _sk_cover(ck, args)
+    if ranges:
+        assert p.sk_phases == 0
     T, G = p.num_tiles, p.grid
     waves = T // G
     assert p.sk_tiles == T - waves * G  # whole waves data-parallel, the rest stream-K
-    # balance: every workgroup reduces the same number of K-slices, +-1 (a
-    # partial last slice counts as one)
-    per_wg = []
-    for wg in range(G):
-        per_wg.append(sum(-(-(ke - kb) // p.block_k) for _, _, kb, ke, _, _ in ck.abi.work_items(args, wg)))
-    assert max(per_wg) - min(per_wg) <= 1
+    # balance: contiguous ranges give every workgroup the same number of
+    # K-slices, +-1 (a partial last slice counts as one); phases give the
+    # busiest workgroup no more slices + 2 per segment (kSkSegCost, the
+    # planner's charge for a segment's store and restart) than the ranges
+    # give theirs
+    def costs(a):
+        out = []
+        for wg in range(G):
+            items = ck.abi.work_items(a, wg)
+            out.append((sum(-(-(ke - kb) // p.block_k) for _, _, kb, ke, _, _ in items), len(items)))
+        return out
+    per_wg = costs(args)
+    ipt = -(-K // p.block_k)
+    assert sum(n for n, _ in per_wg) == T * ipt
+    if p.sk_phases == 0:
+        assert max(n for n, _ in per_wg) - min(n for n, _ in per_wg) <= 1
+    else:
+        args_r = ck.abi.make_args(M, N, K, op_a=ops[0], op_b=ops[1], workspace_bytes=1 << 40,
+                                  plan_override=cfg | SK_FORCE | SK_RANGES)
+        assert max(n + 2 * s for n, s in per_wg) <= max(n + 2 * s for n, s in costs(args_r))
+
+
+def _sk_phase_offsets(ck, args, p):
+    """For every stream-K segment: (slice offset = its first k-slice minus the
+    slices its workgroup ran before it, tile, hardware workgroup)."""
+    out = []
+    n_dp = (p.num_tiles - p.sk_tiles) // p.grid
+    for wg in range(p.grid):
+        t = 0
+        for i, (tm, tn, kb, ke, _, _) in enumerate(ck.abi.work_items(args, wg)):
+            n = -(-(ke - kb) // p.block_k)
+            if i >= n_dp:
+                out.append((kb // p.block_k - t, (tm, tn), wg))
+            t += n
+    return out
+
+
+def _sk_panel_share(segs):
+    """Distinct tile rows + columns read by each (slice offset, XCD) group of
+    segments -- the A and B panels its workgroups read together -- over twice
+    the segments: 1.0 when no two co-running segments of an XCD share a panel."""
+    groups = {}
+    for o, tile, wg in segs:
+        groups.setdefault((o, wg % 8), []).append(tile)
+    panels = sum(len({a for a, _ in t}) + len({b for _, b in t}) for t in groups.values())
+    return panels / (2 * len(segs))
+
+
+@pytest.mark.parametrize("M,N,K", [(3072, 3072, 8192), (4608, 4608, 4608), (3584, 3584, 3584)])
+def test_stream_k_phases_run_in_step(ck, M, N, K):
+    """The planner's phased schedule: every segment of a phase reduces the same
+    K range starting at the same moment (one slice offset per phase), and the
+    segments an XCD runs together read few distinct A row and B column panels
+    (0.17-0.30 of one pair per segment on these shapes), where contiguous
+    ranges share none (1.0)."""
+    args = ck.abi.make_args(M, N, K, workspace_bytes=1 << 40)
+    rc, p = ck.abi.plan(M, N, K, workspace_bytes=1 << 40)
+    assert rc == 0 and p.stream_k == 1 and 0 < p.sk_phases <= 12
+    segs = _sk_phase_offsets(ck, args, p)
+    assert len({o for o, _, _ in segs}) <= p.sk_phases
+    assert _sk_panel_share(segs) <= 0.35
+    args_r = ck.abi.make_args(M, N, K, workspace_bytes=1 << 40, plan_override=SK_RANGES)
+    rc, pr = ck.abi.plan(M, N, K, workspace_bytes=1 << 40, plan_override=SK_RANGES)
+    assert rc == 0 and pr.stream_k == 1 and pr.sk_phases == 0
+    assert _sk_panel_share(_sk_phase_offsets(ck, args_r, pr)) >= 0.9
 
 
 def test_stream_k_applies_only_where_it_can(ck):

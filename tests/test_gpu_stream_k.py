@@ -3,7 +3,8 @@ in every layout on the direct-staged 256 and 128 tiles (16-byte and, on the
 128 tile, 4-byte staging with a partial last slice) and the k-split 64 tile, tiles split over many workgroups
 and ragged edges, a data-parallel wave ahead of the stream-K tiles, bitwise
 repeatability (the fixup adds partials in a fixed order), and agreement with
-the data-parallel plan of the same problem.
+the data-parallel plan of the same problem -- each under both schedules the
+planner deals K-slices with (phases, where they apply, and contiguous ranges).
 
 Bar: normalised max error <= 1e-4 against fp64; bitwise equality across runs.
 """
@@ -17,6 +18,7 @@ from gpu_util import assert_close, gemm_args, run_gemm, to_dev, to_host, workspa
 pytestmark = pytest.mark.gpu
 
 SK_FORCE, SK_NEVER = 0x10, 0x20
+SK_RANGES = 0x40000000  # contiguous K-slice ranges instead of the phased schedule
 LAYOUTS = [(0, 0), (1, 0), (0, 1), (1, 1)]
 
 
@@ -53,13 +55,18 @@ def _plan(ck, M, N, K, op_a, op_b, override):
     (1000, 1100, 1021, 2),   # 4-byte staging (K % 16 != 0): each tile's last slice partial
     (640, 643, 2047, 2),     # 4-byte staging, N and K odd
 ])
-def test_stream_k_parity(ck, orc, dev, op_a, op_b, M, N, K, cfg):
-    p = _plan(ck, M, N, K, op_a, op_b, cfg | SK_FORCE)
+@pytest.mark.parametrize("ranges", [False, True])
+def test_stream_k_parity(ck, orc, dev, op_a, op_b, M, N, K, cfg, ranges):
+    ov = cfg | SK_FORCE | (SK_RANGES if ranges else 0)
+    p = _plan(ck, M, N, K, op_a, op_b, ov)
     assert p.stream_k == 1 and p.plan_id == cfg
+    if ranges:
+        assert p.sk_phases == 0
     a_st, b_st, a, b = _operands(orc, M, N, K, op_a, op_b, seed=4100 + cfg)
     A, B = to_dev(a_st), to_dev(b_st)
-    C = _run(ck, A, B, M, N, K, op_a, op_b, cfg | SK_FORCE)
-    assert_close(orc, to_host(C), orc.gemm(a, b), K, what=f"stream-K {op_a}{op_b} {M}x{N}x{K} cfg{cfg}")
+    C = _run(ck, A, B, M, N, K, op_a, op_b, ov)
+    assert_close(orc, to_host(C), orc.gemm(a, b), K,
+                 what=f"stream-K {op_a}{op_b} {M}x{N}x{K} cfg{cfg} phases {p.sk_phases}")
 
 
 @pytest.mark.parametrize("M,N,K,cfg,ops", [
@@ -67,18 +74,20 @@ def test_stream_k_parity(ck, orc, dev, op_a, op_b, M, N, K, cfg):
     (5120, 5120, 2048, 3, (1, 1)),   # 400 tiles of 256: 1.56 tiles per workgroup
     (3584, 3584, 1024, 3, (0, 1)),   # 196 tiles < 256 workgroups
     (1536, 1536, 2048, 10, (1, 0)),  # 576 tiles of 64: 256 data-parallel + 320 stream-K
-    (8205, 2949, 5921, 2, (0, 0)),   # 4-byte staging: one data-parallel wave + 792 stream-K tiles
+    (8205, 2949, 5921, 2, (0, 0)),   # 4-byte staging: two data-parallel waves + 24 stream-K tiles
     (3001, 3001, 3001, 2, (1, 1)),   # 4-byte staging: 576 tiles, every one stream-K
 ])
-def test_stream_k_larger_every_element(ck, orc, dev, M, N, K, cfg, ops):
+@pytest.mark.parametrize("ranges", [False, True])
+def test_stream_k_larger_every_element(ck, orc, dev, M, N, K, cfg, ops, ranges):
     """Bigger stream-K schedules, every element through fp64 row and column
     checksums, plus exact fp64 rows."""
     op_a, op_b = ops
-    p = _plan(ck, M, N, K, op_a, op_b, cfg | SK_FORCE)
+    ov = cfg | SK_FORCE | (SK_RANGES if ranges else 0)
+    p = _plan(ck, M, N, K, op_a, op_b, ov)
     assert p.stream_k == 1 and p.plan_id == cfg
     a_st, b_st, a, b = _operands(orc, M, N, K, op_a, op_b, seed=4200 + cfg)
     A, B = to_dev(a_st), to_dev(b_st)
-    Cd = _run(ck, A, B, M, N, K, op_a, op_b, cfg | SK_FORCE)
+    Cd = _run(ck, A, B, M, N, K, op_a, op_b, ov)
     C = to_host(Cd)
     rows = sorted({0, 1, 255, 256, 257, M // 2, M - 1})
     assert_close(orc, C[rows], orc.gemm(a, b, rows=rows), K, what="stream-K rows")
@@ -89,13 +98,15 @@ def test_stream_k_larger_every_element(ck, orc, dev, M, N, K, cfg, ops):
 
 @pytest.mark.parametrize("M,N,K,cfg", [(1280, 1280, 2048, 3), (640, 640, 2048, 2), (640, 640, 2048, 10),
                                        (1000, 1100, 1021, 2)])
-def test_stream_k_bitwise_repeatable(ck, orc, dev, M, N, K, cfg):
+@pytest.mark.parametrize("ranges", [False, True])
+def test_stream_k_bitwise_repeatable(ck, orc, dev, M, N, K, cfg, ranges):
     """20 runs, bitwise identical: every partial tile is added in slot order."""
+    ov = cfg | SK_FORCE | (SK_RANGES if ranges else 0)
     a_st, b_st, _, _ = _operands(orc, M, N, K, 0, 0, seed=4300)
     A, B = to_dev(a_st), to_dev(b_st)
-    first = to_host(_run(ck, A, B, M, N, K, 0, 0, cfg | SK_FORCE))
+    first = to_host(_run(ck, A, B, M, N, K, 0, 0, ov))
     for _ in range(19):
-        np.testing.assert_array_equal(to_host(_run(ck, A, B, M, N, K, 0, 0, cfg | SK_FORCE)), first)
+        np.testing.assert_array_equal(to_host(_run(ck, A, B, M, N, K, 0, 0, ov)), first)
 
 
 @pytest.mark.parametrize("M,N,K,cfg", [(1280, 1280, 2048, 3), (640, 640, 2048, 2), (640, 640, 2048, 10),
@@ -107,8 +118,10 @@ def test_stream_k_integer_inputs_exact(ck, orc, dev, M, N, K, cfg):
     b = orc.integers((K, N), 4401)
     A, B = to_dev(a), to_dev(b)
     sk = to_host(_run(ck, A, B, M, N, K, 0, 0, cfg | SK_FORCE))
+    skr = to_host(_run(ck, A, B, M, N, K, 0, 0, cfg | SK_FORCE | SK_RANGES))
     dp = to_host(_run(ck, A, B, M, N, K, 0, 0, cfg | SK_NEVER))
     np.testing.assert_array_equal(sk, dp)
+    np.testing.assert_array_equal(skr, dp)
     np.testing.assert_array_equal(sk, (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float32))
 
 
