@@ -14,7 +14,8 @@
 //                   + exposed(c, occ) * output bytes * s / sustained write bandwidth
 //                   + split-K reduction (read s partials, write C; one pass)
 //   stream-K(c)   = the same MFMA work spread evenly over every resident
-//                   workgroup, one partial tile per workgroup, and the fixup
+//                   workgroup, a partial tile per workgroup (the priced
+//                   upper bound of either schedule's workspace slots), and the fixup
 // and picks the cheapest.  The constants are fitted to MI355X timings (see
 // kModels).  Triangular problems use a square tiling with the compute tiles
 // ordered longest-K first.
@@ -163,11 +164,13 @@ int validate_shape(const mi_gemm_args& a) {
 
 namespace {
 
-// Stream-K schedule of a dense product on config cfg (sk_work in
-// mi_device.hpp), or sk.tiles = 0 where it does not apply: batch 1, no bias,
-// the direct-staged 16-byte kernels (every K-slice full), a tile count that
-// whole waves of the persistent grid do not cover exactly, at least two
-// slices per workgroup, and a workspace for one partial tile per workgroup.
+// Stream-K schedule of a dense product on config cfg (sk_item in
+// mi_device.hpp: contiguous K-slice ranges, or the phase table), or
+// sk.tiles = 0 where it does not apply: batch 1, no bias, the direct-staged
+// 16-byte kernels (every K-slice full), a tile count that whole waves of the
+// persistent grid do not cover exactly, at least two slices per workgroup,
+// and a workspace of one partial tile per workgroup (either schedule's slots
+// fit it).
 struct SkChoice {
     int dp = 0, tiles = 0, ipt = 0, grid = 0;
     size_t ws = 0;
