@@ -311,15 +311,26 @@ inline int sk_build_phases(int64_t S, int64_t ipt, int64_t G, int64_t B, SkPhase
 
 // Host: the busiest workgroup's cost (slices + kSkSegCost per segment) under
 // the contiguous ranges.
+// (The planner asks this for every candidate tile config, so it walks the
+// ranges incrementally: range lg is [lg I / G, (lg + 1) I / G) with
+// I = S ipt, and its first and last slices' tiles only move forward.)
 inline int64_t sk_ranges_cost(int64_t S, int64_t ipt, int64_t G) {
-    const int64_t iters = S * ipt;
-    int64_t most = 0;
+    const int64_t iters = S * ipt, q = iters / G, rem = iters % G;
+    int64_t most = 0, b = 0, acc = 0, tb = 0, te = 0;  // tb = b / ipt, te = (e - 1) / ipt
     for (int64_t lg = 0; lg < G; ++lg) {
-        const int64_t b = lg * iters / G, e = (lg + 1) * iters / G;
-        if (e == b) continue;
-        const int64_t segs = (e - 1) / ipt - b / ipt + 1;
-        const int64_t cost = e - b + kSkSegCost * segs;
-        most = cost > most ? cost : most;
+        int64_t e = b + q;
+        acc += rem;
+        if (acc >= G) {
+            acc -= G;
+            ++e;
+        }
+        if (e > b) {
+            while ((tb + 1) * ipt <= b) ++tb;
+            while ((te + 1) * ipt <= e - 1) ++te;
+            const int64_t cost = e - b + kSkSegCost * (te - tb + 1);
+            most = cost > most ? cost : most;
+        }
+        b = e;
     }
     return most;
 }

@@ -226,25 +226,31 @@ SkChoice plan_stream_k(const mi_gemm_args& a, int cfg, int num_cus) {
     sk.ipt = (int)ipt;
     sk.grid = (int)G;
     sk.ws = need;
-    // The phased schedule (sk_build_phases) at the smallest budget it meets,
-    // where that is no more than the contiguous ranges' busiest workgroup
-    // (plan_override MI_PLAN_SK_RANGES: always the ranges).  Its slots must
-    // not outnumber the workgroups, so the workspace stays the same.
-    if ((a.plan_override & MI_PLAN_SK_RANGES) == 0) {
-        const int64_t limit = sk_ranges_cost(S, ipt, G);
-        for (int64_t B = cdiv(S * ipt, G) + kSkSegCost; B <= limit; ++B) {
-            SkPhase ph[kSkMaxPhases];
-            int nph = 0;
-            int64_t slots = 0;
-            const int most = sk_build_phases(S, ipt, G, B, ph, nph, slots);
-            if (most > 0 && most <= kSkMaxSegments && slots <= G) {
-                sk.nph = nph;
-                for (int q = 0; q < nph; ++q) sk.ph[q] = ph[q];
-                break;
-            }
+    return sk;
+}
+
+// The phased schedule (sk_build_phases) of a stream-K choice at the smallest
+// budget it meets, where that is no more than the contiguous ranges' busiest
+// workgroup (plan_override MI_PLAN_SK_RANGES: always the ranges).  Its slots
+// must not outnumber the workgroups, so the workspace stays the same.  Only
+// the chosen plan's schedule is built: the cost model prices stream-K the
+// same under either.
+void sk_choose_phases(const mi_gemm_args& a, SkChoice& sk) {
+    sk.nph = 0;
+    if (sk.tiles <= 0 || (a.plan_override & MI_PLAN_SK_RANGES) != 0) return;
+    const int64_t S = sk.tiles, ipt = sk.ipt, G = sk.grid;
+    const int64_t limit = sk_ranges_cost(S, ipt, G);
+    for (int64_t B = cdiv(S * ipt, G) + kSkSegCost; B <= limit; ++B) {
+        SkPhase ph[kSkMaxPhases];
+        int nph = 0;
+        int64_t slots = 0;
+        const int most = sk_build_phases(S, ipt, G, B, ph, nph, slots);
+        if (most > 0 && most <= kSkMaxSegments && slots <= G) {
+            sk.nph = nph;
+            for (int q = 0; q < nph; ++q) sk.ph[q] = ph[q];
+            return;
         }
     }
-    return sk;
 }
 
 // The planner proper (plan_gemm below adds the choice of packing the
@@ -528,6 +534,7 @@ int plan_core(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
     out.grid = grid;
     out.workspace_bytes =
         best_split > 1 ? (size_t)best_split * batch * a.M * a.N * sizeof(float) : best_sk.ws;
+    sk_choose_phases(a, best_sk);
     out.stream_k = best_sk.tiles > 0 ? 1 : 0;
     out.sk_tiles = best_sk.tiles;
     out.sk_phases = best_sk.tiles > 0 ? best_sk.nph : 0;
