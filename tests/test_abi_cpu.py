@@ -588,6 +588,47 @@ def test_stream_k_phases_run_in_step(ck, M, N, K):
     assert _sk_panel_share(_sk_phase_offsets(ck, args_r, pr)) >= 0.9
 
 
+def _random_sk_shapes(n, seed):
+    """Seeded shapes spread over the stream-K region of each tile config: M, N
+    multiples of 16 (16-byte rows), K a multiple of 64 (every config's slices
+    full), from a few tiles to just under a few waves."""
+    import random
+    rnd = random.Random(seed)
+    out = []
+    for _ in range(n):
+        cfg = rnd.choice([3, 3, 2, 9, 10])
+        M = 16 * rnd.randint(8, 480)
+        N = 16 * rnd.randint(8, 480)
+        K = 64 * rnd.randint(16, 96)
+        out.append((M, N, K, cfg))
+    return out
+
+
+@pytest.mark.parametrize("M,N,K,cfg", _random_sk_shapes(40, 2026))
+def test_stream_k_random_shapes_both_schedules(ck, M, N, K, cfg):
+    """Random shapes, stream-K forced on the config, under the planner's
+    schedule and under contiguous ranges: the full coverage, slot and fixup
+    checks of _sk_cover, and the phased schedule never more than 3 segments
+    per workgroup nor a higher busiest-workgroup cost than the ranges."""
+    cost = {}
+    for extra in (0, SK_RANGES):
+        args = ck.abi.make_args(M, N, K, workspace_bytes=1 << 40, plan_override=cfg | SK_FORCE | extra)
+        rc, p = ck.abi.plan(M, N, K, workspace_bytes=1 << 40, plan_override=cfg | SK_FORCE | extra)
+        assert rc == 0
+        if p.stream_k != 1:   # the config does not take stream-K here (whole waves, too few slices)
+            return
+        if extra:
+            assert p.sk_phases == 0
+        _sk_cover(ck, args)
+        # busiest workgroup: its slices + 2 per item (kSkSegCost)
+        worst = 0
+        for wg in range(p.grid):
+            items = ck.abi.work_items(args, wg)
+            worst = max(worst, sum(-(-(ke - kb) // p.block_k) + 2 for _, _, kb, ke, _, _ in items))
+        cost[extra] = worst
+    assert cost[0] <= cost[SK_RANGES]
+
+
 def test_stream_k_applies_only_where_it_can(ck):
     # whole waves (1024 tiles of 256 on 256 CUs), a batch, a bias, operands the
     # direct kernel cannot stage, no workspace: no stream-K even when asked
