@@ -132,3 +132,34 @@ def test_stream_k_matches_data_parallel_within_tolerance(ck, orc, dev):
     sk = to_host(_run(ck, A, B, M, N, K, 0, 0, 3 | SK_FORCE))
     dp = to_host(_run(ck, A, B, M, N, K, 0, 0, 3 | SK_NEVER))
     assert orc.norm_err(sk, dp.astype(np.float64), K, 1.0, 1.0) <= 2 * orc.TOL
+
+
+def _random_sk_shapes(n, seed):
+    """Seeded shapes over the stream-K region of each tile config (16-byte
+    rows, K a multiple of 64), the same generator as the CPU schedule test."""
+    import random
+    rnd = random.Random(seed)
+    out = []
+    for _ in range(n):
+        cfg = rnd.choice([3, 3, 2, 9, 10])
+        out.append((16 * rnd.randint(8, 480), 16 * rnd.randint(8, 480), 64 * rnd.randint(16, 96), cfg))
+    return out
+
+
+@pytest.mark.parametrize("M,N,K,cfg", _random_sk_shapes(12, 2027))
+def test_stream_k_random_shapes_every_element(ck, orc, dev, M, N, K, cfg):
+    """Seeded random shapes with stream-K forced on their config, under the
+    planner's schedule (phases where they apply): every element through fp64
+    row and column checksums, plus exact rows."""
+    p = _plan(ck, M, N, K, 0, 0, cfg | SK_FORCE)
+    if p.stream_k != 1:
+        pytest.skip("the config takes no stream-K plan for this shape")
+    a = orc.uniform((M, K), 4600 + cfg)
+    b = orc.uniform((K, N), 4601 + cfg)
+    C = to_host(_run(ck, to_dev(a), to_dev(b), M, N, K, 0, 0, cfg | SK_FORCE))
+    rows = sorted({0, M // 3, M - 1})
+    assert_close(orc, C[rows], orc.gemm(a, b, rows=rows), K,
+                 what=f"stream-K {M}x{N}x{K} cfg{cfg} phases {p.sk_phases} rows")
+    v, u = fv.signs(N, 11), fv.signs(M, 12)
+    fv.check(orc, *orc.checksums(C, v, u), *fv.reference(orc, a, b, v, u), K, 1.0, 1.0,
+             f"stream-K {M}x{N}x{K} cfg{cfg} phases {p.sk_phases} every element")
