@@ -374,8 +374,9 @@ struct QkSoftmaxParams {
 
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
     qk_softmax_kernel(const QkSoftmaxParams p, int heads) {
-    constexpr int BM = 128, BN = 512, WM = 64, WN = 128, TM = 2, TN = 4, BKH = 64;
-    using LA = DirectLoader<true, 8, 128, 32>;
+    // a 128-query x 512-key tile (BN = 512 keys: the loader shape below)
+    constexpr int BM = 128, WM = 64, WN = 128, TM = 2, TN = 4, BKH = 64;
+    using LA = DirectLoader<true, 8, BM, 32>;
     using LB = DirectLoader<true, 8, 512, 32>;
     __shared__ __attribute__((aligned(16))) float sA0[LA::ELEMS];
     __shared__ __attribute__((aligned(16))) float sA1[LA::ELEMS];
