@@ -582,7 +582,9 @@ __global__ void __launch_bounds__(T::NT)
     // registers (set 0) when compute starts.
     constexpr int NKB = T::BK / 8;
     constexpr bool SPREAD = VB == 16 && NKB >= 2;
-    constexpr bool PRIO = T::BM == 256;  // see the slice barrier below
+    // wave priority across the slice barrier (see there): the 256 tile, and
+    // the 8-wave 128 tile with a row-major B
+    constexpr bool PRIO = T::BM == 256 || (std::is_same<T, Tile128W8>::value && !B_KC);
     auto compute = [&](const float* As, const float* Bs, auto&& loads, auto&& part) __attribute__((always_inline)) {
         if constexpr (!SPREAD) loads();
         __builtin_amdgcn_sched_barrier(0);
@@ -765,6 +767,10 @@ __global__ void __launch_bounds__(T::NT)
         // 8192^3: N/N 151.7 vs 149.9, T/N 151.9 vs 149.2, N/T 152.3 vs 149.8,
         // T/T 151.4 vs 150.4 TFLOP/s.  (The 128 tile, three workgroups per CU
         // at different phases, lost 2.5 % that way on 65536 x 512 x 256.)
+        // The 8-wave 128 tile (two workgroups per CU) gains 0.2-0.8 % with a
+        // row-major B (2048 x 4096 x 8192 0.920 vs 0.926 ms, 4096 x 2048 x
+        // 4096 0.465 vs 0.468, 16384 x 768 x 2048 0.355 vs 0.356) and loses
+        // 0.2 % with B stored N x K, so only the former raises it.
         if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
         // the next slice's first k-block (fragment set 0; the held-back MFMAs
         // use set (NKB - 1) & 1 = 1), with that slice's masks
