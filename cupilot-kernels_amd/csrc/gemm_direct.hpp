@@ -582,9 +582,12 @@ __global__ void __launch_bounds__(T::NT)
     // registers (set 0) when compute starts.
     constexpr int NKB = T::BK / 8;
     constexpr bool SPREAD = VB == 16 && NKB >= 2;
-    // wave priority across the slice barrier (see there): the 256 tile, and
-    // the 8-wave 128 tile with a row-major B
-    constexpr bool PRIO = T::BM == 256 || (std::is_same<T, Tile128W8>::value && !B_KC);
+    // wave priority across the slice barrier (see there): the 256 tile; with
+    // a row-major B the 8-wave 128 tile and the 32-deep 128 tile's stream-K
+    // kernel; the 128 tile's 16-byte stream-K kernel
+    constexpr bool PRIO = T::BM == 256 || (std::is_same<T, Tile128W8>::value && !B_KC) ||
+                          (std::is_same<T, Tile128B32>::value && !B_KC && SK) ||
+                          (std::is_same<T, Tile128>::value && SK && VB == 16);
     auto compute = [&](const float* As, const float* Bs, auto&& loads, auto&& part) __attribute__((always_inline)) {
         if constexpr (!SPREAD) loads();
         __builtin_amdgcn_sched_barrier(0);
@@ -770,7 +773,12 @@ __global__ void __launch_bounds__(T::NT)
         // The 8-wave 128 tile (two workgroups per CU) gains 0.2-0.8 % with a
         // row-major B (2048 x 4096 x 8192 0.920 vs 0.926 ms, 4096 x 2048 x
         // 4096 0.465 vs 0.468, 16384 x 768 x 2048 0.355 vs 0.356) and loses
-        // 0.2 % with B stored N x K, so only the former raises it.
+        // 0.2 % with B stored N x K, so only the former raises it.  So does
+        // the 32-deep 128 tile's stream-K kernel (N/N 0.5-1.1 %, T/N 1.4-2.2 %
+        // faster; N/T and T/T 0.2-0.5 % slower, and its data-parallel plans up
+        // to 1.2 % slower); the 128 tile's 16-byte stream-K kernel gains in
+        // every layout (3072^3 N/N 0.432 vs 0.438 ms, 4608^3 1.383 vs 1.414).
+        // Measured in one process each, alternating, medians of 3.
         if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
         // the next slice's first k-block (fragment set 0; the held-back MFMAs
         // use set (NKB - 1) & 1 = 1), with that slice's masks
