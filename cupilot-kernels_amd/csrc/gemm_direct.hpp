@@ -584,10 +584,10 @@ __global__ void __launch_bounds__(T::NT)
     constexpr bool SPREAD = VB == 16 && NKB >= 2;
     // wave priority across the slice barrier (see there): the 256 tile; with
     // a row-major B the 8-wave 128 tile and the 32-deep 128 tile's stream-K
-    // kernel; the 128 tile's stream-K kernels
+    // kernel; the 128 tile's stream-K kernels and its 4-byte staging
     constexpr bool PRIO = T::BM == 256 || (std::is_same<T, Tile128W8>::value && !B_KC) ||
                           (std::is_same<T, Tile128B32>::value && !B_KC && SK) ||
-                          (std::is_same<T, Tile128>::value && SK);
+                          (std::is_same<T, Tile128>::value && (SK || VB == 4));
     auto compute = [&](const float* As, const float* Bs, auto&& loads, auto&& part) __attribute__((always_inline)) {
         if constexpr (!SPREAD) loads();
         __builtin_amdgcn_sched_barrier(0);
@@ -779,7 +779,10 @@ __global__ void __launch_bounds__(T::NT)
         // to 1.2 % slower); the 128 tile's stream-K kernels gain in every
         // layout (16-byte staging: 3072^3 N/N 0.432 vs 0.438 ms, 4608^3 1.383
         // vs 1.414; 4-byte: 4097 x 4099 x 4095 1.202 vs 1.234, 1.4-2.9 % on
-        // eight unaligned shapes, N/T within noise).
+        // eight unaligned shapes, N/T within noise), and so does its 4-byte
+        // data-parallel kernel (1.2-2.6 % on six unaligned shapes: 3652 x 8764
+        // x 1435 0.690 vs 0.700 ms); its 16-byte data-parallel kernel is the
+        // one the 65536 x 512 x 256 figure above is for.
         // Measured in one process each, alternating, medians of 3.
         if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
         // the next slice's first k-block (fragment set 0; the held-back MFMAs
