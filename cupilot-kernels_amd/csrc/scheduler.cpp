@@ -97,6 +97,14 @@ constexpr double kPackBytesPerNs = 5000.0;
 constexpr double kPackLaunchNs = 5000.0;
 constexpr double kPackMargin = 0.97;
 constexpr int64_t kPackMinK = 1536;
+// Against an unpacked stream-K plan on the 4-byte path the packed plan is
+// taken unless it is modelled kPackMarginSk times slower: on 40 random
+// unaligned shapes (M, N 768-9000, K 1536-10000, all four layouts) that
+// plan's modelled time ran 10-30 % below its measured time while the packed
+// plans' stayed within 3-8 %, and packing measured faster on 35 of them
+// (mean regret of the choice 2.9 %, up to 12 %, with kPackMargin; 0.05 %,
+// up to 0.9 %, with this margin).
+constexpr double kPackMarginSk = 1.25;
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
@@ -657,7 +665,9 @@ int plan_gemm(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
     // the packing pass: read both operands, write them padded, two launches
     const double moved = 4.0 * (double)(a.M + a.N) * (double)(a.K + kp);
     t1 += moved / kPackBytesPerNs + 2.0 * kPackLaunchNs;
-    if (!force_pack && !(t1 >= 0 && t1 < kPackMargin * t0)) return MI_OK;
+    const bool four_byte_sk = out.stream_k && !(choose_vec(a) == 4 && a.K % 16 == 0);
+    const double margin = four_byte_sk ? kPackMarginSk : kPackMargin;
+    if (!force_pack && !(t1 >= 0 && t1 < margin * t0)) return MI_OK;
     if (pp.workspace_bytes > SIZE_MAX - pb) return MI_OK;
     out = pp;
     out.workspace_bytes = pb + pp.workspace_bytes;
