@@ -629,6 +629,28 @@ def test_stream_k_random_shapes_both_schedules(ck, M, N, K, cfg):
     assert cost[0] <= cost[SK_RANGES]
 
 
+@pytest.mark.parametrize("M,N,K,lay", [
+    # packed against the planner's unpacked 4-byte stream-K plan, measured on
+    # MI355X (ms, unpacked / packed, each the planner's own plan of that kind)
+    (5873, 1615, 9337, "NT"),   # 1.618 / 1.441
+    (4592, 1449, 2239, "NN"),   # 0.318 / 0.288
+    (3973, 4394, 9405, "NN"),   # 2.741 / 2.564
+    (8205, 2949, 5921, "NN"),   # 2.512 / 2.320
+    (6244, 4005, 8002, "NN"),   # 3.422 / 3.137
+    (4451, 5722, 4312, "TT"),   # 1.916 / 1.752
+])
+def test_plan_packs_where_the_four_byte_stream_k_plan_measured_slower(ck, M, N, K, lay):
+    """Unaligned operands whose unpacked plan would be stream-K on the 4-byte
+    path: the packed plan is taken unless modelled 25 % slower (the model's
+    4-byte stream-K times ran 10-30 % below the measured ones)."""
+    op_a, op_b = int(lay[0] == "T"), int(lay[1] == "T")
+    rc, u = ck.abi.plan(M, N, K, op_a=op_a, op_b=op_b, workspace_bytes=1 << 40,
+                        plan_override=ck.abi.PLAN_NO_PACK)
+    assert rc == 0 and u.stream_k == 1 and not u.packed, (u.plan_id, u.stream_k)
+    rc, p = ck.abi.plan(M, N, K, op_a=op_a, op_b=op_b, workspace_bytes=1 << 40)
+    assert rc == 0 and p.packed, (p.plan_id, p.stream_k)
+
+
 def test_stream_k_applies_only_where_it_can(ck):
     # whole waves (1024 tiles of 256 on 256 CUs), a batch, a bias, operands the
     # direct kernel cannot stage, no workspace: no stream-K even when asked
