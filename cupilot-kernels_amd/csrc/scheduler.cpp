@@ -90,13 +90,14 @@ constexpr double kScalarReduceEff = 0.2811;
 // packing pass (plan_gemm): bytes per ns over what it reads and writes and
 // a fixed cost per pack launch (measured: 8205 x 5921 x 2949 in the four
 // layouts 58-87 us for 335 MB, 4095^3 63 us, 1021^3 15 us); the gain a
-// packed plan must promise, and the smallest K it is offered for (40 random
-// unaligned shapes timed packed and unpacked: below K = 1536 the model's
-// choice lost up to 9 %, from it on at most 0.6 %)
+// packed plan must promise, and the smallest K it is offered for (30 random
+// unaligned shapes with K 256-1535, M, N 768-9000, timed packed and unpacked:
+// never packing them cost 5.3 % on average, up to 29 % (1471 x 1329 x 1188);
+// the model's choice 0.6 %, up to 6.5 % (7494 x 2940 x 465))
 constexpr double kPackBytesPerNs = 5000.0;
 constexpr double kPackLaunchNs = 5000.0;
 constexpr double kPackMargin = 0.97;
-constexpr int64_t kPackMinK = 1536;
+constexpr int64_t kPackMinK = 256;
 // Against an unpacked stream-K plan on the 4-byte path the packed plan is
 // taken unless it is modelled kPackMarginSk times slower: on 40 random
 // unaligned shapes (M, N 768-9000, K 1536-10000, all four layouts) that
