@@ -651,6 +651,22 @@ def test_plan_packs_where_the_four_byte_stream_k_plan_measured_slower(ck, M, N, 
     assert rc == 0 and p.packed, (p.plan_id, p.stream_k)
 
 
+@pytest.mark.parametrize("M,N,K,lay,want", [
+    # K below 1536, measured on MI355X (ms, unpacked / packed)
+    (1471, 1329, 1188, "NN", 1),   # 0.0884 / 0.0685
+    (4245, 918, 1081, "TN", 1),    # 0.1316 / 0.1058
+    (5455, 8338, 692, "NN", 1),    # 0.6046 / 0.5641
+    (7821, 1432, 573, "TT", 0),    # 0.1164 / 0.1275
+    (1162, 7509, 420, "TT", 0),    # 0.0999 / 0.1175
+    (2309, 2706, 488, "NN", 0),    # 0.0852 / 0.0972
+])
+def test_plan_packing_choice_below_k_1536(ck, M, N, K, lay, want):
+    """From K = 256 the cost model decides whether to pack unaligned operands."""
+    rc, p = ck.abi.plan(M, N, K, op_a=int(lay[0] == "T"), op_b=int(lay[1] == "T"),
+                        workspace_bytes=1 << 40)
+    assert rc == 0 and p.packed == want, (p.plan_id, p.stream_k, p.packed)
+
+
 def test_stream_k_applies_only_where_it_can(ck):
     # whole waves (1024 tiles of 256 on 256 CUs), a batch, a bias, operands the
     # direct kernel cannot stage, no workspace: no stream-K even when asked
