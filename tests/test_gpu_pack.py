@@ -83,6 +83,9 @@ def test_packed_stream_k_on_the_256_tile(ck, orc, dev):
 @pytest.mark.parametrize("M,N,K,ops", [
     (8205, 5921, 2949, (0, 0)),   # the planner packs (PID 8-style irregular extents)
     (4095, 4095, 4095, (1, 0)),
+    (8205, 2949, 5921, (0, 0)),   # packed where the unpacked plan is 4-byte stream-K
+    (1471, 1329, 1188, (0, 0)),   # packed below K = 1536 (the k-split 64 tile on the copies)
+    (4245, 918, 1081, (1, 0)),
 ])
 def test_auto_packed_large_every_element(ck, orc, dev, M, N, K, ops):
     op_a, op_b = ops
