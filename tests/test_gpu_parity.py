@@ -89,6 +89,39 @@ def test_random_shapes_auto_plan(ck, orc, dev, M, N, K, op_a, op_b):
                  f"auto plan {p.plan_id}/{p.split_k}/{p.stream_k} {op_a}{op_b} {M}x{N}x{K}")
 
 
+def _random_unaligned_shapes(n, seed):
+    """Seeded problems with at least one extent not a multiple of 4 floats
+    (rows the 16-byte loaders cannot stage): the planner then chooses
+    between the 4-byte direct staging, the register-staged tiles, split-K
+    and packing the operands into 16-byte rows (offered from K = 256)."""
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        M, N = (int(rng.integers(200, 1400)) for _ in range(2))
+        K = int(rng.integers(256, 2000))
+        if M % 4 == 0 and N % 4 == 0 and K % 4 == 0:
+            continue
+        out.append((M, N, K, int(rng.integers(0, 2)), int(rng.integers(0, 2))))
+    return out
+
+
+@pytest.mark.parametrize("M,N,K,op_a,op_b", _random_unaligned_shapes(12, 2040))
+def test_random_unaligned_shapes_auto_plan(ck, orc, dev, M, N, K, op_a, op_b):
+    """Whatever the planner picks for unaligned operands (packed or not, any
+    tile, split-K), the result matches the oracle."""
+    rc, p = ck.abi.plan(M, N, K, op_a=op_a, op_b=op_b, workspace_bytes=1 << 40)
+    assert rc == 0
+    a_st, b_st = _host_operands(orc, M, N, K, op_a, op_b, seed=M + 2 * N + 3 * K)
+    A, B = to_dev(a_st), to_dev(b_st)
+    C = torch.full((M, N), float("nan"), device="cuda")
+    ws = workspace(ck, gemm_args(ck, A, B, C, M, N, K, op_a, op_b))
+    ck.abi.check(run_gemm(ck, gemm_args(ck, A, B, C, M, N, K, op_a, op_b, ws=ws)))
+    ref = orc.gemm(_logical(a_st, op_a), _logical(b_st, op_b))
+    assert_close(orc, to_host(C), ref, K, np.abs(a_st).max(), np.abs(b_st).max(),
+                 f"auto plan {p.plan_id}/{p.split_k}/{p.stream_k} packed={p.packed} "
+                 f"{op_a}{op_b} {M}x{N}x{K}")
+
+
 @pytest.mark.parametrize("op_a,op_b", LAYOUTS)
 @pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5, 6, 7])
 @pytest.mark.parametrize("M,N,K", [(512, 512, 512), (300, 200, 100), (64, 640, 37), (700, 520, 31),
