@@ -6,7 +6,11 @@
     python bench.py --mode gemm:MxNxK[:TN|NT|TT][@BITS][,...] [--override BITS]
     python bench.py --mode torch:MxNxK[:TN|NT|TT][,...]     (torch-ROCm's own GEMM, for profiling)
                                                     dense products through the C ABI, with a
-                                                    plan override (stream-K / tile / split)
+                                                    plan override (stream-K / tile / split);
+                                                    --mode runs keep exactly --warmup calls
+                                                    per entry: with few (5), the first entry
+                                                    after a change of shape measured up to
+                                                    ~2 % slow, so compare plans with >= 30
     python bench.py --summarize DIR [DIR ...] [--calib DIR]  rocprofv3 CSV output -> text summary
 
 One step = the BASELINE configs[1] workload: an fp32 8192^3 GEMM in each of the
