@@ -89,6 +89,61 @@ def test_random_shapes_auto_plan(ck, orc, dev, M, N, K, op_a, op_b):
                  f"auto plan {p.plan_id}/{p.split_k}/{p.stream_k} {op_a}{op_b} {M}x{N}x{K}")
 
 
+_SWEEP_OVERRIDES = [0, 0, 0x40, 0x80, 0x12, 0x19, 0x13, 0x2, 0x3, 0x9, 0xb, 0xa, 0x1, 0x22, 0x29,
+                    0x203, 0x402]
+
+
+def _sweep_cases(n, seed):
+    """Seeded problems over the ABI's combinations: aligned or not, every
+    layout, padded leading dimensions, batches, the row bias (N/N), and
+    forced plans (tiles, split-K, stream-K, packing on or off; a plan the
+    problem cannot take is ignored by the planner)."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        align = rng.random() < 0.5
+        ext = lambda lo, hi: max(1, (int(rng.integers(lo, hi)) // 4) * 4 if align else int(rng.integers(lo, hi)))
+        M, N, K = ext(1, 700), ext(1, 700), ext(1, 1500)
+        op_a, op_b = int(rng.integers(0, 2)), int(rng.integers(0, 2))
+        batch = int(rng.choice([1, 1, 2, 3]))
+        pad = int(rng.choice([0, 0, 3, 4]))
+        bias = bool(op_a == 0 and op_b == 0 and rng.random() < 0.3)
+        ov = int(rng.choice(_SWEEP_OVERRIDES))
+        out.append((M, N, K, op_a, op_b, batch, pad, bias, ov))
+    return out
+
+
+@pytest.mark.parametrize("M,N,K,op_a,op_b,batch,pad,bias,ov", _sweep_cases(40, 2041))
+def test_random_abi_combinations(ck, orc, dev, M, N, K, op_a, op_b, batch, pad, bias, ov):
+    lda, ldb, ldc = (M if op_a else K) + pad, (K if op_b else N) + pad, N + pad
+    a_st = orc.uniform((batch,) + ((K, M) if op_a else (M, K)), 191)
+    b_st = orc.uniform((batch,) + ((N, K) if op_b else (K, N)), 192)
+    bi = orc.uniform((M,), 193)
+    a_pad = np.zeros((batch, a_st.shape[1], lda), np.float32)
+    a_pad[:, :, :a_st.shape[2]] = a_st
+    b_pad = np.zeros((batch, b_st.shape[1], ldb), np.float32)
+    b_pad[:, :, :b_st.shape[2]] = b_st
+    A, B, Bi = to_dev(a_pad), to_dev(b_pad), to_dev(bi)
+    C = torch.full((batch, M, ldc), float("nan"), device="cuda")
+    args = gemm_args(ck, A, B, C, M, N, K, op_a, op_b, batch=batch, lda=lda, ldb=ldb, ldc=ldc,
+                     sa=a_pad[0].size, sb=b_pad[0].size, sc=M * ldc, override=ov)
+    if bias:
+        args.bias_m = Bi.data_ptr()
+    ws = workspace(ck, args)
+    args = gemm_args(ck, A, B, C, M, N, K, op_a, op_b, batch=batch, lda=lda, ldb=ldb, ldc=ldc,
+                     sa=a_pad[0].size, sb=b_pad[0].size, sc=M * ldc, override=ov, ws=ws)
+    if bias:
+        args.bias_m = Bi.data_ptr()
+    ck.abi.check(run_gemm(ck, args))
+    la = np.swapaxes(a_st, 1, 2) if op_a else a_st
+    lb = np.swapaxes(b_st, 1, 2) if op_b else b_st
+    ref = orc.gemm(la, lb) + (bi.astype(np.float64)[None, :, None] if bias else 0.0)
+    got = to_host(C)
+    assert_close(orc, got[:, :, :N], ref, K,
+                 what=f"{M}x{N}x{K}x{batch} {op_a}{op_b} pad={pad} bias={bias} override={ov:#x}")
+    if pad:
+        assert np.isnan(got[:, :, N:]).all(), "a store landed in the ldc padding"
+
 def _random_unaligned_shapes(n, seed):
     """Seeded problems with at least one extent not a multiple of 4 floats
     (rows the 16-byte loaders cannot stage): the planner then chooses
