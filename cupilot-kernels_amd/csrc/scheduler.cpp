@@ -443,8 +443,16 @@ int plan_core(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
             // Below K = 1024 stream-K measured slower than the data-parallel
             // plan on all 25 shapes of the timing table; the 8-wave tile is
             // offered data-parallel only.
+            // The k-split tile below one wave of tiles with K <= 2048 (at most
+            // 32 slices per tile, about two segments each) measured faster
+            // data-parallel or split in two on all 18 such shapes tried
+            // (768^2 x 2048 36.7 vs 40.4 us, 1408 x 256 x 2048 24.9 vs 33.1,
+            // 256 x 1280 x 1024 17.0 vs 18.8); with deeper K its stream-K
+            // stayed ahead of the split-K plans (2688 x 256 x 4096 53.6 vs
+            // 61.4 us, 1152 x 256 x 8192 51.5 vs 57.4).
             const bool sk_offered =
                 a.K >= 1024 && m.id != kCfg128W8 &&
+                !(m.id == kCfg64W && a.K <= 2048 && sk.dp == 0) &&
                 (!four_byte || (a.K >= 1536 && 6 * tiles >= (int64_t)sk.grid &&
                                 (double)cdiv(tiles, num_cus) * num_cus >= 1.12 * (double)tiles));
             if (sk.tiles > 0 && sk_offered) {

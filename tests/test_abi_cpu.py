@@ -752,6 +752,27 @@ def test_plan_takes_stream_k_where_it_measured_faster(ck, M, N, K, sk):
     assert rc == 0 and p.stream_k == sk, (M, N, K, p.plan_id, p.split_k, p.stream_k)
 
 
+@pytest.mark.parametrize("M,N,K,sk", [
+    # the k-split 64 tile with fewer tiles than workgroups (MI355X, us, the
+    # planner's previous stream-K plan / the plan it takes now): K <= 2048
+    # runs data-parallel or split in two ...
+    (768, 768, 2048, 0),      # 40.4 / 36.7
+    (1408, 256, 2048, 0),     # 33.1 / 24.9
+    (256, 1280, 1024, 0),     # 18.8 / 17.0
+    (1152, 256, 1024, 0),     # 20.6 / 16.5
+    # ... deeper K keeps stream-K, which the split-K plans did not beat
+    (2688, 256, 4096, 1),     # 53.6 / 61.4 split 16
+    (1152, 256, 8192, 1),     # 51.5 / 57.4 split 16
+    (384, 1792, 4096, 1),     # 53.5 / 61.2 split 16
+])
+def test_plan_k_split_tile_stream_k_below_one_wave(ck, M, N, K, sk):
+    rc, p = ck.abi.plan(M, N, K, workspace_bytes=1 << 40)
+    assert rc == 0 and p.plan_id == 10 and p.stream_k == sk, (p.plan_id, p.split_k, p.stream_k)
+    # an override still forces that tile's stream-K schedule
+    rc, p = ck.abi.plan(M, N, K, workspace_bytes=1 << 40, plan_override=10 | SK_FORCE)
+    assert rc == 0 and p.plan_id == 10 and p.stream_k == 1
+
+
 def _plan_timings():
     import csv
     from collections import defaultdict
