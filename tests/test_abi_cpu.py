@@ -773,6 +773,24 @@ def test_plan_k_split_tile_stream_k_below_one_wave(ck, M, N, K, sk):
     assert rc == 0 and p.plan_id == 10 and p.stream_k == 1
 
 
+@pytest.mark.parametrize("M,N,K,want", [
+    # one round of at most one 128 x 128 tile per CU (MI355X, us, the 8-wave
+    # tile data-parallel / the 32-deep 128 tile's stream-K): well below 256
+    # tiles and K >= 2048, stream-K ...
+    (1792, 1792, 2048, (9, 1)),   # 123.2 / 115.5
+    (1152, 2816, 2048, (9, 1)),   # 123.1 / 115.2
+    (1536, 2304, 4096, (9, 1)),   # 240.7 / 225.7
+    (1792, 2048, 6144, (9, 1)),   # 356.3 / 336.3
+    # ... near 256 tiles or with short K, the 8-wave tile
+    (1280, 3072, 2048, (11, 0)),  # 123.8 / 135.7
+    (1792, 2304, 2048, (11, 0)),  # 123.8 / 136.0
+    (1792, 1792, 1024, (11, 0)),  # 65.0 / 70.0
+])
+def test_plan_one_round_of_128_tiles(ck, M, N, K, want):
+    rc, p = ck.abi.plan(M, N, K, workspace_bytes=1 << 40)
+    assert rc == 0 and (p.plan_id, p.stream_k) == want, (p.plan_id, p.split_k, p.stream_k)
+
+
 def _plan_timings():
     import csv
     from collections import defaultdict
