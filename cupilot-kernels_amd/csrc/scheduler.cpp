@@ -64,6 +64,7 @@ constexpr CfgModel kModels[] = {
 
 constexpr double kPeakFlopsPerCuNs = 256.0 * 2.4;  // fp32 MFMA flop per ns per CU
 constexpr double kW8OneRoundEff = 0.95;              // config 11, one round of <= 1 tile per CU
+constexpr double kB32OneRoundEff = 0.90;             // config 9, likewise
 constexpr double kWriteBytesPerNs = 5500.0;        // sustained write-only bandwidth (measured)
 // split-K reduction and stream-K fixup passes: bytes per ns over what they
 // read and write, plus a fixed cost per reduction pass
@@ -418,12 +419,19 @@ int plan_core(const mi_gemm_args& a, int num_cus, mi_plan& out, GemmLaunch* laun
                 // full rounds of occ resident items at that occupancy, then the
                 // last round's leftover items at their own, lower occupancy
                 const int64_t rounds = per_cu / occ, rem = per_cu % occ;
-                // the 8-wave tile with at most one tile per CU (the whole
-                // problem in one round) measured ~5 % below the efficiency its
-                // fit gives full rounds: 1792^2 x 2048 123.2 us, 1536 x 2304 x
-                // 4096 240.7 us, against 115.5 / 225.7 us for the 32-deep 128
-                // tile's stream-K, which the model had priced higher
-                const double e_one = (m.id == kCfg128W8 && per_cu == 1) ? kW8OneRoundEff : m.eff[0];
+                // With at most one tile per CU (the whole problem in one
+                // round) two tiles run at efficiencies of their own: the
+                // 8-wave tile ~5 % below what its fit gives full rounds
+                // (1792^2 x 2048 123.2 us, 1536 x 2304 x 4096 240.7 us, against
+                // 115.5 / 225.7 us for the 32-deep 128 tile's stream-K, which
+                // the model had priced higher), and the 32-deep 128 tile
+                // above it, ~2.5 % faster than the 16-deep 128 tile in every
+                // one-round case of the timing table, all layouts (2048^2 x
+                // 4096 T/N 250.4 vs 267.6 us, T/T 252.0 vs 264.5)
+                const double e_one = per_cu != 1              ? m.eff[0]
+                                     : m.id == kCfg128W8   ? kW8OneRoundEff
+                                     : m.id == kCfg128B32  ? kB32OneRoundEff
+                                                           : m.eff[0];
                 const double slots = (double)(rounds * occ) / (occ == 1 ? e_one : m.eff[std::min(occ, 3) - 1]) +
                                      (rem ? (double)rem / m.eff[std::min<int64_t>(rem, 3) - 1] : 0.0);
                 double t = slots * 2.0 * ci.bm * ci.bn * (double)kc / (scale * kPeakFlopsPerCuNs);
